@@ -1,0 +1,198 @@
+/*
+ * trainscale_amd.h — C ABI of the MI355X (gfx950) fused kernel layer.
+ *
+ * Every entry point takes caller-owned device buffers as plain pointers, sizes
+ * and strides counted in ELEMENTS, and the HIP stream to launch on. Nothing here
+ * allocates device memory; scratch space is passed in as a workspace buffer whose
+ * size the matching *_workspace_size() function reports. Launches are
+ * asynchronous on `stream` and never synchronise. Every function returns a
+ * ts_status; on failure ts_last_error() describes the problem (thread-local).
+ *
+ * Arguments are validated on the host before anything touches the GPU, so a bad
+ * call returns an error code instead of launching.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (paths relative to generalaimodels/TrainScale, data_pipeline/trainer/).
+ */
+#ifndef TRAINSCALE_AMD_H
+#define TRAINSCALE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ts_stream_t; /* a hipStream_t; NULL is the legacy default stream */
+
+typedef int32_t ts_status;
+enum {
+  TS_OK = 0,
+  TS_ERR_INVALID_ARGUMENT = -1, /* NULL pointer, negative size, bad flag */
+  TS_ERR_UNSUPPORTED_DTYPE = -2,
+  TS_ERR_SHAPE = -3,            /* inconsistent sizes / strides */
+  TS_ERR_WORKSPACE = -4,        /* workspace missing or too small */
+  TS_ERR_LAUNCH = -5,           /* the HIP runtime rejected a launch */
+  TS_ERR_DEVICE = -6            /* device query failed */
+};
+
+typedef enum {
+  TS_F32 = 0,
+  TS_BF16 = 1,
+  TS_F16 = 2
+} ts_dtype;
+
+/* Human-readable description of the last error raised on this thread. */
+const char* ts_last_error(void);
+/* Library version string, e.g. "trainscale_amd 0.1.0 gfx950". */
+const char* ts_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* round_mode for ts_rmsnorm_fwd */
+enum {
+  /* y = round(x * rstd * w) in fp32, rounded once.
+   * Replaces _rms_layernorm_forward_kernel, kernels/triton_kernels.py:477-514,
+   * launched by Fast_RMS_LayerNorm.forward, triton_kernels.py:605-643. */
+  TS_RMS_ROUND_ONCE = 0,
+  /* y = round(round(x * rstd) * w) when w has the data dtype (bf16/fp16),
+   * otherwise identical to ROUND_ONCE.
+   * Replaces _rms_layernorm_forward_kernel, kernels/layernorm_kernels.py:143-199
+   * (y = x_norm.to(w.dtype) * w), launched by RMSLayerNormFunction.forward,
+   * layernorm_kernels.py:686-750. */
+  TS_RMS_ROUND_TWICE = 1
+};
+
+/*
+ * y[r, :] = x[r, :] * rstd[r] * w,   rstd[r] = 1 / sqrt(mean(x[r, :]^2) + eps)
+ * x, y: [rows, cols] of x_dtype with row strides ldx, ldy (elements).
+ * w: [cols] of w_dtype, or NULL for no weight (elementwise_affine=False).
+ * rstd: [rows] fp32, written (saved for the backward pass).
+ */
+ts_status ts_rmsnorm_fwd(const void* x, int64_t ldx, ts_dtype x_dtype,
+                         const void* w, ts_dtype w_dtype,
+                         void* y, int64_t ldy,
+                         float* rstd,
+                         int64_t rows, int64_t cols, float eps,
+                         int32_t round_mode, ts_stream_t stream);
+
+/* Bytes of workspace ts_rmsnorm_bwd needs for these sizes (dW partial sums). */
+size_t ts_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols);
+
+/*
+ * dx = rstd * (dy*w - xhat * mean(dy*w*xhat)),  xhat = x * rstd
+ * dw = sum_rows(dy * xhat), accumulated in fp32 in a fixed order
+ *      (deterministic: per-workgroup partials, then an ordered column sum).
+ * dy, x, dx: [rows, cols] of x_dtype, row strides lddy, ldx, lddx.
+ * w: [cols] of w_dtype or NULL. dw: [cols] of w_dtype, or NULL to skip dW.
+ * Replaces _rms_layernorm_backward_kernel + _rms_layernorm_backward_dw_kernel,
+ * kernels/triton_kernels.py:517-599 (Fast_RMS_LayerNorm.backward :646-684) and
+ * _rms_layernorm_backward_dx_kernel + _rms_layernorm_backward_dw_kernel,
+ * kernels/layernorm_kernels.py:203-308 (RMSLayerNormFunction.backward :752-807).
+ */
+ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy,
+                         const void* x, int64_t ldx, ts_dtype x_dtype,
+                         const void* w, ts_dtype w_dtype,
+                         const float* rstd,
+                         void* dx, int64_t lddx,
+                         void* dw,
+                         void* workspace, size_t workspace_bytes,
+                         int64_t rows, int64_t cols, ts_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Rotary position embedding                                                 */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Rotates the head_dim pairs of up to two [B, S, H, D] tensors ("q" and "k") at
+ * positions pos(b, s). The last dimension must be contiguous; other strides are
+ * free. in == out rotates in place.
+ *
+ *   NeoX layout (interleaved=0): pairs (i, i + D/2);  interleaved=1: (2i, 2i+1)
+ *   forward:  o1 = x1*cos - x2*sin,  o2 = x2*cos + x1*sin
+ *   backward: the same with sin negated (the transpose rotation)
+ *
+ * pos(b, s) = position_ids[b*pos_sb + s*pos_ss] when position_ids != NULL
+ *             (int64, device), else s + position_offset.
+ *
+ * Angle source, exactly one of:
+ *   - tables: cos_tab/sin_tab != NULL, [table_rows, D/2] of tab_dtype with row
+ *     stride tab_ld; cos/sin are read at row pos. Positions outside
+ *     [0, table_rows) produce NaN outputs for that token instead of a fault.
+ *   - in-register: cos_tab == sin_tab == NULL, inv_freq = HOST array of D/2
+ *     fp32 values; angle_i = fp32(pos / pos_div) * inv_freq[i] (the fp32
+ *     product torch.outer forms), then sin/cos are evaluated on the GPU.
+ *
+ * Replaces _rope_forward_kernel/_rope_backward_kernel (kernels/triton_kernels.py
+ * :713-890, Fast_RoPE :893-981), _rope_fwd_kernel/_rope_bwd_kernel,
+ * _rope_single_tensor_kernel and _rope_with_position_ids_kernel
+ * (kernels/rope_kernels.py:385-804, launched by :837-951).
+ * k may be NULL (Hk = 0) for the single-tensor forms.
+ */
+ts_status ts_rope_apply(const void* q_in, void* q_out,
+                        int64_t q_in_sb, int64_t q_in_ss, int64_t q_in_sh,
+                        int64_t q_out_sb, int64_t q_out_ss, int64_t q_out_sh,
+                        int64_t Hq,
+                        const void* k_in, void* k_out,
+                        int64_t k_in_sb, int64_t k_in_ss, int64_t k_in_sh,
+                        int64_t k_out_sb, int64_t k_out_ss, int64_t k_out_sh,
+                        int64_t Hk,
+                        ts_dtype dtype, int64_t B, int64_t S, int64_t D,
+                        const void* cos_tab, const void* sin_tab,
+                        ts_dtype tab_dtype, int64_t tab_ld, int64_t table_rows,
+                        const float* inv_freq, float pos_div,
+                        const int64_t* position_ids, int64_t pos_sb, int64_t pos_ss,
+                        int64_t position_offset,
+                        int32_t interleaved, int32_t backward,
+                        ts_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Cross-entropy over the vocabulary                                         */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Per row r of logits [N, V] (row stride ld, dtype any of f32/bf16/f16):
+ *   z = logit_scale != 0 ? logit_scale * x : x
+ *   z = softcap != 0 ? softcap * tanh(z / softcap) : z
+ *   lse[r] = log(sum_j exp(z_j))                      (fp32, online max)
+ *   loss[r] = (1-a)*(lse - z[label]) + a*(lse - mean_j z_j), a = label_smoothing
+ *   loss[r] = 0 (and lse still written) when labels[r] == ignore_index.
+ * labels: int64 [N], device. Labels outside [0, V) other than ignore_index
+ * give loss NaN for that row.
+ * Replaces _cross_entropy_forward_kernel/_chunked_cross_entropy_forward_kernel
+ * (kernels/triton_kernels.py:122-235, Fast_CrossEntropyLoss.forward :320-397),
+ * _fused_cross_entropy_fwd_kernel (loss/sota_losses.py:135-228) and
+ * cross_entropy_fwd_kernel (loss/__init__.py:41-123).
+ */
+ts_status ts_ce_fwd(const void* logits, int64_t ld, ts_dtype dtype,
+                    const int64_t* labels, int64_t N, int64_t V,
+                    int64_t ignore_index, float logit_scale, float softcap,
+                    float label_smoothing,
+                    float* loss, float* lse, ts_stream_t stream);
+
+/*
+ * grad[r, j] = dloss[r] * dz/dx * (softmax(z)_j - (1-a)*[j == label] - a/V)
+ * with dloss[r] = dloss_ptr[r * dloss_stride] * dloss_scale (stride 0
+ * broadcasts one value) and grad = 0 on rows whose label is ignore_index.
+ * grad may alias logits (in place, as the reference writes the gradient into
+ * the saved logits buffer); grad has its own row stride ld_grad and dtype.
+ * Replaces _cross_entropy_backward_kernel (kernels/triton_kernels.py:238-306,
+ * Fast_CrossEntropyLoss.backward :400-424) and _fused_cross_entropy_bwd_kernel
+ * (loss/sota_losses.py:230-289).
+ */
+ts_status ts_ce_bwd(const void* logits, int64_t ld, ts_dtype dtype,
+                    const int64_t* labels, const float* lse,
+                    const float* dloss, int64_t dloss_stride, float dloss_scale,
+                    void* grad, int64_t ld_grad, ts_dtype grad_dtype,
+                    int64_t N, int64_t V, int64_t ignore_index,
+                    float logit_scale, float softcap, float label_smoothing,
+                    ts_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRAINSCALE_AMD_H */

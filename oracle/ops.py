@@ -1,0 +1,233 @@
+"""Oracle restatements (torch CPU, fp32 arithmetic). TEST INFRASTRUCTURE ONLY.
+
+Each function cites the reference lines it restates (paths relative to
+data_pipeline/trainer/ of generalaimodels/TrainScale). Inputs may be bf16/fp16
+CPU tensors; arithmetic is fp32 and the result is rounded once to the output
+dtype, as the reference's GPU kernels do (they upcast every load to fp32).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+__all__ = [
+    "rms_norm_fwd",
+    "rms_norm_bwd",
+    "rope_inv_freq",
+    "rope_tables",
+    "rope_apply",
+    "rope_positions",
+    "ce_fwd",
+    "ce_bwd",
+    "linear_ce",
+]
+
+
+def _cpu(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.detach().cpu()
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+
+def rms_norm_fwd(x: Tensor, w: Optional[Tensor], eps: float = 1e-6,
+                 round_twice: bool = False) -> Tuple[Tensor, Tensor]:
+    """y = x * rstd * w, rstd = rsqrt(mean(x^2) + eps), fp32, rounded once to x.dtype.
+
+    Restates _rms_layernorm_forward_kernel (kernels/triton_kernels.py:501-514;
+    eager form :612-616). With round_twice and a weight of x's 16-bit dtype it
+    restates layernorm_kernels.py:189-194 instead: y = round(round(x*rstd) * w).
+    Returns (y [..., C] in x.dtype, rstd fp32 [rows]).
+    """
+    x = _cpu(x)
+    w = _cpu(w)
+    c = x.shape[-1]
+    x32 = x.reshape(-1, c).float()
+    mean_sq = (x32 * x32).sum(-1) / c
+    rstd = 1.0 / torch.sqrt(mean_sq + eps)
+    xn = x32 * rstd[:, None]
+    if w is not None:
+        if round_twice and w.dtype == x.dtype and x.dtype != torch.float32:
+            y = xn.to(x.dtype).float() * w.float()
+        else:
+            y = xn * w.float()
+    else:
+        y = xn
+    return y.to(x.dtype).reshape(x.shape), rstd
+
+
+def rms_norm_bwd(dy: Tensor, x: Tensor, w: Optional[Tensor],
+                 rstd: Tensor) -> Tuple[Tensor, Optional[Tensor]]:
+    """dx = rstd*(dy*w - xhat*mean(dy*w*xhat)), dw = sum_rows(dy*xhat), fp32.
+
+    Restates _rms_layernorm_backward_kernel and _rms_layernorm_backward_dw_kernel
+    (kernels/triton_kernels.py:557-562, :596-597; eager form
+    kernels/layernorm_kernels.py:777-781, :804-805). dx in x.dtype, dw in w.dtype.
+    """
+    dy, x, w, rstd = _cpu(dy), _cpu(x), _cpu(w), _cpu(rstd)
+    c = x.shape[-1]
+    x32 = x.reshape(-1, c).float()
+    dy32 = dy.reshape(-1, c).float()
+    r = rstd.float()[:, None]
+    xhat = x32 * r
+    dyw = dy32 * (w.float() if w is not None else 1.0)
+    c1 = (dyw * xhat).sum(-1, keepdim=True) / c
+    dx = r * (dyw - xhat * c1)
+    dw = None
+    if w is not None:
+        dw = (dy32 * xhat).sum(0).to(w.dtype)
+    return dx.to(x.dtype).reshape(x.shape), dw
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+
+def rope_inv_freq(dim: int, theta: float) -> Tensor:
+    """inv_freq_i = 1/theta**(2i/dim) in fp32 (kernels/rope_kernels.py:203-207)."""
+    return 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+
+
+def rope_tables(dim: int, n_pos: int, theta: float, pos_div: float = 1.0,
+                dtype: torch.dtype = torch.float32) -> Tuple[Tensor, Tensor]:
+    """cos/sin [n_pos, dim/2]: fp32 angle outer(arange/pos_div, inv_freq).
+
+    Restates compute_rope_frequencies / precompute_freqs_cis
+    (kernels/rope_kernels.py:172-195; kernels/triton_kernels.py:1029-1032).
+    """
+    t = torch.arange(n_pos, dtype=torch.float32) / pos_div
+    ang = torch.outer(t, rope_inv_freq(dim, theta))
+    return torch.cos(ang).to(dtype), torch.sin(ang).to(dtype)
+
+
+def rope_positions(B: int, S: int, position_ids: Optional[Tensor] = None,
+                   position_offset: int = 0) -> Tensor:
+    """int64 [B, S] positions: position_ids broadcast over the batch, else s + offset."""
+    if position_ids is None:
+        return (torch.arange(S, dtype=torch.int64) + position_offset).expand(B, S)
+    p = _cpu(position_ids).to(torch.int64)
+    if p.dim() == 1:
+        p = p[None, :]
+    return p.expand(B, S)
+
+
+def rope_apply(x: Tensor, cos: Tensor, sin: Tensor, positions: Tensor,
+               interleaved: bool = False, backward: bool = False) -> Tensor:
+    """Rotation of x [B,S,H,D] by the table rows at positions [B,S], fp32, rounded once.
+
+    NeoX: o1 = x1*c - x2*s, o2 = x2*c + x1*s on halves [0, D/2) / [D/2, D);
+    interleaved: the same on (x[2i], x[2i+1]). Backward negates sin.
+    Restates _rope_forward_kernel / _rope_backward_kernel
+    (kernels/triton_kernels.py:764-806, :848-890) and the eager form with the
+    BSHD broadcast of triton_kernels.py:908-925 and the position_ids gather of
+    kernels/rope_kernels.py:965-993 (cos[position_ids] -> [B, S, 1, D/2]).
+    """
+    x, cos, sin, positions = _cpu(x), _cpu(cos), _cpu(sin), _cpu(positions)
+    D = x.shape[-1]
+    h = D // 2
+    c = cos.float()[positions][:, :, None, :h]
+    s = sin.float()[positions][:, :, None, :h]
+    if backward:
+        s = -s
+    x32 = x.float()
+    if interleaved:
+        x1, x2 = x32[..., 0::2], x32[..., 1::2]
+    else:
+        x1, x2 = x32[..., :h], x32[..., h:]
+    o1 = x1 * c - x2 * s
+    o2 = x2 * c + x1 * s
+    if interleaved:
+        out = torch.stack([o1, o2], dim=-1).flatten(-2)
+    else:
+        out = torch.cat([o1, o2], dim=-1)
+    return out.to(x.dtype)
+
+
+# ---------------------------------------------------------------------------
+# Cross-entropy
+# ---------------------------------------------------------------------------
+
+def _xform(x32: Tensor, logit_scale: float, softcap: float) -> Tensor:
+    # scale then softcap, kernels/triton_kernels.py:331-334
+    if logit_scale != 0.0:
+        x32 = logit_scale * x32
+    if softcap != 0.0:
+        x32 = softcap * torch.tanh(x32 / softcap)
+    return x32
+
+
+def ce_fwd(logits: Tensor, labels: Tensor, ignore_index: int = -100,
+           logit_scale: float = 0.0, softcap: float = 0.0,
+           label_smoothing: float = 0.0) -> Tuple[Tensor, Tensor]:
+    """Per-row (loss, lse) in fp32; loss 0 on ignore_index rows.
+
+    loss = (1-a)*(lse - z[label]) + a*(lse - mean(z)), z the transformed logits.
+    Restates Fast_CrossEntropyLoss's eager path (kernels/triton_kernels.py:
+    328-337: F.cross_entropy(logits.float(), reduction='none') after scaling and
+    softcapping) and ChunkedCrossEntropyLoss's training path
+    (loss/sota_losses.py:695-744, incl. label smoothing :726-731).
+    """
+    logits, labels = _cpu(logits), _cpu(labels).reshape(-1).to(torch.int64)
+    z = _xform(logits.reshape(-1, logits.shape[-1]).float(), logit_scale, softcap)
+    lse = torch.logsumexp(z, dim=-1)
+    valid = labels != ignore_index
+    tgt = torch.gather(z, 1, labels.clamp(min=0)[:, None]).squeeze(1)
+    loss = lse - tgt
+    if label_smoothing > 0:
+        loss = (1 - label_smoothing) * loss + label_smoothing * (lse - z.mean(dim=-1))
+    loss = torch.where(valid, loss, torch.zeros_like(loss))
+    return loss, lse
+
+
+def ce_bwd(logits: Tensor, labels: Tensor, dloss: Tensor, ignore_index: int = -100,
+           logit_scale: float = 0.0, softcap: float = 0.0, label_smoothing: float = 0.0,
+           out_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """dL/dlogits = dloss * dz/dx * (softmax(z) - (1-a)*onehot - a/V), 0 on ignored rows.
+
+    Restates _cross_entropy_backward_kernel (kernels/triton_kernels.py:271-306)
+    and _fused_cross_entropy_bwd_kernel (loss/sota_losses.py:262-289).
+    dloss: fp32 [N] or a scalar. Returns the gradient in out_dtype (default logits.dtype).
+    """
+    logits, labels, dloss = _cpu(logits), _cpu(labels).reshape(-1).to(torch.int64), _cpu(dloss)
+    n, v = logits.shape[0], logits.shape[-1]
+    x32 = logits.reshape(n, v).float()
+    z = _xform(x32, logit_scale, softcap)
+    p = torch.softmax(z, dim=-1)
+    onehot = torch.zeros_like(p)
+    valid = labels != ignore_index
+    onehot[torch.arange(n)[valid], labels[valid]] = 1.0
+    g = (1 - label_smoothing) * (p - onehot) + label_smoothing * (p - 1.0 / v)
+    if softcap != 0.0:
+        t = torch.tanh((logit_scale * x32 if logit_scale != 0.0 else x32) / softcap)
+        g = g * (1 - t * t)
+    if logit_scale != 0.0:
+        g = g * logit_scale
+    d = dloss.float().reshape(-1)
+    d = d.expand(n) if d.numel() == 1 else d
+    g = g * torch.where(valid, d, torch.zeros_like(d))[:, None]
+    return g.to(out_dtype or logits.dtype).reshape(logits.shape)
+
+
+def linear_ce(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
+              reduction: str = "mean") -> Tuple[Tensor, Tensor, Tensor]:
+    """Fused linear cross-entropy as its composition: logits = hidden @ weight.T -> CE.
+
+    hidden [N, H], weight [V, H] (the lm_head layout of rl_training.py:156-177),
+    fp32 products. Returns (loss fp32 scalar, grad_hidden, grad_weight) in the
+    input dtypes, for mean (over non-ignored rows) or sum reduction.
+    """
+    hidden, weight, labels = _cpu(hidden), _cpu(weight), _cpu(labels).reshape(-1)
+    h32, w32 = hidden.float(), weight.float()
+    logits = h32 @ w32.t()
+    loss_rows, _ = ce_fwd(logits, labels, ignore_index)
+    n_valid = max(int((labels != ignore_index).sum()), 1)
+    scale = 1.0 / n_valid if reduction == "mean" else 1.0
+    loss = loss_rows.sum() * scale
+    g = ce_bwd(logits, labels, torch.tensor(scale), ignore_index, out_dtype=torch.float32)
+    grad_h = (g @ w32).to(hidden.dtype)
+    grad_w = (g.t() @ h32).to(weight.dtype)
+    return loss, grad_h, grad_w

@@ -1,0 +1,111 @@
+"""The C-ABI library loads, exports every declared symbol, and rejects bad calls
+on the host before anything reaches a GPU (no compute calls here)."""
+import ctypes
+
+import pytest
+
+from trainscale_amd import _lib
+
+TS_OK, INVALID, DTYPE, SHAPE, WORKSPACE = 0, -1, -2, -3, -4
+NULL = None
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_every_header_symbol_is_exported(lib):
+    names = _lib.header_symbols()
+    assert set(names) == set(_lib.SIGNATURES), (names, sorted(_lib.SIGNATURES))
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_error_string(lib):
+    assert lib.ts_version().decode().startswith("trainscale_amd")
+    assert isinstance(lib.ts_last_error(), bytes)
+
+
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: every call below fails validation
+
+
+def test_rmsnorm_fwd_validation(lib):
+    st = NULL
+    assert lib.ts_rmsnorm_fwd(FAKE, 64, 1, FAKE, 1, FAKE, 64, FAKE, -1, 64, 1e-6, 0, st) == SHAPE
+    assert lib.ts_rmsnorm_fwd(FAKE, 64, 7, FAKE, 1, FAKE, 64, FAKE, 4, 64, 1e-6, 0, st) == DTYPE
+    assert lib.ts_rmsnorm_fwd(FAKE, 64, 1, FAKE, 2, FAKE, 64, FAKE, 4, 64, 1e-6, 0, st) == DTYPE
+    assert lib.ts_rmsnorm_fwd(NULL, 64, 1, FAKE, 1, FAKE, 64, FAKE, 4, 64, 1e-6, 0, st) == INVALID
+    assert lib.ts_rmsnorm_fwd(FAKE, 32, 1, FAKE, 1, FAKE, 64, FAKE, 4, 64, 1e-6, 0, st) == SHAPE
+    assert lib.ts_rmsnorm_fwd(FAKE, 64, 1, FAKE, 1, FAKE, 64, FAKE, 4, 64, -1.0, 0, st) == INVALID
+    assert lib.ts_rmsnorm_fwd(FAKE, 64, 1, FAKE, 1, FAKE, 64, FAKE, 4, 64, 1e-6, 5, st) == INVALID
+    assert b"round_mode" in lib.ts_last_error()
+    # an empty batch is a no-op
+    assert lib.ts_rmsnorm_fwd(NULL, 64, 1, NULL, 1, NULL, 64, NULL, 0, 64, 1e-6, 0, st) == TS_OK
+
+
+def test_rmsnorm_bwd_validation(lib):
+    st = NULL
+    need = lib.ts_rmsnorm_bwd_workspace_size(16384, 4096)
+    assert need > 0 and need % 4 == 0
+    assert lib.ts_rmsnorm_bwd_workspace_size(0, 4096) == 0
+    # dW requested with a too-small workspace
+    rc = lib.ts_rmsnorm_bwd(FAKE, 4096, FAKE, 4096, 1, FAKE, 1, FAKE, FAKE, 4096, FAKE,
+                            FAKE, need - 16, 16384, 4096, st)
+    assert rc == WORKSPACE, _lib.last_error()
+    # dW without a weight
+    rc = lib.ts_rmsnorm_bwd(FAKE, 4096, FAKE, 4096, 1, NULL, 1, FAKE, FAKE, 4096, FAKE,
+                            FAKE, need, 16384, 4096, st)
+    assert rc == INVALID
+    rc = lib.ts_rmsnorm_bwd(NULL, 4096, FAKE, 4096, 1, FAKE, 1, FAKE, FAKE, 4096, NULL,
+                            NULL, 0, 16, 4096, st)
+    assert rc == INVALID
+
+
+def _rope(lib, **kw):
+    a = dict(q_in=FAKE, q_out=FAKE, qs=(4096, 512, 128), qos=(4096, 512, 128), Hq=4,
+             k_in=NULL, k_out=NULL, ks=(0, 0, 0), kos=(0, 0, 0), Hk=0, dtype=1, B=2, S=8, D=128,
+             cos=FAKE, sin=FAKE, tab_dtype=0, tab_ld=64, rows=8, inv=NULL, pos_div=1.0,
+             pos=NULL, psb=0, pss=0, off=0, il=0, bwd=0)
+    a.update(kw)
+    return lib.ts_rope_apply(a["q_in"], a["q_out"], *a["qs"], *a["qos"], a["Hq"], a["k_in"],
+                             a["k_out"], *a["ks"], *a["kos"], a["Hk"], a["dtype"], a["B"], a["S"],
+                             a["D"], a["cos"], a["sin"], a["tab_dtype"], a["tab_ld"], a["rows"],
+                             a["inv"], a["pos_div"], a["pos"], a["psb"], a["pss"], a["off"],
+                             a["il"], a["bwd"], NULL)
+
+
+def test_rope_validation(lib):
+    assert _rope(lib, D=127) == SHAPE
+    assert _rope(lib, D=1024) == SHAPE
+    assert _rope(lib, rows=7) == SHAPE  # positions 0..7 need 8 table rows
+    assert b"exceed" in lib.ts_last_error()
+    assert _rope(lib, off=1) == SHAPE
+    assert _rope(lib, sin=NULL) == INVALID
+    assert _rope(lib, cos=NULL, sin=NULL) == INVALID  # neither tables nor inv_freq
+    assert _rope(lib, Hk=2) == INVALID  # K heads without K pointers
+    assert _rope(lib, il=2) == INVALID
+    assert _rope(lib, dtype=9) == DTYPE
+    assert _rope(lib, S=0) == TS_OK
+
+
+def test_ce_validation(lib):
+    st = NULL
+    f = lambda **k: lib.ts_ce_fwd(k.get("x", FAKE), k.get("ld", 128), k.get("dt", 1),
+                                  k.get("lab", FAKE), k.get("N", 4), k.get("V", 128), -100,
+                                  k.get("scale", 0.0), k.get("cap", 0.0), k.get("ls", 0.0),
+                                  FAKE, FAKE, st)
+    assert f(ld=64) == SHAPE
+    assert f(V=0) == SHAPE
+    assert f(ls=1.0) == INVALID
+    assert f(cap=-1.0) == INVALID
+    assert f(lab=NULL) == INVALID
+    assert f(dt=5) == DTYPE
+    assert f(N=0) == TS_OK
+    # in-place backward needs the logits layout
+    rc = lib.ts_ce_bwd(FAKE, 128, 1, FAKE, FAKE, FAKE, 1, 1.0, FAKE, 256, 1, 4, 128, -100,
+                       0.0, 0.0, 0.0, st)
+    assert rc == INVALID
+    rc = lib.ts_ce_bwd(FAKE, 128, 1, FAKE, FAKE, FAKE, 1, 1.0, FAKE, 128, 2, 4, 128, -100,
+                       0.0, 0.0, 0.0, st)
+    assert rc == DTYPE

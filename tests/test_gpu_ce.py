@@ -1,0 +1,163 @@
+"""Cross-entropy kernels vs the oracle and the golden vectors (GPU).
+
+Bar (north star): loss within 1e-5 relative (fp32), gradients within 2e-2
+absolute; since that absolute bound is vacuous for CE gradients (|g| <=
+1/n_valid), gradients are also held to 1 bf16 ulp of the oracle.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_ulp, golden, round_to
+from trainscale_amd import ops, workloads
+from trainscale_amd.kernels import Fast_CrossEntropyLoss, fast_cross_entropy_loss
+from trainscale_amd.loss import (ChunkedCrossEntropyLoss, CrossEntropyLoss,
+                                 FusedCrossEntropyLoss)
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+TINY = 1e-37  # below bf16's normal range: v_exp_f32 flushes what the CPU keeps as a denormal
+
+
+@pytest.mark.parametrize("case", ["ce_plain", "ce_odd_v", "ce_smooth", "ce_softcap_scale"])
+def test_golden(gpu, case):
+    g = golden(case)
+    x = torch.from_numpy(g["logits"]).to(BF).to(gpu)
+    labels = torch.from_numpy(g["labels"]).to(gpu)
+    a, sc, cap = float(g["smoothing"]), float(g["scale"]), float(g["softcap"])
+    loss, lse = ops.ce_forward(x, x.shape[1], labels, -100, sc, cap, a)
+    np.testing.assert_allclose(loss.double().cpu().numpy(), g["loss"], rtol=1e-5, atol=1e-6)
+    valid = g["labels"] != -100
+    n_valid = max(int(valid.sum()), 1)
+    grad = torch.empty_like(x)
+    ops.ce_backward(x, x.shape[1], labels, lse, torch.tensor([1.0 / n_valid], device=gpu), grad,
+                    x.shape[1], 1.0, -100, sc, cap, a)
+    assert_ulp(grad, round_to(g["grad"], BF), 1, tiny=TINY, what="grad")
+
+
+def test_c3_full(gpu):
+    wl = workloads.ce_workload(gpu)
+    logits, labels = wl.tensors["logits"], wl.tensors["labels"]
+    N, V = logits.shape
+    n_valid = int((labels != -100).sum())
+    x = logits.clone().requires_grad_()
+    loss = fast_cross_entropy_loss(x, labels)
+    rows = Fast_CrossEntropyLoss.apply(logits.clone(), labels)
+    # every row's loss against the oracle, in chunks of rows
+    lab_cpu = labels.cpu()
+    ref_rows = []
+    for s in range(0, N, 1024):
+        l, _ = oracle.ce_fwd(logits[s:s + 1024].cpu(), lab_cpu[s:s + 1024])
+        ref_rows.append(l)
+    ref_rows = torch.cat(ref_rows)
+    torch.testing.assert_close(rows.cpu(), ref_rows, rtol=1e-5, atol=1e-6)
+    ref_mean = ref_rows.double().sum() / n_valid
+    assert abs(loss.item() - ref_mean.item()) <= 1e-5 * abs(ref_mean.item())
+    loss.backward()
+    grad = x.grad
+    # gradients of a sample of rows (incl. ignored ones) at 1 ulp and 2e-2 absolute
+    sample = torch.cat([torch.arange(0, 128), torch.arange(N - 128, N),
+                        (labels == -100).nonzero().flatten()[:16].cpu()])
+    ref_g = oracle.ce_bwd(logits[sample].cpu(), lab_cpu[sample], torch.tensor(1.0 / n_valid))
+    assert_ulp(grad[sample], ref_g, 1, tiny=TINY, what="grad")
+    assert (grad[sample].float().cpu() - ref_g.float()).abs().max() <= 2e-2
+    # full-size properties: ignored rows are zero, valid rows sum to ~0
+    ign = labels == -100
+    assert torch.count_nonzero(grad[ign]) == 0
+    rs = grad[~ign].float().sum(-1)
+    assert rs.abs().max().item() <= 1e-3 / n_valid
+
+
+def test_fast_ce_backward_is_in_place(gpu):
+    torch.manual_seed(0)
+    logits = (2 * torch.randn(64, 1024, device=gpu)).to(BF).requires_grad_()
+    labels = torch.randint(0, 1024, (64,), device=gpu)
+    buf = logits.detach().clone().requires_grad_()
+    loss = Fast_CrossEntropyLoss.apply(buf, labels).sum()
+    loss.backward()
+    # the gradient was written into the logits buffer saved by forward
+    ref = oracle.ce_bwd(logits.detach().cpu(), labels.cpu(), torch.tensor(1.0))
+    assert_ulp(buf.grad, ref, 1, tiny=TINY)
+
+
+@pytest.mark.parametrize("V", [8, 37, 1000, 4096, 50257, 128256])
+@pytest.mark.parametrize("dtype", [BF, torch.float16, torch.float32])
+def test_vocab_sizes_and_dtypes(gpu, V, dtype):
+    torch.manual_seed(V)
+    N = 24
+    logits = (2 * torch.randn(N, V, device=gpu)).to(dtype)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::5] = -100
+    loss, lse = ops.ce_forward(logits, V, labels)
+    ref, ref_lse = oracle.ce_fwd(logits.cpu(), labels.cpu())
+    torch.testing.assert_close(loss.cpu(), ref, rtol=1e-5, atol=1e-6)
+    grad = torch.empty_like(logits)
+    ops.ce_backward(logits, V, labels, lse, torch.tensor([0.5], device=gpu), grad, V)
+    ref_g = oracle.ce_bwd(logits.cpu(), labels.cpu(), torch.tensor(0.5))
+    if dtype == torch.float32:
+        torch.testing.assert_close(grad.cpu(), ref_g, rtol=1e-5, atol=1e-9)
+    else:
+        assert_ulp(grad, ref_g, 1, tiny=TINY if dtype == BF else 1e-7)
+
+
+def test_modules_and_reductions(gpu):
+    torch.manual_seed(1)
+    N, V = 96, 3000
+    logits = (2 * torch.randn(N, V, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[:7] = -100
+    lab = labels.cpu()
+    n_valid = int((lab != -100).sum())
+    for a in (0.0, 0.1):
+        rows, _ = oracle.ce_fwd(logits.cpu(), lab, label_smoothing=a)
+        refs = {"mean": rows.sum() / n_valid, "sum": rows.sum(), "none": rows,
+                "batchmean": rows.sum() / N}
+        for red, ref in refs.items():
+            for mod in (ChunkedCrossEntropyLoss(label_smoothing=a, reduction=red),
+                        FusedCrossEntropyLoss(label_smoothing=a, reduction=red)):
+                x = logits.clone().requires_grad_()
+                out = mod(x.view(4, N // 4, V), labels.view(4, N // 4))
+                torch.testing.assert_close(out.cpu().reshape(ref.shape), ref, rtol=1e-5, atol=1e-5)
+                out.sum().backward()
+                scale = {"mean": 1.0 / n_valid, "sum": 1.0, "none": 1.0, "batchmean": 1.0 / N}[red]
+                ref_g = oracle.ce_bwd(logits.cpu(), lab, torch.tensor(scale), label_smoothing=a)
+                assert_ulp(x.grad, ref_g, 1, tiny=TINY, what=f"{type(mod).__name__} {red} {a}")
+        if True:
+            ce = CrossEntropyLoss(label_smoothing=a)
+            out = ce(logits, labels)
+            torch.testing.assert_close(out.cpu(), refs["mean"], rtol=1e-5, atol=1e-6)
+
+
+def test_all_rows_ignored(gpu):
+    logits = torch.randn(8, 512, device=gpu).to(BF).requires_grad_()
+    labels = torch.full((8,), -100, device=gpu)
+    loss = ChunkedCrossEntropyLoss()(logits, labels)
+    assert loss.item() == 0.0
+    loss.backward()
+    assert torch.count_nonzero(logits.grad) == 0
+
+
+def test_softcap_scaling_fast_ce(gpu):
+    torch.manual_seed(2)
+    logits = (4 * torch.randn(40, 2048, device=gpu)).to(BF)
+    labels = torch.randint(0, 2048, (40,), device=gpu)
+    for cap, sc in ((30.0, 0.0), (0.0, 0.125), (5.0, 0.5)):
+        x = logits.clone().requires_grad_()
+        loss = fast_cross_entropy_loss(x, labels, logit_softcapping=cap, logit_scaling=sc)
+        rows, _ = oracle.ce_fwd(logits.cpu(), labels.cpu(), logit_scale=sc, softcap=cap)
+        assert abs(loss.item() - rows.mean().item()) <= 1e-5 * abs(rows.mean().item())
+        loss.backward()
+        ref_g = oracle.ce_bwd(logits.cpu(), labels.cpu(), torch.tensor(1.0 / 40),
+                              logit_scale=sc, softcap=cap)
+        assert_ulp(x.grad, ref_g, 1, tiny=TINY)
+
+
+def test_out_of_range_label_is_nan(gpu):
+    logits = torch.randn(3, 64, device=gpu).to(BF)
+    labels = torch.tensor([1, 64, -100], device=gpu)
+    loss, _ = ops.ce_forward(logits, 64, labels)
+    l = loss.cpu()
+    assert math.isnan(l[1]) and not math.isnan(l[0]) and l[2] == 0.0

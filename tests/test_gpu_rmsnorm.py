@@ -1,0 +1,139 @@
+"""RMSNorm kernels vs the oracle and the golden vectors (GPU).
+
+Bar: outputs and gradients within 1 bf16 ulp of the oracle (plus the north
+star's 2e-2 absolute for gradients), rstd within 1e-6 relative, dW
+bit-reproducible run to run.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import assert_ulp, golden, max_ulp, round_to
+from trainscale_amd import ops, workloads
+from trainscale_amd.kernels import (Fast_RMS_LayerNorm, RMSLayerNormFunction, RMSNorm,
+                                    fast_rms_layernorm, rms_layernorm)
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def run_fwd_bwd(fn, x, w, dy, *args):
+    xg = x.detach().clone().requires_grad_()
+    wg = w.detach().clone().requires_grad_() if w is not None else None
+    y = fn(xg, wg, *args)
+    y.backward(dy)
+    return y.detach(), xg.grad, (wg.grad if wg is not None else None)
+
+
+@pytest.mark.parametrize("case", ["rmsnorm_64", "rmsnorm_4096", "rmsnorm_100"])
+def test_golden(gpu, case):
+    g = golden(case)
+    x = torch.from_numpy(g["x"]).to(BF).to(gpu)
+    w = torch.from_numpy(g["w"]).to(BF).to(gpu)
+    dy = torch.from_numpy(g["dy"]).to(BF).to(gpu)
+    y, dx, dw = run_fwd_bwd(Fast_RMS_LayerNorm.apply, x, w, dy, float(g["eps"]))
+    assert_ulp(y, round_to(g["y"], BF), 1, what="y")
+    assert_ulp(dx, round_to(g["dx"], BF), 1, tiny=1e-4, what="dx")
+    assert_ulp(dw, round_to(g["dw"], BF), 1, tiny=1e-4, what="dw")
+
+
+def check_against_oracle(x, w, dy, eps, round_twice=False, fn=None):
+    fn = fn or (RMSLayerNormFunction.apply if round_twice else Fast_RMS_LayerNorm.apply)
+    args = (eps, True) if round_twice else (eps,)
+    y, dx, dw = run_fwd_bwd(fn, x, w, dy, *args)
+    y_ref, rstd_ref = oracle.rms_norm_fwd(x, w, eps, round_twice=round_twice)
+    dx_ref, dw_ref = oracle.rms_norm_bwd(dy, x, w, rstd_ref)
+    assert_ulp(y, y_ref, 1, what="y")
+    # rstd saved by the kernel
+    x2d, ld = ops.as_rows(x)
+    _, rstd = ops.rmsnorm_forward(x2d, ld, w, eps)
+    torch.testing.assert_close(rstd.cpu(), rstd_ref, rtol=1e-6, atol=0)
+    tiny = 1e-6 if x.dtype == torch.float32 else 1e-4
+    assert_ulp(dx, dx_ref, 1 if x.dtype != torch.float32 else 64, tiny=tiny, what="dx")
+    assert (dx.float().cpu() - dx_ref.float()).abs().max() <= 2e-2
+    if w is not None:
+        assert_ulp(dw, dw_ref, 1 if w.dtype != torch.float32 else 256, tiny=tiny, what="dw")
+        assert (dw.float().cpu() - dw_ref.float()).abs().max() <= 2e-2
+
+
+def test_c1_full(gpu):
+    wl = workloads.rmsnorm_workload(gpu)
+    x, w, dy = wl.tensors["x"], wl.tensors["w"], wl.tensors["dy"]
+    check_against_oracle(x, w, dy, 1e-6)
+
+
+@pytest.mark.parametrize("cols", [8, 64, 100, 768, 4096, 5000, 8192, 12288, 16384, 20000])
+@pytest.mark.parametrize("rows", [1, 37])
+def test_shapes_bf16(gpu, rows, cols):
+    torch.manual_seed(rows * 7 + cols)
+    x = torch.randn(rows, cols, device=gpu).to(BF)
+    w = (1 + 0.02 * torch.randn(cols, device=gpu)).to(BF)
+    dy = torch.randn(rows, cols, device=gpu).to(BF)
+    check_against_oracle(x, w, dy, 1e-6)
+
+
+@pytest.mark.parametrize("dtype,wdtype", [(torch.float16, torch.float16),
+                                          (torch.float32, torch.float32),
+                                          (BF, torch.float32), (torch.float16, torch.float32)])
+def test_dtypes(gpu, dtype, wdtype):
+    torch.manual_seed(11)
+    x = torch.randn(129, 1024, device=gpu).to(dtype)
+    w = (1 + 0.1 * torch.randn(1024, device=gpu)).to(wdtype)
+    dy = torch.randn(129, 1024, device=gpu).to(dtype)
+    check_against_oracle(x, w, dy, 1e-5)
+
+
+def test_round_twice(gpu):
+    torch.manual_seed(12)
+    x = torch.randn(513, 4096, device=gpu).to(BF)
+    w = (1 + 0.3 * torch.randn(4096, device=gpu)).to(BF)
+    dy = torch.randn(513, 4096, device=gpu).to(BF)
+    check_against_oracle(x, w, dy, 1e-6, round_twice=True)
+    y = rms_layernorm(x, w)
+    y_ref, _ = oracle.rms_norm_fwd(x, w, 1e-6, round_twice=True)
+    assert max_ulp(y.cpu(), y_ref) <= 1
+
+
+def test_no_weight_module(gpu):
+    torch.manual_seed(13)
+    m = RMSNorm(2048, eps=1e-6, elementwise_affine=False)
+    x = torch.randn(4, 33, 2048, device=gpu).to(BF).requires_grad_()
+    y = m(x)
+    y_ref, rstd = oracle.rms_norm_fwd(x.detach(), None, 1e-6)
+    assert_ulp(y, y_ref, 1)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    dx_ref, _ = oracle.rms_norm_bwd(dy, x.detach(), None, rstd)
+    assert_ulp(x.grad, dx_ref, 1, tiny=1e-4)
+
+
+def test_strided_input(gpu):
+    torch.manual_seed(14)
+    big = torch.randn(64, 3 * 4096, device=gpu).to(BF)
+    x = big[:, 4096:8192]  # row stride 3*4096, unit column stride
+    w = (1 + 0.02 * torch.randn(4096, device=gpu)).to(BF)
+    dy = torch.randn(64, 4096, device=gpu).to(BF)
+    check_against_oracle(x, w, dy, 1e-6)
+
+
+def test_dw_deterministic(gpu):
+    wl = workloads.rmsnorm_workload(gpu, scale=0.25)
+    x, w, dy = wl.tensors["x"], wl.tensors["w"], wl.tensors["dy"]
+    _, _, dw1 = run_fwd_bwd(Fast_RMS_LayerNorm.apply, x, w, dy, 1e-6)
+    _, _, dw2 = run_fwd_bwd(Fast_RMS_LayerNorm.apply, x, w, dy, 1e-6)
+    assert torch.equal(dw1, dw2)
+
+
+def test_c4_packed_rmsnorm(gpu):
+    wl = workloads.packed_workload(gpu, scale=0.25)
+    x, w, dy = wl.tensors["x"], wl.tensors["w"], wl.tensors["dy"]
+    check_against_oracle(x, w, dy, 1e-6)
+
+
+def test_empty_batch(gpu):
+    x = torch.empty(0, 4096, device=gpu, dtype=BF)
+    w = torch.ones(4096, device=gpu, dtype=BF)
+    y, dx, dw = run_fwd_bwd(Fast_RMS_LayerNorm.apply, x, w, torch.empty_like(x), 1e-6)
+    assert y.shape == (0, 4096) and dx.shape == (0, 4096)
+    assert torch.count_nonzero(dw) == 0

@@ -1,0 +1,97 @@
+"""Host-side logic that needs no GPU: no silent CPU fallback, workload generators,
+byte accounting, and the RMSNorm patch boundary."""
+import pytest
+import torch
+import torch.nn as nn
+
+from trainscale_amd import ops, registry, workloads as W
+from trainscale_amd.kernels import (Fast_RoPE, apply_rope, fast_cross_entropy_loss,
+                                    fast_rms_layernorm, rms_layernorm)
+from trainscale_amd.loss import ChunkedCrossEntropyLoss
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    x = torch.randn(4, 64)
+    w = torch.ones(64)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fast_rms_layernorm(x, w)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        rms_layernorm(x, w)
+    q = torch.randn(1, 4, 2, 16)
+    cos = torch.ones(4, 8)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        Fast_RoPE.apply(q, q.clone(), cos, cos, False)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        apply_rope(q, cos, cos)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fast_cross_entropy_loss(torch.randn(4, 32), torch.zeros(4, dtype=torch.long))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        ChunkedCrossEntropyLoss()(torch.randn(4, 32), torch.zeros(4, dtype=torch.long))
+
+
+def test_as_rows_strides():
+    t = torch.randn(3, 5, 16)
+    t2, ld = ops.as_rows(t)
+    assert t2.shape == (15, 16) and ld == 16
+    big = torch.randn(10, 48)
+    v, ld = ops.as_rows(big[:, 16:32])
+    assert ld == 48 and v.data_ptr() == big[:, 16:32].data_ptr()
+    e = torch.randn(1, 16).expand(4, 16)
+    v, ld = ops.as_rows(e)
+    assert ld == 16 and v.is_contiguous()
+
+
+def test_survey_byte_counts():
+    # compulsory traffic quoted for the configs (fwd + bwd)
+    b = W.rmsnorm_bytes(16384, 4096)
+    assert b["fwd"] == 268_509_184 and b["fwd"] + b["bwd"] == 671_244_288
+    b = W.rope_bytes(16384, 40, 128)
+    assert b["fwd"] + b["bwd"] == 671_088_640
+    b = W.rmsnorm_bytes(32768, 8192)
+    assert b["fwd"] == 1_073_889_280 and b["bwd"] == 1_610_776_576
+    b = W.rope_bytes(32768, 72, 128, pos_bytes=32768 * 8)
+    assert b["fwd"] == 1_208_221_696
+    assert W.linear_ce_flops(8192, 4096, 128256) == 25_821_343_383_552
+
+
+def test_packed_lengths_and_position_ids():
+    lens = W.packed_doc_lengths(32768, 64, 4096, 3)
+    assert sum(lens) == 32768
+    assert all(1 <= n <= 4096 for n in lens) and all(n >= 64 for n in lens[:-1])
+    pos = W.packed_position_ids(lens)
+    assert pos.shape == (1, 32768)
+    starts = [0]
+    for n in lens[:-1]:
+        starts.append(starts[-1] + n)
+    assert all(int(pos[0, s]) == 0 for s in starts)
+    assert int(pos.max()) == max(lens) - 1
+
+
+def test_workload_generators_are_seeded():
+    a = W.ce_workload("cpu", scale=1 / 256, V=1000)
+    b = W.ce_workload("cpu", scale=1 / 256, V=1000)
+    assert torch.equal(a.tensors["logits"], b.tensors["logits"])
+    labels = a.tensors["labels"]
+    assert int((labels == -100).sum()) == round(0.1 * labels.numel())
+
+
+class LlamaRMSNorm(nn.Module):
+    def __init__(self, n, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(n))
+        self.variance_epsilon = eps
+
+    def forward(self, h):
+        var = h.float().pow(2).mean(-1, keepdim=True)
+        return self.weight * (h * torch.rsqrt(var + self.variance_epsilon)).to(h.dtype)
+
+
+def test_patch_boundary_keeps_cpu_modules_on_their_own_forward():
+    model = nn.Sequential(nn.Linear(8, 8), LlamaRMSNorm(8))
+    x = torch.randn(3, 8)
+    before = model(x)
+    patcher = registry.KernelPatcher()
+    patcher.patch(model)
+    assert patcher.patched_layers == [("1", "LlamaRMSNorm")]
+    assert torch.equal(model(x), before)  # CPU tensors: the module's original forward
+    assert "LlamaRMSNorm" in registry.LAYER_PATCHES

@@ -1,0 +1,291 @@
+"""Pins the CPU oracle (oracle/ops.py) before anything is checked against it.
+
+Each oracle function is compared with formulations that do not share its code:
+the float64 golden vectors (tests/golden/make_golden.py: closed forms, complex
+rotation, smoothed-target cross-entropy, full-Jacobian RMSNorm backward),
+torch.autograd on float64 forwards, finite differences, torch's own
+F.cross_entropy, and invariants (scale/shift invariance, norm preservation,
+transpose rotation, packed == per-document). The mutation tests at the end plant
+plausible mistakes in the oracle's inputs/flags and check that these same
+comparisons catch them.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from helpers import assert_ulp, golden, max_ulp, round_to
+
+BF = torch.bfloat16
+
+
+def t32(a):
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["rmsnorm_64", "rmsnorm_4096", "rmsnorm_100"])
+def test_rmsnorm_fwd_matches_golden(case):
+    g = golden(case)
+    x, w = t32(g["x"]).to(BF), t32(g["w"]).to(BF)
+    y, rstd = oracle.rms_norm_fwd(x, w, float(g["eps"]))
+    assert_ulp(y, round_to(g["y"], BF), 1, what=case)
+    np.testing.assert_allclose(rstd.double().numpy(), g["rstd"], rtol=2e-6)
+
+
+@pytest.mark.parametrize("case", ["rmsnorm_64", "rmsnorm_4096", "rmsnorm_100"])
+def test_rmsnorm_bwd_matches_golden(case):
+    g = golden(case)
+    x, w, dy = t32(g["x"]).to(BF), t32(g["w"]).to(BF), t32(g["dy"]).to(BF)
+    _, rstd = oracle.rms_norm_fwd(x, w, float(g["eps"]))
+    dx, dw = oracle.rms_norm_bwd(dy, x, w, rstd)
+    assert_ulp(dx, round_to(g["dx"], BF), 1, tiny=1e-4, what=case + " dx")
+    assert_ulp(dw, round_to(g["dw"], BF), 1, tiny=1e-4, what=case + " dw")
+
+
+def test_rmsnorm_bwd_matches_autograd_float64():
+    torch.manual_seed(0)
+    x = torch.randn(7, 48, dtype=torch.float64, requires_grad=True)
+    w = (1 + 0.1 * torch.randn(48, dtype=torch.float64)).requires_grad_()
+    dy = torch.randn(7, 48, dtype=torch.float64)
+    eps = 1e-5
+    y = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
+    y.backward(dy)
+    _, rstd = oracle.rms_norm_fwd(x.detach().float(), w.detach().float(), eps)
+    dx, dw = oracle.rms_norm_bwd(dy.float(), x.detach().float(), w.detach().float(), rstd)
+    torch.testing.assert_close(dx.double(), x.grad, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(dw.double(), w.grad, rtol=1e-5, atol=1e-5)
+
+
+def test_rmsnorm_bwd_finite_differences():
+    torch.manual_seed(1)
+    x = torch.randn(2, 12, dtype=torch.float64)
+    w = 1 + 0.1 * torch.randn(12, dtype=torch.float64)
+    dy = torch.randn(2, 12, dtype=torch.float64)
+    eps = 1e-6
+
+    def L(xx):
+        y = xx * torch.rsqrt((xx * xx).mean(-1, keepdim=True) + eps) * w
+        return (y * dy).sum()
+
+    _, rstd = oracle.rms_norm_fwd(x.float(), w.float(), eps)
+    dx, _ = oracle.rms_norm_bwd(dy.float(), x.float(), w.float(), rstd)
+    h = 1e-6
+    for i in range(2):
+        for j in range(0, 12, 3):
+            e = torch.zeros_like(x)
+            e[i, j] = h
+            fd = (L(x + e) - L(x - e)) / (2 * h)
+            assert abs(fd.item() - dx[i, j].item()) < 1e-4
+
+
+def test_rmsnorm_invariants():
+    torch.manual_seed(2)
+    x = torch.randn(5, 64).to(BF)
+    w = torch.ones(64, dtype=BF)
+    y1, _ = oracle.rms_norm_fwd(x, w, 0.0)
+    y2, _ = oracle.rms_norm_fwd((x.float() * 4).to(BF), w, 0.0)
+    assert torch.equal(y1, y2)  # scale invariance (eps = 0, exact power-of-two scaling)
+    rms = y1.float().pow(2).mean(-1).sqrt()
+    torch.testing.assert_close(rms, torch.ones(5), atol=1e-2, rtol=0)
+    z = torch.zeros(2, 64, dtype=BF)
+    yz, _ = oracle.rms_norm_fwd(z, w, 1e-6)
+    assert torch.count_nonzero(yz.float()) == 0
+
+
+def test_rmsnorm_round_twice_is_double_rounding():
+    torch.manual_seed(3)
+    x = torch.randn(64, 256).to(BF)
+    w = (1 + 0.3 * torch.randn(256)).to(BF)
+    y1, rstd = oracle.rms_norm_fwd(x, w, 1e-6)
+    y2, _ = oracle.rms_norm_fwd(x, w, 1e-6, round_twice=True)
+    expect = ((x.float() * rstd[:, None]).to(BF).float() * w.float()).to(BF)
+    assert torch.equal(y2, expect)
+    assert max_ulp(y1, y2) <= 1
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["rope_neox_seq", "rope_inter_seq", "rope_neox_packed",
+                                  "rope_neox_far"])
+def test_rope_matches_golden(case):
+    g = golden(case)
+    x, gr = t32(g["x"]).to(BF), t32(g["g"]).to(BF)
+    pos = t32(g["positions"])
+    D = x.shape[-1]
+    cos, sin = oracle.rope_tables(D, int(pos.max()) + 1, float(g["theta"]))
+    il = bool(g["interleaved"])
+    fwd = oracle.rope_apply(x, cos, sin, pos, interleaved=il)
+    bwd = oracle.rope_apply(gr, cos, sin, pos, interleaved=il, backward=True)
+    assert_ulp(fwd, round_to(g["fwd"], BF), 1, what=case + " fwd")
+    assert_ulp(bwd, round_to(g["bwd"], BF), 1, what=case + " bwd")
+
+
+def test_rope_tables_match_float64():
+    cos, sin = oracle.rope_tables(128, 4096, 500000.0)
+    inv32 = oracle.rope_inv_freq(128, 500000.0).numpy()
+    inv64 = 1.0 / (500000.0 ** (np.arange(0, 128, 2) / 128.0))
+    np.testing.assert_allclose(inv32, inv64, rtol=3e-7)  # fp32 pow/divide of the reference
+    # the reference forms the angle in fp32 (torch.outer of fp32 operands); cos/sin of
+    # that fp32 angle must be accurate to fp32 rounding
+    ang32 = np.arange(4096, dtype=np.float32)[:, None] * inv32[None, :]
+    np.testing.assert_allclose(cos.numpy(), np.cos(ang32.astype(np.float64)), atol=2e-7)
+    np.testing.assert_allclose(sin.numpy(), np.sin(ang32.astype(np.float64)), atol=2e-7)
+
+
+def test_rope_invariants():
+    torch.manual_seed(4)
+    B, S, H, D = 2, 9, 3, 32
+    x = torch.randn(B, S, H, D, dtype=torch.float64).float()
+    cos, sin = oracle.rope_tables(D, 64, 10000.0)
+    pos = oracle.rope_positions(B, S, position_offset=3)
+    y = oracle.rope_apply(x, cos, sin, pos)
+    # pair norms preserved
+    n0 = x[..., :16] ** 2 + x[..., 16:] ** 2
+    n1 = y[..., :16] ** 2 + y[..., 16:] ** 2
+    torch.testing.assert_close(n0, n1, rtol=1e-5, atol=1e-5)
+    # backward is the inverse and the transpose
+    back = oracle.rope_apply(y, cos, sin, pos, backward=True)
+    torch.testing.assert_close(back, x, rtol=1e-5, atol=1e-5)
+    g = torch.randn_like(x)
+    lhs = (y.double() * g.double()).sum()
+    rhs = (x.double() * oracle.rope_apply(g, cos, sin, pos, backward=True).double()).sum()
+    assert abs(lhs - rhs) < 1e-3
+    # position 0 is the identity
+    p0 = torch.zeros(B, S, dtype=torch.int64)
+    torch.testing.assert_close(oracle.rope_apply(x, cos, sin, p0), x)
+
+
+def test_rope_packed_equals_per_document():
+    torch.manual_seed(5)
+    lens = [5, 3, 8]
+    T, H, D = sum(lens), 4, 16
+    x = torch.randn(1, T, H, D).to(BF)
+    pos = torch.cat([torch.arange(n) for n in lens])[None]
+    cos, sin = oracle.rope_tables(D, 16, 10000.0)
+    packed = oracle.rope_apply(x, cos, sin, pos)
+    start = 0
+    for n in lens:
+        doc = x[:, start:start + n]
+        ref = oracle.rope_apply(doc, cos, sin, oracle.rope_positions(1, n))
+        assert torch.equal(packed[:, start:start + n], ref)
+        start += n
+
+
+# ---------------------------------------------------------------------------
+# Cross-entropy
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case", ["ce_plain", "ce_odd_v", "ce_smooth", "ce_softcap_scale"])
+def test_ce_matches_golden(case):
+    g = golden(case)
+    x = t32(g["logits"]).to(BF)
+    labels = t32(g["labels"])
+    kw = dict(label_smoothing=float(g["smoothing"]), logit_scale=float(g["scale"]),
+              softcap=float(g["softcap"]))
+    loss, lse = oracle.ce_fwd(x, labels, **kw)
+    np.testing.assert_allclose(loss.double().numpy(), g["loss"], rtol=1e-5, atol=1e-6)
+    valid = g["labels"] != -100
+    np.testing.assert_allclose(lse.double().numpy()[valid], g["lse"][valid], rtol=1e-6)
+    n_valid = max(int(valid.sum()), 1)
+    grad = oracle.ce_bwd(x, labels, torch.tensor(1.0 / n_valid), **kw)
+    assert_ulp(grad, round_to(g["grad"], BF), 1, tiny=1e-30, what=case + " grad")
+
+
+def test_ce_matches_torch_cross_entropy():
+    torch.manual_seed(6)
+    x = (2 * torch.randn(32, 1000)).to(BF)
+    labels = torch.randint(0, 1000, (32,))
+    labels[[3, 7]] = -100
+    for a in (0.0, 0.2):
+        loss, _ = oracle.ce_fwd(x, labels, label_smoothing=a)
+        ref = F.cross_entropy(x.double(), labels, ignore_index=-100, reduction="none",
+                              label_smoothing=a)
+        torch.testing.assert_close(loss.double(), ref, rtol=1e-5, atol=1e-6)
+        xr = x.double().requires_grad_()
+        F.cross_entropy(xr, labels, ignore_index=-100, reduction="sum", label_smoothing=a).backward()
+        grad = oracle.ce_bwd(x, labels, torch.tensor(1.0), label_smoothing=a,
+                             out_dtype=torch.float32)
+        torch.testing.assert_close(grad.double(), xr.grad, rtol=1e-4, atol=1e-6)
+
+
+def test_ce_invariants():
+    torch.manual_seed(7)
+    V = 512
+    x = torch.randn(8, V)
+    labels = torch.randint(0, V, (8,))
+    l1, _ = oracle.ce_fwd(x, labels)
+    l2, _ = oracle.ce_fwd(x + 3.0, labels)
+    torch.testing.assert_close(l1, l2, rtol=1e-5, atol=1e-5)
+    lu, _ = oracle.ce_fwd(torch.zeros(3, V), torch.tensor([0, 5, 9]))
+    torch.testing.assert_close(lu, torch.full((3,), math.log(V)), rtol=1e-6, atol=1e-6)
+    g = oracle.ce_bwd(x, labels, torch.tensor(1.0), out_dtype=torch.float32)
+    torch.testing.assert_close(g.sum(-1), torch.zeros(8), atol=1e-5, rtol=0)
+    lab = labels.clone()
+    lab[:] = -100
+    lz, _ = oracle.ce_fwd(x, lab)
+    assert torch.count_nonzero(lz) == 0
+    gz = oracle.ce_bwd(x, lab, torch.tensor(1.0))
+    assert torch.count_nonzero(gz.float()) == 0
+
+
+def test_linear_ce_matches_golden():
+    g = golden("linear_ce")
+    h, w = t32(g["hidden"]).to(BF), t32(g["weight"]).to(BF)
+    labels = t32(g["labels"])
+    loss, gh, gw = oracle.linear_ce(h, w, labels)
+    np.testing.assert_allclose(float(loss), float(g["loss"]), rtol=1e-5)
+    assert_ulp(gh, round_to(g["grad_hidden"], BF), 1, tiny=1e-6, what="grad_hidden")
+    assert_ulp(gw, round_to(g["grad_weight"], BF), 1, tiny=1e-6, what="grad_weight")
+
+
+# ---------------------------------------------------------------------------
+# Mutations: plausible mistakes in the oracle must fail the checks above.
+# ---------------------------------------------------------------------------
+
+def test_mutation_rope_sign_is_caught():
+    g = golden("rope_neox_seq")
+    x = t32(g["x"]).to(BF)
+    pos = t32(g["positions"])
+    cos, sin = oracle.rope_tables(16, 8, float(g["theta"]))
+    wrong = oracle.rope_apply(x, cos, sin, pos, backward=True)  # sign of sin flipped
+    with pytest.raises(AssertionError):
+        assert_ulp(wrong, round_to(g["fwd"], BF), 1)
+    wrong_layout = oracle.rope_apply(x, cos, sin, pos, interleaved=True)
+    with pytest.raises(AssertionError):
+        assert_ulp(wrong_layout, round_to(g["fwd"], BF), 1)
+
+
+def test_mutation_rmsnorm_terms_are_caught():
+    g = golden("rmsnorm_64")
+    x, w, dy = t32(g["x"]).to(BF), t32(g["w"]).to(BF), t32(g["dy"]).to(BF)
+    y_bad, _ = oracle.rms_norm_fwd(x, None, float(g["eps"]))  # weight dropped
+    with pytest.raises(AssertionError):
+        assert_ulp(y_bad, round_to(g["y"], BF), 1)
+    _, rstd = oracle.rms_norm_fwd(x, w, float(g["eps"]))
+    dx_bad, _ = oracle.rms_norm_bwd(dy, x, None, rstd)  # w missing from dx
+    with pytest.raises(AssertionError):
+        assert_ulp(dx_bad, round_to(g["dx"], BF), 1, tiny=1e-4)
+
+
+def test_mutation_ce_label_is_caught():
+    g = golden("ce_plain")
+    x = t32(g["logits"]).to(BF)
+    labels = t32(g["labels"])
+    shifted = torch.where(labels >= 0, (labels + 1) % x.shape[1], labels)
+    loss, _ = oracle.ce_fwd(x, shifted)
+    with pytest.raises(AssertionError):
+        np.testing.assert_allclose(loss.double().numpy(), g["loss"], rtol=1e-5, atol=1e-6)
+    n_valid = int((labels != -100).sum())
+    grad_bad = oracle.ce_bwd(x, labels, torch.tensor(1.0))  # dloss scale 1/n_valid dropped
+    with pytest.raises(AssertionError):
+        assert_ulp(grad_bad, round_to(g["grad"], BF), 1)
+    assert n_valid > 1

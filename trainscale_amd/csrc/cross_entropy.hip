@@ -1,0 +1,470 @@
+// Vocabulary cross-entropy forward/backward for gfx950.
+//
+// Forward: one 256-thread workgroup per row. Each lane streams the row with
+// 16-byte non-temporal loads (kUnroll vectors in flight per lane) and keeps an
+// online (max, sum of exp) pair: a new chunk's max rescales the running sum
+// once per chunk, not once per element. exp is evaluated as
+// exp2(z*log2(e) - m*log2(e)) with one FMA and one v_exp_f32. The per-lane
+// pairs are folded with a wave64 DPP max, a rescale, and DPP sums, then across
+// the four waves through LDS. Rows whose label is ignore_index are not read:
+// their loss is 0 and their lse is stored as 0 (the backward never reads it).
+//
+// Backward: one workgroup per row, one read and one write per element:
+// grad = dloss * (softmax - onehot) (with the label-smoothing, softcap and
+// logit-scale chain rules), written with 16-byte stores; it may overwrite the
+// logits in place. Ignored rows are written as zeros without being read.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace {
+
+using namespace ts;
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kUnroll = 4;
+
+struct Xform {
+  float scale;    // 0 = off
+  float softcap;  // 0 = off
+};
+
+// Applies logit scaling then softcapping, in the reference's order
+// (kernels/triton_kernels.py:214-217).
+template <bool kXform>
+__device__ inline float xform(float x, const Xform& t) {
+  if constexpr (kXform) {
+    if (t.scale != 0.f) x = t.scale * x;
+    if (t.softcap != 0.f) x = t.softcap * tanhf(x / t.softcap);
+  }
+  return x;
+}
+
+// Block-wide (max, sum exp, sum z) fold. Every thread receives the results.
+__device__ inline void block_fold(float& m, float& s, float& sz, float* lds) {
+  float bm = wave_max(m);
+  const int wid = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (lane == 0) lds[wid] = bm;
+  __syncthreads();
+  bm = lds[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) bm = fmaxf(bm, lds[i]);
+  __syncthreads();
+  // Rescale this lane's sum to the row max. A lane that saw only -inf has
+  // s == 0 and contributes nothing.
+  const float scaled = s == 0.f ? 0.f : s * fast_exp2((m - bm) * kLog2e);
+  float ws = wave_sum(scaled);
+  float wz = wave_sum(sz);
+  if (lane == 0) {
+    lds[wid] = ws;
+    lds[kWaves + wid] = wz;
+  }
+  __syncthreads();
+  float ts = 0.f, tz = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    ts += lds[i];
+    tz += lds[kWaves + i];
+  }
+  m = bm;
+  s = ts;
+  sz = tz;
+}
+
+template <typename T, bool kXform, bool kSmooth>
+__global__ __launch_bounds__(kThreads) void ce_fwd_vec(const T* __restrict__ logits, int64_t ld,
+                                                       const int64_t* __restrict__ labels,
+                                                       int64_t V, int64_t nvec,
+                                                       int64_t ignore_index, Xform xf,
+                                                       float smoothing, float* __restrict__ loss,
+                                                       float* __restrict__ lse_out) {
+  constexpr int VE = Elt<T>::kVec;
+  __shared__ float lds[2 * kWaves];
+  const int64_t row = blockIdx.x;
+  const int64_t label = labels[row];
+  if (label == ignore_index) {
+    if (threadIdx.x == 0) {
+      loss[row] = 0.f;
+      lse_out[row] = 0.f;
+    }
+    return;
+  }
+  const T* xr = logits + row * ld;
+  float m = -INFINITY, s = 0.f, sz = 0.f;
+  const int64_t step = (int64_t)kThreads * kUnroll;
+  int64_t base = 0;
+  for (; base + step <= nvec; base += step) {
+    u32x4 buf[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) buf[u] = ld16_stream(xr + (base + u * kThreads + threadIdx.x) * VE);
+    float z[kUnroll][VE];
+    float lm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      Elt<T>::unpack(buf[u], z[u]);
+#pragma unroll
+      for (int i = 0; i < VE; ++i) {
+        z[u][i] = xform<kXform>(z[u][i], xf);
+        lm = fmaxf(lm, z[u][i]);
+        if constexpr (kSmooth) sz += z[u][i];
+      }
+    }
+    if (lm > m) {
+      s = s == 0.f ? 0.f : s * fast_exp2((m - lm) * kLog2e);
+      m = lm;
+    }
+    const float mb = m * kLog2e;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int i = 0; i < VE; ++i) s += fast_exp2(__builtin_fmaf(z[u][i], kLog2e, -mb));
+  }
+  // Tail: fewer than kThreads*kUnroll vectors remain.
+  for (int64_t v = base + threadIdx.x; v < nvec; v += kThreads) {
+    float z[VE];
+    Elt<T>::unpack(ld16_stream(xr + v * VE), z);
+    float lm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      z[i] = xform<kXform>(z[i], xf);
+      lm = fmaxf(lm, z[i]);
+      if constexpr (kSmooth) sz += z[i];
+    }
+    if (lm > m) {
+      s = s == 0.f ? 0.f : s * fast_exp2((m - lm) * kLog2e);
+      m = lm;
+    }
+    const float mb = m * kLog2e;
+#pragma unroll
+    for (int i = 0; i < VE; ++i) s += fast_exp2(__builtin_fmaf(z[i], kLog2e, -mb));
+  }
+  block_fold(m, s, sz, lds);
+  if (threadIdx.x == 0) {
+    const float l = m + logf(s);
+    float out;
+    if (label < 0 || label >= V) {
+      out = __builtin_nanf("");
+    } else {
+      const float zt = xform<kXform>(Elt<T>::load1(xr + label), xf);
+      out = l - zt;
+      if constexpr (kSmooth) out = (1.f - smoothing) * out + smoothing * (l - sz / (float)V);
+    }
+    loss[row] = out;
+    lse_out[row] = l;
+  }
+}
+
+// Element-wise forward for rows that are not 16-byte aligned / divisible.
+template <typename T, bool kXform, bool kSmooth>
+__global__ __launch_bounds__(kThreads) void ce_fwd_generic(
+    const T* __restrict__ logits, int64_t ld, const int64_t* __restrict__ labels, int64_t V,
+    int64_t ignore_index, Xform xf, float smoothing, float* __restrict__ loss,
+    float* __restrict__ lse_out) {
+  __shared__ float lds[2 * kWaves];
+  const int64_t row = blockIdx.x;
+  const int64_t label = labels[row];
+  if (label == ignore_index) {
+    if (threadIdx.x == 0) {
+      loss[row] = 0.f;
+      lse_out[row] = 0.f;
+    }
+    return;
+  }
+  const T* xr = logits + row * ld;
+  float m = -INFINITY, s = 0.f, sz = 0.f;
+  for (int64_t j = threadIdx.x; j < V; j += kThreads) {
+    const float z = xform<kXform>(Elt<T>::load1(xr + j), xf);
+    if constexpr (kSmooth) sz += z;
+    if (z > m) {
+      s = s == 0.f ? 0.f : s * fast_exp2((m - z) * kLog2e);
+      m = z;
+    }
+    s += fast_exp2((z - m) * kLog2e);
+  }
+  block_fold(m, s, sz, lds);
+  if (threadIdx.x == 0) {
+    const float l = m + logf(s);
+    float out;
+    if (label < 0 || label >= V) {
+      out = __builtin_nanf("");
+    } else {
+      const float zt = xform<kXform>(Elt<T>::load1(xr + label), xf);
+      out = l - zt;
+      if constexpr (kSmooth) out = (1.f - smoothing) * out + smoothing * (l - sz / (float)V);
+    }
+    loss[row] = out;
+    lse_out[row] = l;
+  }
+}
+
+struct BwdRow {
+  float dl;     // upstream gradient of this row
+  float lse2;   // lse * log2(e)
+  int64_t label;
+};
+
+// Gradient of one element given its raw logit x at column j.
+template <bool kXform, bool kSmooth>
+__device__ inline float ce_grad(float x, int64_t j, const BwdRow& r, const Xform& xf,
+                                float smoothing, float inv_v) {
+  float z = x, t = 0.f;
+  if constexpr (kXform) {
+    if (xf.scale != 0.f) z = xf.scale * z;
+    if (xf.softcap != 0.f) {
+      t = tanhf(z / xf.softcap);
+      z = xf.softcap * t;
+    }
+  }
+  const float p = fast_exp2(__builtin_fmaf(z, kLog2e, -r.lse2));
+  float g;
+  if constexpr (kSmooth) {
+    g = (1.f - smoothing) * (j == r.label ? p - 1.f : p) + smoothing * (p - inv_v);
+  } else {
+    g = j == r.label ? p - 1.f : p;
+  }
+  if constexpr (kXform) {
+    if (xf.softcap != 0.f) g = g * (1.f - t * t);
+    if (xf.scale != 0.f) g = g * xf.scale;
+  }
+  return r.dl * g;
+}
+
+template <typename T, typename G, bool kXform, bool kSmooth>
+__global__ __launch_bounds__(kThreads) void ce_bwd_vec(
+    const T* logits, int64_t ld, const int64_t* __restrict__ labels,
+    const float* __restrict__ lse, const float* __restrict__ dloss, int64_t dloss_stride,
+    float dloss_scale, G* grad, int64_t ld_grad, int64_t V, int64_t nvec, int64_t ignore_index,
+    Xform xf, float smoothing) {
+  constexpr int VE = Elt<T>::kVec;
+  static_assert(Elt<G>::kVec == VE || sizeof(G) == 4, "grad vector width");
+  const int64_t row = blockIdx.x;
+  const int64_t label = labels[row];
+  G* gr = grad + row * ld_grad;
+  if (label == ignore_index) {
+    const float zero[VE] = {};
+    for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
+      if constexpr (sizeof(G) == 4 && VE == 8) {
+        st16_stream(gr + v * VE, Elt<float>::pack(zero));
+        st16_stream(gr + v * VE + 4, Elt<float>::pack(zero));
+      } else {
+        st16_stream(gr + v * VE, Elt<G>::pack(zero));
+      }
+    }
+    return;
+  }
+  BwdRow r;
+  r.dl = dloss[row * dloss_stride] * dloss_scale;
+  r.lse2 = lse[row] * kLog2e;
+  r.label = label;
+  const float inv_v = 1.f / (float)V;
+  const T* xr = logits + row * ld;
+  const int64_t step = (int64_t)kThreads * kUnroll;
+  int64_t base = 0;
+  for (; base + step <= nvec; base += step) {
+    u32x4 buf[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) buf[u] = ld16_stream(xr + (base + u * kThreads + threadIdx.x) * VE);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t v = base + u * kThreads + threadIdx.x;
+      float x[VE], g[VE];
+      Elt<T>::unpack(buf[u], x);
+#pragma unroll
+      for (int i = 0; i < VE; ++i) g[i] = ce_grad<kXform, kSmooth>(x[i], v * VE + i, r, xf, smoothing, inv_v);
+      if constexpr (sizeof(G) == 4 && VE == 8) {
+        st16_stream(gr + v * VE, Elt<float>::pack(g));
+        st16_stream(gr + v * VE + 4, Elt<float>::pack(g + 4));
+      } else {
+        st16_stream(gr + v * VE, Elt<G>::pack(g));
+      }
+    }
+  }
+  for (int64_t v = base + threadIdx.x; v < nvec; v += kThreads) {
+    float x[VE], g[VE];
+    Elt<T>::unpack(ld16_stream(xr + v * VE), x);
+#pragma unroll
+    for (int i = 0; i < VE; ++i) g[i] = ce_grad<kXform, kSmooth>(x[i], v * VE + i, r, xf, smoothing, inv_v);
+    if constexpr (sizeof(G) == 4 && VE == 8) {
+      st16_stream(gr + v * VE, Elt<float>::pack(g));
+      st16_stream(gr + v * VE + 4, Elt<float>::pack(g + 4));
+    } else {
+      st16_stream(gr + v * VE, Elt<G>::pack(g));
+    }
+  }
+}
+
+template <typename T, typename G, bool kXform, bool kSmooth>
+__global__ __launch_bounds__(kThreads) void ce_bwd_generic(
+    const T* logits, int64_t ld, const int64_t* __restrict__ labels,
+    const float* __restrict__ lse, const float* __restrict__ dloss, int64_t dloss_stride,
+    float dloss_scale, G* grad, int64_t ld_grad, int64_t V, int64_t ignore_index, Xform xf,
+    float smoothing) {
+  const int64_t row = blockIdx.x;
+  const int64_t label = labels[row];
+  G* gr = grad + row * ld_grad;
+  if (label == ignore_index) {
+    for (int64_t j = threadIdx.x; j < V; j += kThreads) Elt<G>::store1(gr + j, 0.f);
+    return;
+  }
+  BwdRow r;
+  r.dl = dloss[row * dloss_stride] * dloss_scale;
+  r.lse2 = lse[row] * kLog2e;
+  r.label = label;
+  const float inv_v = 1.f / (float)V;
+  const T* xr = logits + row * ld;
+  for (int64_t j = threadIdx.x; j < V; j += kThreads) {
+    const float x = Elt<T>::load1(xr + j);
+    Elt<G>::store1(gr + j, ce_grad<kXform, kSmooth>(x, j, r, xf, smoothing, inv_v));
+  }
+}
+
+template <typename T>
+ts_status fwd_typed(const void* logits, int64_t ld, const int64_t* labels, int64_t N, int64_t V,
+                    int64_t ignore_index, Xform xf, float smoothing, float* loss, float* lse,
+                    hipStream_t st) {
+  constexpr int VE = sizeof(T) == 4 ? 4 : 8;
+  const T* lp = static_cast<const T*>(logits);
+  const bool vec = V % VE == 0 && ld % VE == 0 && ts_host::aligned16(logits);
+  const bool xform_on = xf.scale != 0.f || xf.softcap != 0.f;
+  const bool smooth = smoothing != 0.f;
+  const dim3 grid((unsigned)N), block(kThreads);
+#define TS_CE_FWD(X, S)                                                                       \
+  if (xform_on == X && smooth == S) {                                                         \
+    if (vec) {                                                                                \
+      hipLaunchKernelGGL((ce_fwd_vec<T, X, S>), grid, block, 0, st, lp, ld, labels, V,        \
+                         V / VE, ignore_index, xf, smoothing, loss, lse);                     \
+      return ts_host::check_launch("ce_fwd_vec");                                             \
+    }                                                                                         \
+    hipLaunchKernelGGL((ce_fwd_generic<T, X, S>), grid, block, 0, st, lp, ld, labels, V,      \
+                       ignore_index, xf, smoothing, loss, lse);                               \
+    return ts_host::check_launch("ce_fwd_generic");                                           \
+  }
+  TS_CE_FWD(false, false)
+  TS_CE_FWD(false, true)
+  TS_CE_FWD(true, false)
+  TS_CE_FWD(true, true)
+#undef TS_CE_FWD
+  return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "ce_fwd: unreachable");
+}
+
+template <typename T, typename G>
+ts_status bwd_typed(const void* logits, int64_t ld, const int64_t* labels, const float* lse,
+                    const float* dloss, int64_t dloss_stride, float dloss_scale, void* grad,
+                    int64_t ld_grad, int64_t N, int64_t V, int64_t ignore_index, Xform xf,
+                    float smoothing, hipStream_t st) {
+  constexpr int VE = sizeof(T) == 4 ? 4 : 8;
+  const T* lp = static_cast<const T*>(logits);
+  G* gp = static_cast<G*>(grad);
+  // The vector path needs the grad rows to take the same vector width.
+  const bool grad_ok = sizeof(G) == sizeof(T) || (sizeof(G) == 4 && VE == 8);
+  const bool vec = V % VE == 0 && ld % VE == 0 && ld_grad % VE == 0 &&
+                   ts_host::aligned16(logits) && ts_host::aligned16(grad) && grad_ok;
+  const bool xform_on = xf.scale != 0.f || xf.softcap != 0.f;
+  const bool smooth = smoothing != 0.f;
+  const dim3 grid((unsigned)N), block(kThreads);
+#define TS_CE_BWD(X, S)                                                                        \
+  if (xform_on == X && smooth == S) {                                                          \
+    if (vec) {                                                                                 \
+      hipLaunchKernelGGL((ce_bwd_vec<T, G, X, S>), grid, block, 0, st, lp, ld, labels, lse,    \
+                         dloss, dloss_stride, dloss_scale, gp, ld_grad, V, V / VE,             \
+                         ignore_index, xf, smoothing);                                         \
+      return ts_host::check_launch("ce_bwd_vec");                                              \
+    }                                                                                          \
+    hipLaunchKernelGGL((ce_bwd_generic<T, G, X, S>), grid, block, 0, st, lp, ld, labels, lse,  \
+                       dloss, dloss_stride, dloss_scale, gp, ld_grad, V, ignore_index, xf,     \
+                       smoothing);                                                             \
+    return ts_host::check_launch("ce_bwd_generic");                                            \
+  }
+  TS_CE_BWD(false, false)
+  TS_CE_BWD(false, true)
+  TS_CE_BWD(true, false)
+  TS_CE_BWD(true, true)
+#undef TS_CE_BWD
+  return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "ce_bwd: unreachable");
+}
+
+ts_status check_ce(const void* logits, int64_t ld, ts_dtype dtype, const int64_t* labels,
+                   int64_t N, int64_t V, float logit_scale, float softcap,
+                   float label_smoothing) {
+  using ts_host::fail;
+  if (!ts_host::valid_dtype(dtype)) return fail(TS_ERR_UNSUPPORTED_DTYPE, "ce: bad dtype");
+  if (N < 0 || V <= 0) return fail(TS_ERR_SHAPE, "ce: bad shape N=%lld V=%lld", (long long)N,
+                                   (long long)V);
+  if (N > 0x7fffffffLL) return fail(TS_ERR_SHAPE, "ce: too many rows (%lld)", (long long)N);
+  if (ld < V) return fail(TS_ERR_SHAPE, "ce: row stride %lld < V %lld", (long long)ld,
+                          (long long)V);
+  if (N > 0 && (logits == nullptr || labels == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "ce: logits or labels is NULL");
+  if (!(label_smoothing >= 0.f && label_smoothing < 1.f))
+    return fail(TS_ERR_INVALID_ARGUMENT, "ce: label_smoothing must be in [0, 1)");
+  if (!isfinite(logit_scale) || !isfinite(softcap) || softcap < 0.f)
+    return fail(TS_ERR_INVALID_ARGUMENT, "ce: bad logit_scale/softcap");
+  return TS_OK;
+}
+
+}  // namespace
+
+extern "C" ts_status ts_ce_fwd(const void* logits, int64_t ld, ts_dtype dtype,
+                               const int64_t* labels, int64_t N, int64_t V,
+                               int64_t ignore_index, float logit_scale, float softcap,
+                               float label_smoothing, float* loss, float* lse,
+                               ts_stream_t stream) {
+  ts_status s = check_ce(logits, ld, dtype, labels, N, V, logit_scale, softcap, label_smoothing);
+  if (s != TS_OK) return s;
+  if (N > 0 && (loss == nullptr || lse == nullptr))
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "ce_fwd: loss or lse is NULL");
+  if (N == 0) return TS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Xform xf{logit_scale, softcap};
+  switch (dtype) {
+    case TS_BF16:
+      return fwd_typed<__bf16>(logits, ld, labels, N, V, ignore_index, xf, label_smoothing, loss,
+                               lse, st);
+    case TS_F16:
+      return fwd_typed<_Float16>(logits, ld, labels, N, V, ignore_index, xf, label_smoothing,
+                                 loss, lse, st);
+    case TS_F32:
+      return fwd_typed<float>(logits, ld, labels, N, V, ignore_index, xf, label_smoothing, loss,
+                              lse, st);
+  }
+  return ts_host::fail(TS_ERR_UNSUPPORTED_DTYPE, "ce_fwd: bad dtype");
+}
+
+extern "C" ts_status ts_ce_bwd(const void* logits, int64_t ld, ts_dtype dtype,
+                               const int64_t* labels, const float* lse, const float* dloss,
+                               int64_t dloss_stride, float dloss_scale, void* grad,
+                               int64_t ld_grad, ts_dtype grad_dtype, int64_t N, int64_t V,
+                               int64_t ignore_index, float logit_scale, float softcap,
+                               float label_smoothing, ts_stream_t stream) {
+  using ts_host::fail;
+  ts_status s = check_ce(logits, ld, dtype, labels, N, V, logit_scale, softcap, label_smoothing);
+  if (s != TS_OK) return s;
+  if (!ts_host::valid_dtype(grad_dtype))
+    return fail(TS_ERR_UNSUPPORTED_DTYPE, "ce_bwd: bad grad dtype");
+  if (grad_dtype != dtype && grad_dtype != TS_F32)
+    return fail(TS_ERR_UNSUPPORTED_DTYPE, "ce_bwd: grad dtype must equal logits dtype or be f32");
+  if (N > 0 && (lse == nullptr || dloss == nullptr || grad == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "ce_bwd: lse, dloss or grad is NULL");
+  if (ld_grad < V) return fail(TS_ERR_SHAPE, "ce_bwd: grad row stride < V");
+  if (dloss_stride < 0) return fail(TS_ERR_SHAPE, "ce_bwd: negative dloss stride");
+  if (grad == logits && (ld_grad != ld || grad_dtype != dtype))
+    return fail(TS_ERR_INVALID_ARGUMENT, "ce_bwd: in-place grad needs the logits layout");
+  if (N == 0) return TS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Xform xf{logit_scale, softcap};
+#define TS_CE_BWD_T(T)                                                                         \
+  return grad_dtype == TS_F32 && dtype != TS_F32                                               \
+             ? bwd_typed<T, float>(logits, ld, labels, lse, dloss, dloss_stride, dloss_scale,  \
+                                   grad, ld_grad, N, V, ignore_index, xf, label_smoothing, st) \
+             : bwd_typed<T, T>(logits, ld, labels, lse, dloss, dloss_stride, dloss_scale,      \
+                               grad, ld_grad, N, V, ignore_index, xf, label_smoothing, st);
+  switch (dtype) {
+    case TS_BF16: TS_CE_BWD_T(__bf16)
+    case TS_F16: TS_CE_BWD_T(_Float16)
+    case TS_F32: TS_CE_BWD_T(float)
+  }
+#undef TS_CE_BWD_T
+  return fail(TS_ERR_UNSUPPORTED_DTYPE, "ce_bwd: bad dtype");
+}

@@ -1,0 +1,570 @@
+// RMSNorm forward/backward for gfx950.
+//
+// Forward (register path): one row per wave64. Each lane loads its share of
+// the row with 16-byte loads (lane-interleaved, so every load instruction of a
+// wave covers one contiguous 1 KiB span), keeps it in VGPRs, reduces the sum
+// of squares with DPP, and writes y from the same registers: x is read from
+// HBM exactly once. Four rows per 256-thread workgroup.
+//
+// Backward (register path): 8 waves per workgroup, one workgroup per compute
+// unit (grid capped at the CU count). Each wave walks rows with a grid stride:
+// per row it reads dy and x once, reduces sum(dy*w*xhat) with DPP, writes dx,
+// and accumulates dy*xhat for dW in fp32 registers. At the end the 8 waves
+// fold their accumulators through LDS in a fixed order and the workgroup
+// writes one fp32 partial row; a second kernel sums the partial rows in a
+// fixed order. dW is therefore bit-reproducible run to run (no float atomics),
+// unlike the reference's atomic_add variant.
+//
+// Generic path (row length not a multiple of the 16-byte vector, unaligned
+// pointers, or rows too long for registers): one workgroup per row with
+// element-wise loads and two passes over the row.
+#include "common.hpp"
+
+namespace {
+
+using namespace ts;
+
+// Loads kVec weights for the 16-byte data vector starting at element e.
+template <typename W, int kVec>
+__device__ inline void load_w(const W* __restrict__ w, int64_t e, float* f) {
+  if constexpr (sizeof(W) == 4) {
+#pragma unroll
+    for (int h = 0; h < kVec / 4; ++h) Elt<float>::unpack(ld16(w + e + 4 * h), f + 4 * h);
+  } else {
+    static_assert(Elt<W>::kVec == kVec, "16-bit weight vector must match data vector");
+    Elt<W>::unpack(ld16(w + e), f);
+  }
+}
+
+constexpr int kFwdWaves = 4;
+constexpr int kBwdWaves = 8;
+
+// ---------------------------------------------------------------------------
+// Forward, register path.
+// ---------------------------------------------------------------------------
+template <typename T, typename W, int kMaxV>
+__global__ __launch_bounds__(kFwdWaves* kWave) void rms_fwd_reg(
+    const T* __restrict__ x, int64_t ldx, const W* __restrict__ w, T* __restrict__ y,
+    int64_t ldy, float* __restrict__ rstd_out, int64_t rows, int nvec, float fcols, float eps,
+    int twice) {
+  constexpr int V = Elt<T>::kVec;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * kFwdWaves + threadIdx.x / kWave;
+  if (row >= rows) return;  // wave-uniform; no workgroup barrier below
+
+  const T* xr = x + row * ldx;
+  u32x4 xv[kMaxV];
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    const int v = lane + j * kWave;
+    xv[j] = v < nvec ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    float f[V];
+    Elt<T>::unpack(xv[j], f);
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+  }
+  ss = wave_sum(ss);
+  // mean(x^2) = sum / n (a division, as the reference divides by n_cols), then
+  // 1/sqrt with correctly rounded sqrt and divide.
+  const float rstd = 1.0f / __builtin_sqrtf(ss / fcols + eps);
+  if (lane == 0) rstd_out[row] = rstd;
+
+  T* yr = y + row * ldy;
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j) {
+    const int v = lane + j * kWave;
+    if (v < nvec) {
+      float f[V];
+      Elt<T>::unpack(xv[j], f);
+      if (w != nullptr) {
+        float wf[V];
+        load_w<W, V>(w, (int64_t)v * V, wf);
+        if (twice) {
+#pragma unroll
+          for (int i = 0; i < V; ++i) f[i] = Elt<T>::round(f[i] * rstd) * wf[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < V; ++i) f[i] = (f[i] * rstd) * wf[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) f[i] = f[i] * rstd;
+      }
+      st16_stream(yr + (int64_t)v * V, Elt<T>::pack(f));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, register path: dx plus per-workgroup dW partial rows.
+// kSplit waves share one row (each holds kMaxV vectors per lane); their
+// partial row sums meet in double-buffered LDS slots, one barrier per step.
+// ---------------------------------------------------------------------------
+template <typename T, typename W, int kMaxV, int kSplit>
+__global__ __launch_bounds__(kBwdWaves* kWave) void rms_bwd_reg(
+    const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x, int64_t ldx,
+    const W* __restrict__ w, const float* __restrict__ rstd_in, T* __restrict__ dx,
+    int64_t lddx, float* __restrict__ partial, int64_t rows, int nvec, float fcols) {
+  constexpr int V = Elt<T>::kVec;
+  constexpr int kRowsPerStep = kBwdWaves / kSplit;
+  extern __shared__ float lds_acc[];  // [nvec * V] fp32
+  __shared__ float red[2][kBwdWaves];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int sub = wid % kSplit;
+  const int vbase = sub * kWave + lane;
+
+  float acc[kMaxV][V];
+#pragma unroll
+  for (int j = 0; j < kMaxV; ++j)
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[j][i] = 0.f;
+
+  const int64_t nsteps = (rows + kRowsPerStep - 1) / kRowsPerStep;
+  int it = 0;
+  // The loop bound is uniform over the workgroup (barriers inside when kSplit > 1).
+  for (int64_t g = blockIdx.x; g < nsteps; g += gridDim.x, ++it) {
+    const int64_t row = g * kRowsPerStep + wid / kSplit;
+    const bool valid = row < rows;
+    const T* xr = x + row * ldx;
+    const T* dyr = dy + row * lddy;
+    u32x4 xv[kMaxV], dv[kMaxV];
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+      const int v = vbase + j * kWave * kSplit;
+      const bool ok = valid && v < nvec;
+      xv[j] = ok ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+      dv[j] = ok ? ld16_stream(dyr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+    }
+    const float rstd = valid ? rstd_in[row] : 0.f;
+    // c1 = mean(dy * w * xhat)
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxV; ++j) {
+      const int v = vbase + j * kWave * kSplit;
+      if (v < nvec) {
+        float xf[V], df[V], wf[V];
+        Elt<T>::unpack(xv[j], xf);
+        Elt<T>::unpack(dv[j], df);
+        if (w != nullptr) {
+          load_w<W, V>(w, (int64_t)v * V, wf);
+        } else {
+#pragma unroll
+          for (int i = 0; i < V; ++i) wf[i] = 1.f;
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const float xh = xf[i] * rstd;
+          s = __builtin_fmaf(df[i] * wf[i], xh, s);
+          acc[j][i] = __builtin_fmaf(df[i], xh, acc[j][i]);
+        }
+      }
+    }
+    float c1;
+    if constexpr (kSplit == 1) {
+      c1 = wave_sum(s) / fcols;
+    } else {
+      const float sw = wave_sum(s);
+      if (lane == 0) red[it & 1][wid] = sw;
+      __syncthreads();
+      const int first = (wid / kSplit) * kSplit;
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < kSplit; ++k) t += red[it & 1][first + k];
+      c1 = t / fcols;
+    }
+    if (valid) {
+      T* dxr = dx + row * lddx;
+#pragma unroll
+      for (int j = 0; j < kMaxV; ++j) {
+        const int v = vbase + j * kWave * kSplit;
+        if (v < nvec) {
+          float xf[V], df[V], wf[V], o[V];
+          Elt<T>::unpack(xv[j], xf);
+          Elt<T>::unpack(dv[j], df);
+          if (w != nullptr) {
+            load_w<W, V>(w, (int64_t)v * V, wf);
+          } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i) wf[i] = 1.f;
+          }
+#pragma unroll
+          for (int i = 0; i < V; ++i) o[i] = rstd * (df[i] * wf[i] - (xf[i] * rstd) * c1);
+          st16_stream(dxr + (int64_t)v * V, Elt<T>::pack(o));
+        }
+      }
+    }
+  }
+
+  if (partial == nullptr) return;  // dW not requested (uniform over the grid)
+  // Fold the waves' accumulators in wave order through one LDS row.
+  for (int wv = 0; wv < kBwdWaves; ++wv) {
+    if (wid == wv) {
+#pragma unroll
+      for (int j = 0; j < kMaxV; ++j) {
+        const int v = vbase + j * kWave * kSplit;
+        if (v < nvec) {
+#pragma unroll
+          for (int i = 0; i < V; ++i) {
+            float* p = lds_acc + v * V + i;
+            *p = (wv < kSplit ? 0.f : *p) + acc[j][i];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const int ncols = nvec * V;
+  float* prow = partial + (int64_t)blockIdx.x * ncols;
+  for (int c = threadIdx.x * 4; c < ncols; c += kBwdWaves * kWave * 4) {
+    // ncols is a multiple of 4 on this path (16-byte vectors of >= 2-byte data)
+    *reinterpret_cast<float4*>(prow + c) = *reinterpret_cast<const float4*>(lds_acc + c);
+  }
+}
+
+// dW[c] = sum over partial rows in a fixed order. 64 columns per workgroup,
+// 4 row-groups per column combined in a fixed order through LDS.
+template <typename W>
+__global__ __launch_bounds__(256) void rms_dw_reduce(const float* __restrict__ partial,
+                                                     int64_t nparts, int64_t cols,
+                                                     W* __restrict__ dw) {
+  __shared__ float red[4][64];
+  const int cl = threadIdx.x & 63;
+  const int g = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + cl;
+  float s = 0.f;
+  if (c < cols) {
+    for (int64_t b = g; b < nparts; b += 4) s += partial[b * cols + c];
+  }
+  red[g][cl] = s;
+  __syncthreads();
+  if (g == 0 && c < cols) {
+    const float t = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
+    Elt<W>::store1(dw + c, t);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic path: one 256-thread workgroup per row, element-wise.
+// ---------------------------------------------------------------------------
+template <typename T, typename W>
+__global__ __launch_bounds__(256) void rms_fwd_generic(const T* __restrict__ x, int64_t ldx,
+                                                       const W* __restrict__ w,
+                                                       T* __restrict__ y, int64_t ldy,
+                                                       float* __restrict__ rstd_out,
+                                                       int64_t cols, float eps, int twice) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ldx;
+  float ss = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float f = Elt<T>::load1(xr + c);
+    ss = __builtin_fmaf(f, f, ss);
+  }
+  ss = block_sum<4>(ss, red);
+  const float rstd = 1.0f / __builtin_sqrtf(ss / (float)cols + eps);
+  if (threadIdx.x == 0) rstd_out[row] = rstd;
+  T* yr = y + row * ldy;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float f = Elt<T>::load1(xr + c);
+    float o;
+    if (w != nullptr) {
+      const float wf = Elt<W>::load1(w + c);
+      o = twice ? Elt<T>::round(f * rstd) * wf : (f * rstd) * wf;
+    } else {
+      o = f * rstd;
+    }
+    Elt<T>::store1(yr + c, o);
+  }
+}
+
+template <typename T, typename W>
+__global__ __launch_bounds__(256) void rms_bwd_dx_generic(
+    const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x, int64_t ldx,
+    const W* __restrict__ w, const float* __restrict__ rstd_in, T* __restrict__ dx,
+    int64_t lddx, int64_t cols) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ldx;
+  const T* dyr = dy + row * lddy;
+  const float rstd = rstd_in[row];
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float wf = w != nullptr ? Elt<W>::load1(w + c) : 1.f;
+    s = __builtin_fmaf(Elt<T>::load1(dyr + c) * wf, Elt<T>::load1(xr + c) * rstd, s);
+  }
+  const float c1 = block_sum<4>(s, red) / (float)cols;
+  T* dxr = dx + row * lddx;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float wf = w != nullptr ? Elt<W>::load1(w + c) : 1.f;
+    const float xh = Elt<T>::load1(xr + c) * rstd;
+    Elt<T>::store1(dxr + c, rstd * (Elt<T>::load1(dyr + c) * wf - xh * c1));
+  }
+}
+
+// partial[g][c] = sum over rows r in row-group g of dy[r,c] * x[r,c] * rstd[r]
+template <typename T>
+__global__ __launch_bounds__(256) void rms_bwd_dw_generic(
+    const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x, int64_t ldx,
+    const float* __restrict__ rstd_in, float* __restrict__ partial, int64_t rows,
+    int64_t cols, int64_t rows_per_group) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t g = blockIdx.y;
+  if (c >= cols) return;
+  const int64_t r0 = g * rows_per_group;
+  const int64_t r1 = r0 + rows_per_group < rows ? r0 + rows_per_group : rows;
+  float s = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    s = __builtin_fmaf(Elt<T>::load1(dy + r * lddy + c), Elt<T>::load1(x + r * ldx + c) * rstd_in[r],
+                       s);
+  }
+  partial[g * cols + c] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+constexpr int kMaxVecPerLane = 16;
+constexpr int kMaxBwdVec = 8;
+
+int pick_maxv(int64_t nvec) {
+  for (int m = 1; m <= kMaxVecPerLane; m *= 2)
+    if (nvec <= (int64_t)m * kWave) return m;
+  return 0;
+}
+
+template <typename T, typename W>
+bool vec_ok(const void* a, int64_t lda, int64_t cols, const void* w) {
+  constexpr int V = sizeof(T) == 4 ? 4 : 8;
+  return cols % V == 0 && lda % V == 0 && ts_host::aligned16(a) &&
+         (w == nullptr || ts_host::aligned16(w));
+}
+
+template <typename T, typename W>
+ts_status fwd_typed(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy,
+                    float* rstd, int64_t rows, int64_t cols, float eps, int twice,
+                    hipStream_t st) {
+  constexpr int V = sizeof(T) == 4 ? 4 : 8;
+  const T* xp = static_cast<const T*>(x);
+  const W* wp = static_cast<const W*>(w);
+  T* yp = static_cast<T*>(y);
+  const int64_t nvec = cols / V;
+  const int maxv = pick_maxv(nvec);
+  if (vec_ok<T, W>(x, ldx, cols, w) && vec_ok<T, W>(y, ldy, cols, nullptr) && maxv > 0) {
+    const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
+    const dim3 block(kFwdWaves * kWave);
+#define TS_LAUNCH_FWD(M)                                                                       \
+  case M:                                                                                      \
+    hipLaunchKernelGGL((rms_fwd_reg<T, W, M>), grid, block, 0, st, xp, ldx, wp, yp, ldy, rstd, \
+                       rows, (int)nvec, (float)cols, eps, twice);                              \
+    break;
+    switch (maxv) {
+      TS_LAUNCH_FWD(1)
+      TS_LAUNCH_FWD(2)
+      TS_LAUNCH_FWD(4)
+      TS_LAUNCH_FWD(8)
+      TS_LAUNCH_FWD(16)
+    }
+#undef TS_LAUNCH_FWD
+    return ts_host::check_launch("rms_fwd_reg");
+  }
+  hipLaunchKernelGGL((rms_fwd_generic<T, W>), dim3((unsigned)rows), dim3(256), 0, st, xp, ldx,
+                     wp, yp, ldy, rstd, cols, eps, twice);
+  return ts_host::check_launch("rms_fwd_generic");
+}
+
+// Workgroups of the register-path backward: one per row-step, capped at the
+// CU count (each workgroup writes one dW partial row).
+int64_t bwd_reg_grid(int64_t rows, int split) {
+  const int64_t per_step = kBwdWaves / split;
+  const int64_t want = (rows + per_step - 1) / per_step;
+  const int64_t cap = ts_host::cu_count();
+  return want < cap ? want : cap;
+}
+
+constexpr int64_t kGenericRowsPerGroup = 64;
+
+template <typename T, typename W>
+ts_status bwd_typed(const void* dy, int64_t lddy, const void* x, int64_t ldx, const void* w,
+                    const float* rstd, void* dx, int64_t lddx, void* dw, float* ws,
+                    int64_t rows, int64_t cols, hipStream_t st) {
+  constexpr int V = sizeof(T) == 4 ? 4 : 8;
+  const T* dyp = static_cast<const T*>(dy);
+  const T* xp = static_cast<const T*>(x);
+  const W* wp = static_cast<const W*>(w);
+  T* dxp = static_cast<T*>(dx);
+  const int64_t nvec = cols / V;
+  // Up to 8 vectors per lane; longer rows are split across 2 or 4 waves.
+  int split = 1;
+  while (split <= 4 && nvec > (int64_t)kWave * kMaxBwdVec * split) split *= 2;
+  const int maxv = split == 1 ? pick_maxv(nvec) : kMaxBwdVec;
+  int64_t nparts = 0;
+  // The dW fold stages one fp32 row in LDS; keep it within 64 KiB.
+  const bool lds_ok = dw == nullptr || cols * (int64_t)sizeof(float) <= 65536 - 1024;
+  if (split <= 4 && lds_ok && maxv > 0 && maxv <= kMaxBwdVec && vec_ok<T, W>(x, ldx, cols, w) &&
+      vec_ok<T, W>(dy, lddy, cols, nullptr) && vec_ok<T, W>(dx, lddx, cols, nullptr)) {
+    const int64_t grid = bwd_reg_grid(rows, split);
+    const size_t lds = dw != nullptr ? (size_t)cols * sizeof(float) : 0;
+    float* part = dw != nullptr ? ws : nullptr;
+#define TS_LAUNCH_BWD(M, SP)                                                                    \
+  if (maxv == M && split == SP) {                                                               \
+    hipLaunchKernelGGL((rms_bwd_reg<T, W, M, SP>), dim3((unsigned)grid),                        \
+                       dim3(kBwdWaves * kWave), lds, st, dyp, lddy, xp, ldx, wp, rstd, dxp,     \
+                       lddx, part, rows, (int)nvec, (float)cols);                               \
+  }
+    TS_LAUNCH_BWD(1, 1)
+    TS_LAUNCH_BWD(2, 1)
+    TS_LAUNCH_BWD(4, 1)
+    TS_LAUNCH_BWD(8, 1)
+    TS_LAUNCH_BWD(8, 2)
+    TS_LAUNCH_BWD(8, 4)
+#undef TS_LAUNCH_BWD
+    ts_status s = ts_host::check_launch("rms_bwd_reg");
+    if (s != TS_OK) return s;
+    nparts = grid;
+  } else {
+    hipLaunchKernelGGL((rms_bwd_dx_generic<T, W>), dim3((unsigned)rows), dim3(256), 0, st, dyp,
+                       lddy, xp, ldx, wp, rstd, dxp, lddx, cols);
+    ts_status s = ts_host::check_launch("rms_bwd_dx_generic");
+    if (s != TS_OK) return s;
+    if (dw != nullptr) {
+      nparts = (rows + kGenericRowsPerGroup - 1) / kGenericRowsPerGroup;
+      hipLaunchKernelGGL((rms_bwd_dw_generic<T>), dim3((unsigned)((cols + 255) / 256),
+                                                       (unsigned)nparts),
+                         dim3(256), 0, st, dyp, lddy, xp, ldx, rstd, ws, rows, cols,
+                         kGenericRowsPerGroup);
+      s = ts_host::check_launch("rms_bwd_dw_generic");
+      if (s != TS_OK) return s;
+    }
+  }
+  if (dw != nullptr) {
+    hipLaunchKernelGGL((rms_dw_reduce<W>), dim3((unsigned)((cols + 63) / 64)), dim3(256), 0, st,
+                       ws, nparts, cols, static_cast<W*>(dw));
+    return ts_host::check_launch("rms_dw_reduce");
+  }
+  return TS_OK;
+}
+
+// Number of partial rows either backward path produces (upper bound).
+int64_t bwd_partial_rows(int64_t rows) {
+  const int64_t reg = bwd_reg_grid(rows, 1);
+  const int64_t gen = (rows + kGenericRowsPerGroup - 1) / kGenericRowsPerGroup;
+  return reg > gen ? reg : gen;
+}
+
+ts_status check_common(const void* x, int64_t ldx, ts_dtype x_dtype, const void* w,
+                       ts_dtype w_dtype, int64_t rows, int64_t cols) {
+  using ts_host::fail;
+  if (!ts_host::valid_dtype(x_dtype) || (w != nullptr && !ts_host::valid_dtype(w_dtype)))
+    return fail(TS_ERR_UNSUPPORTED_DTYPE, "rmsnorm: unsupported dtype (x=%d, w=%d)", (int)x_dtype,
+                (int)w_dtype);
+  if (w != nullptr && w_dtype != x_dtype && w_dtype != TS_F32)
+    return fail(TS_ERR_UNSUPPORTED_DTYPE,
+                "rmsnorm: weight dtype must equal the data dtype or be float32");
+  if (rows < 0 || cols <= 0)
+    return fail(TS_ERR_SHAPE, "rmsnorm: bad shape rows=%lld cols=%lld", (long long)rows,
+                (long long)cols);
+  if (cols > (int64_t)1 << 30 || rows > ((int64_t)1 << 31) - 1)
+    return fail(TS_ERR_SHAPE, "rmsnorm: shape too large rows=%lld cols=%lld", (long long)rows,
+                (long long)cols);
+  if (x == nullptr && rows > 0) return fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm: x is NULL");
+  if (ldx < cols) return fail(TS_ERR_SHAPE, "rmsnorm: row stride %lld < cols %lld",
+                              (long long)ldx, (long long)cols);
+  return TS_OK;
+}
+
+}  // namespace
+
+extern "C" ts_status ts_rmsnorm_fwd(const void* x, int64_t ldx, ts_dtype x_dtype, const void* w,
+                                    ts_dtype w_dtype, void* y, int64_t ldy, float* rstd,
+                                    int64_t rows, int64_t cols, float eps, int32_t round_mode,
+                                    ts_stream_t stream) {
+  using ts_host::fail;
+  ts_status s = check_common(x, ldx, x_dtype, w, w_dtype, rows, cols);
+  if (s != TS_OK) return s;
+  if (rows > 0 && (y == nullptr || rstd == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_fwd: y or rstd is NULL");
+  if (ldy < cols) return fail(TS_ERR_SHAPE, "rmsnorm_fwd: y row stride < cols");
+  if (!(eps >= 0.f)) return fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_fwd: eps must be >= 0");
+  if (round_mode != TS_RMS_ROUND_ONCE && round_mode != TS_RMS_ROUND_TWICE)
+    return fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_fwd: bad round_mode %d", (int)round_mode);
+  if (rows == 0) return TS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // Double rounding only exists when the weight has the 16-bit data dtype.
+  const int twice = round_mode == TS_RMS_ROUND_TWICE && w != nullptr && w_dtype == x_dtype &&
+                    x_dtype != TS_F32;
+  switch (x_dtype) {
+    case TS_BF16:
+      return w_dtype == TS_F32 && w != nullptr
+                 ? fwd_typed<__bf16, float>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st)
+                 : fwd_typed<__bf16, __bf16>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st);
+    case TS_F16:
+      return w_dtype == TS_F32 && w != nullptr
+                 ? fwd_typed<_Float16, float>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st)
+                 : fwd_typed<_Float16, _Float16>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice,
+                                                 st);
+    case TS_F32:
+      return fwd_typed<float, float>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st);
+  }
+  return fail(TS_ERR_UNSUPPORTED_DTYPE, "rmsnorm_fwd: unsupported dtype");
+}
+
+extern "C" size_t ts_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)bwd_partial_rows(rows) * (size_t)cols * sizeof(float);
+}
+
+extern "C" ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx,
+                                    ts_dtype x_dtype, const void* w, ts_dtype w_dtype,
+                                    const float* rstd, void* dx, int64_t lddx, void* dw,
+                                    void* workspace, size_t workspace_bytes, int64_t rows,
+                                    int64_t cols, ts_stream_t stream) {
+  using ts_host::fail;
+  ts_status s = check_common(x, ldx, x_dtype, w, w_dtype, rows, cols);
+  if (s != TS_OK) return s;
+  if (rows > 0 && (dy == nullptr || rstd == nullptr || dx == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: dy, rstd or dx is NULL");
+  if (lddy < cols || lddx < cols) return fail(TS_ERR_SHAPE, "rmsnorm_bwd: row stride < cols");
+  if (dw != nullptr && w == nullptr)
+    return fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: dw requested without a weight");
+  if (dw != nullptr && rows > 0) {
+    const size_t need = ts_rmsnorm_bwd_workspace_size(rows, cols);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(TS_ERR_WORKSPACE, "rmsnorm_bwd: workspace needs %zu bytes, got %zu", need,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    if (!ts_host::aligned16(workspace))
+      return fail(TS_ERR_WORKSPACE, "rmsnorm_bwd: workspace must be 16-byte aligned");
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows == 0) {
+    // Empty batch: dW is all zeros.
+    if (dw != nullptr) {
+      if (hipMemsetAsync(dw, 0, (size_t)cols * ts_host::dtype_size(w_dtype), st) != hipSuccess)
+        return fail(TS_ERR_LAUNCH, "rmsnorm_bwd: memset of dw failed");
+    }
+    return TS_OK;
+  }
+  float* ws = static_cast<float*>(workspace);
+  switch (x_dtype) {
+    case TS_BF16:
+      return w != nullptr && w_dtype == TS_F32
+                 ? bwd_typed<__bf16, float>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows,
+                                            cols, st)
+                 : bwd_typed<__bf16, __bf16>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows,
+                                             cols, st);
+    case TS_F16:
+      return w != nullptr && w_dtype == TS_F32
+                 ? bwd_typed<_Float16, float>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows,
+                                              cols, st)
+                 : bwd_typed<_Float16, _Float16>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws,
+                                                 rows, cols, st);
+    case TS_F32:
+      return bwd_typed<float, float>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows, cols,
+                                     st);
+  }
+  return fail(TS_ERR_UNSUPPORTED_DTYPE, "rmsnorm_bwd: unsupported dtype");
+}

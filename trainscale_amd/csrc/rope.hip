@@ -1,0 +1,342 @@
+// Rotary position embedding (RoPE) forward/backward for gfx950.
+//
+// One 256-thread workgroup handles kTok consecutive tokens (b, s) and every
+// head of both tensors (Q heads then K heads) at those tokens. Phase 1 fills
+// LDS with cos/sin for the workgroup's tokens: either gathered from the
+// caller's tables at pos(b, s), or evaluated in registers from the fp32 angle
+// fp32(pos / pos_div) * inv_freq[i] (the product torch.outer forms on the
+// host), so each (token, frequency) pair is evaluated once and reused across
+// all Hq + Hk heads. Phase 2 streams the heads: a task is one 16-byte vector
+// from each half of a head (NeoX layout: pairs (i, i + D/2)) or one 16-byte
+// vector of adjacent pairs (interleaved layout), so Q and K are read and
+// written exactly once with 128-bit accesses. Backward is the same kernel
+// with sin negated (the transpose rotation).
+//
+// A generic element-wise kernel covers unaligned tensors and head dims whose
+// half is not a multiple of the vector width.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace {
+
+using namespace ts;
+
+constexpr int kTok = 4;           // tokens per workgroup
+constexpr int kThreads = 256;
+constexpr int kMaxHalf = 256;     // head_dim <= 512
+
+struct RopeArgs {
+  const void* q_in;
+  void* q_out;
+  int64_t q_in_sb, q_in_ss, q_in_sh;
+  int64_t q_out_sb, q_out_ss, q_out_sh;
+  const void* k_in;
+  void* k_out;
+  int64_t k_in_sb, k_in_ss, k_in_sh;
+  int64_t k_out_sb, k_out_ss, k_out_sh;
+  int32_t Hq, Hk;
+  int64_t S, ntok;
+  int32_t half;
+  const void* cos_tab;
+  const void* sin_tab;
+  int64_t tab_ld, table_rows;
+  float pos_div;
+  const int64_t* position_ids;
+  int64_t pos_sb, pos_ss, position_offset;
+  int32_t backward;
+  int32_t tasks_per_head;    // 16-byte tasks per head (vector path) or pairs per head
+  int32_t tasks_per_token;   // tasks_per_head * (Hq + Hk)
+  uint32_t tpt_magic;        // ceil(2^32 / tasks_per_token)
+  uint32_t tph_magic;        // ceil(2^32 / tasks_per_head)
+  float inv_freq[kMaxHalf];
+};
+
+// Exact quotient for n < 2^16 and d < 2^16 (magic = ceil(2^32 / d)).
+__device__ inline uint32_t fast_div(uint32_t n, uint32_t magic) { return __umulhi(n, magic); }
+
+template <typename TabT>
+__device__ inline float tab_load(const void* p, int64_t idx) {
+  return Elt<TabT>::load1(static_cast<const TabT*>(p) + idx);
+}
+
+// Phase 1: cos/sin of the workgroup's tokens into LDS ([kTok][half] each).
+template <typename TabT, bool kTable>
+__device__ inline void fill_angles(const RopeArgs& a, int64_t tok0, float* cs, float* sn) {
+  const int n = kTok * a.half;
+  for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+    const int i = idx / a.half;
+    const int f = idx - i * a.half;
+    const int64_t t = tok0 + i;
+    float c = 1.f, s = 0.f;
+    if (t < a.ntok) {
+      const int64_t b = t / a.S;
+      const int64_t sq = t - b * a.S;
+      const int64_t pos = a.position_ids != nullptr
+                              ? a.position_ids[b * a.pos_sb + sq * a.pos_ss]
+                              : sq + a.position_offset;
+      if constexpr (kTable) {
+        if (pos >= 0 && pos < a.table_rows) {
+          c = tab_load<TabT>(a.cos_tab, pos * a.tab_ld + f);
+          s = tab_load<TabT>(a.sin_tab, pos * a.tab_ld + f);
+        } else {
+          c = s = __builtin_nanf("");
+        }
+      } else {
+        const float ang = ((float)pos / a.pos_div) * a.inv_freq[f];
+        sincosf(ang, &s, &c);
+      }
+      if (a.backward) s = -s;
+    }
+    cs[idx] = c;
+    sn[idx] = s;
+  }
+}
+
+template <typename T, typename TabT, bool kTable, bool kInterleaved>
+__global__ __launch_bounds__(kThreads) void rope_vec_kernel(const RopeArgs a) {
+  constexpr int V = Elt<T>::kVec;
+  extern __shared__ float lds[];
+  float* cs = lds;
+  float* sn = lds + kTok * a.half;
+  const int64_t tok0 = (int64_t)blockIdx.x * kTok;
+  fill_angles<TabT, kTable>(a, tok0, cs, sn);
+  __syncthreads();
+
+  const int64_t ntok_here = a.ntok - tok0 < kTok ? a.ntok - tok0 : kTok;
+  const int total = (int)ntok_here * a.tasks_per_token;
+  for (int f = threadIdx.x; f < total; f += kThreads) {
+    const int i = (int)fast_div((uint32_t)f, a.tpt_magic);
+    const int r = f - i * a.tasks_per_token;
+    const int hh = (int)fast_div((uint32_t)r, a.tph_magic);
+    const int j = r - hh * a.tasks_per_head;
+    const int64_t t = tok0 + i;
+    const int64_t b = t / a.S;
+    const int64_t sq = t - b * a.S;
+    const T* src;
+    T* dst;
+    if (hh < a.Hq) {
+      src = static_cast<const T*>(a.q_in) + b * a.q_in_sb + sq * a.q_in_ss + hh * a.q_in_sh;
+      dst = static_cast<T*>(a.q_out) + b * a.q_out_sb + sq * a.q_out_ss + hh * a.q_out_sh;
+    } else {
+      const int kh = hh - a.Hq;
+      src = static_cast<const T*>(a.k_in) + b * a.k_in_sb + sq * a.k_in_ss + kh * a.k_in_sh;
+      dst = static_cast<T*>(a.k_out) + b * a.k_out_sb + sq * a.k_out_ss + kh * a.k_out_sh;
+    }
+    const float* crow = cs + i * a.half;
+    const float* srow = sn + i * a.half;
+    if constexpr (!kInterleaved) {
+      const int e1 = j * V;
+      const int e2 = a.half + j * V;
+      const u32x4 v1 = ld16_stream(src + e1);
+      const u32x4 v2 = ld16_stream(src + e2);
+      float x1[V], x2[V], o1[V], o2[V];
+      Elt<T>::unpack(v1, x1);
+      Elt<T>::unpack(v2, x2);
+#pragma unroll
+      for (int p = 0; p < V; ++p) {
+        const float c = crow[e1 + p];
+        const float s = srow[e1 + p];
+        o1[p] = x1[p] * c - x2[p] * s;
+        o2[p] = x2[p] * c + x1[p] * s;
+      }
+      st16_stream(dst + e1, Elt<T>::pack(o1));
+      st16_stream(dst + e2, Elt<T>::pack(o2));
+    } else {
+      const int e = j * V;
+      const u32x4 v = ld16_stream(src + e);
+      float x[V], o[V];
+      Elt<T>::unpack(v, x);
+#pragma unroll
+      for (int p = 0; p < V / 2; ++p) {
+        const float c = crow[e / 2 + p];
+        const float s = srow[e / 2 + p];
+        o[2 * p] = x[2 * p] * c - x[2 * p + 1] * s;
+        o[2 * p + 1] = x[2 * p + 1] * c + x[2 * p] * s;
+      }
+      st16_stream(dst + e, Elt<T>::pack(o));
+    }
+  }
+}
+
+// Element-wise fallback: a task is one rotation pair.
+template <typename T, typename TabT, bool kTable, bool kInterleaved>
+__global__ __launch_bounds__(kThreads) void rope_generic_kernel(const RopeArgs a) {
+  extern __shared__ float lds[];
+  float* cs = lds;
+  float* sn = lds + kTok * a.half;
+  const int64_t tok0 = (int64_t)blockIdx.x * kTok;
+  fill_angles<TabT, kTable>(a, tok0, cs, sn);
+  __syncthreads();
+  const int64_t ntok_here = a.ntok - tok0 < kTok ? a.ntok - tok0 : kTok;
+  const int total = (int)ntok_here * a.tasks_per_token;
+  for (int f = threadIdx.x; f < total; f += kThreads) {
+    const int i = (int)fast_div((uint32_t)f, a.tpt_magic);
+    const int r = f - i * a.tasks_per_token;
+    const int hh = (int)fast_div((uint32_t)r, a.tph_magic);
+    const int p = r - hh * a.tasks_per_head;  // pair index
+    const int64_t t = tok0 + i;
+    const int64_t b = t / a.S;
+    const int64_t sq = t - b * a.S;
+    const T* src;
+    T* dst;
+    if (hh < a.Hq) {
+      src = static_cast<const T*>(a.q_in) + b * a.q_in_sb + sq * a.q_in_ss + hh * a.q_in_sh;
+      dst = static_cast<T*>(a.q_out) + b * a.q_out_sb + sq * a.q_out_ss + hh * a.q_out_sh;
+    } else {
+      const int kh = hh - a.Hq;
+      src = static_cast<const T*>(a.k_in) + b * a.k_in_sb + sq * a.k_in_ss + kh * a.k_in_sh;
+      dst = static_cast<T*>(a.k_out) + b * a.k_out_sb + sq * a.k_out_ss + kh * a.k_out_sh;
+    }
+    const int e1 = kInterleaved ? 2 * p : p;
+    const int e2 = kInterleaved ? 2 * p + 1 : p + a.half;
+    const float x1 = Elt<T>::load1(src + e1);
+    const float x2 = Elt<T>::load1(src + e2);
+    const float c = cs[i * a.half + p];
+    const float s = sn[i * a.half + p];
+    Elt<T>::store1(dst + e1, x1 * c - x2 * s);
+    Elt<T>::store1(dst + e2, x2 * c + x1 * s);
+  }
+}
+
+uint32_t magic_for(uint32_t d) {
+  return (uint32_t)((((uint64_t)1 << 32) + d - 1) / d);
+}
+
+template <typename T, typename TabT, bool kTable, bool kInterleaved>
+ts_status launch_typed(RopeArgs& a, bool vec, hipStream_t st) {
+  constexpr int V = sizeof(T) == 4 ? 4 : 8;
+  const int ntask_head = vec ? (kInterleaved ? 2 * a.half / V : a.half / V) : a.half;
+  a.tasks_per_head = ntask_head;
+  a.tasks_per_token = ntask_head * (a.Hq + a.Hk);
+  a.tpt_magic = magic_for((uint32_t)a.tasks_per_token);
+  a.tph_magic = magic_for((uint32_t)a.tasks_per_head);
+  const dim3 grid((unsigned)((a.ntok + kTok - 1) / kTok));
+  const size_t lds = 2 * sizeof(float) * kTok * a.half;
+  if (vec) {
+    hipLaunchKernelGGL((rope_vec_kernel<T, TabT, kTable, kInterleaved>), grid, dim3(kThreads),
+                       lds, st, a);
+    return ts_host::check_launch("rope_vec_kernel");
+  }
+  hipLaunchKernelGGL((rope_generic_kernel<T, TabT, kTable, kInterleaved>), grid, dim3(kThreads),
+                     lds, st, a);
+  return ts_host::check_launch("rope_generic_kernel");
+}
+
+template <typename T, typename TabT>
+ts_status dispatch_layout(RopeArgs& a, bool table, bool interleaved, bool vec, hipStream_t st) {
+  if (table) {
+    return interleaved ? launch_typed<T, TabT, true, true>(a, vec, st)
+                       : launch_typed<T, TabT, true, false>(a, vec, st);
+  }
+  return interleaved ? launch_typed<T, TabT, false, true>(a, vec, st)
+                     : launch_typed<T, TabT, false, false>(a, vec, st);
+}
+
+template <typename T>
+ts_status dispatch_tab(RopeArgs& a, ts_dtype tab_dtype, bool table, bool interleaved, bool vec,
+                       hipStream_t st) {
+  if (!table) return dispatch_layout<T, float>(a, false, interleaved, vec, st);
+  switch (tab_dtype) {
+    case TS_F32: return dispatch_layout<T, float>(a, true, interleaved, vec, st);
+    case TS_BF16: return dispatch_layout<T, __bf16>(a, true, interleaved, vec, st);
+    case TS_F16: return dispatch_layout<T, _Float16>(a, true, interleaved, vec, st);
+  }
+  return ts_host::fail(TS_ERR_UNSUPPORTED_DTYPE, "rope: unsupported table dtype");
+}
+
+bool strides_vec_ok(int64_t sb, int64_t ss, int64_t sh, int V) {
+  return sb % V == 0 && ss % V == 0 && sh % V == 0;
+}
+
+}  // namespace
+
+extern "C" ts_status ts_rope_apply(
+    const void* q_in, void* q_out, int64_t q_in_sb, int64_t q_in_ss, int64_t q_in_sh,
+    int64_t q_out_sb, int64_t q_out_ss, int64_t q_out_sh, int64_t Hq, const void* k_in,
+    void* k_out, int64_t k_in_sb, int64_t k_in_ss, int64_t k_in_sh, int64_t k_out_sb,
+    int64_t k_out_ss, int64_t k_out_sh, int64_t Hk, ts_dtype dtype, int64_t B, int64_t S,
+    int64_t D, const void* cos_tab, const void* sin_tab, ts_dtype tab_dtype, int64_t tab_ld,
+    int64_t table_rows, const float* inv_freq, float pos_div, const int64_t* position_ids,
+    int64_t pos_sb, int64_t pos_ss, int64_t position_offset, int32_t interleaved,
+    int32_t backward, ts_stream_t stream) {
+  using ts_host::fail;
+  if (!ts_host::valid_dtype(dtype)) return fail(TS_ERR_UNSUPPORTED_DTYPE, "rope: bad dtype");
+  if (B < 0 || S < 0 || Hq < 0 || Hk < 0 || D <= 0)
+    return fail(TS_ERR_SHAPE, "rope: bad shape B=%lld S=%lld Hq=%lld Hk=%lld D=%lld",
+                (long long)B, (long long)S, (long long)Hq, (long long)Hk, (long long)D);
+  if (D % 2 != 0 || D / 2 > kMaxHalf)
+    return fail(TS_ERR_SHAPE, "rope: head_dim must be even and <= %d (got %lld)", 2 * kMaxHalf,
+                (long long)D);
+  if (Hq + Hk > 4096) return fail(TS_ERR_SHAPE, "rope: more than 4096 heads per token");
+  if (Hq > 0 && (q_in == nullptr || q_out == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "rope: q pointers are NULL");
+  if (Hk > 0 && (k_in == nullptr || k_out == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "rope: k pointers are NULL");
+  if (interleaved != 0 && interleaved != 1)
+    return fail(TS_ERR_INVALID_ARGUMENT, "rope: interleaved must be 0 or 1");
+  if (backward != 0 && backward != 1)
+    return fail(TS_ERR_INVALID_ARGUMENT, "rope: backward must be 0 or 1");
+  const bool table = cos_tab != nullptr || sin_tab != nullptr;
+  if (table) {
+    if (cos_tab == nullptr || sin_tab == nullptr)
+      return fail(TS_ERR_INVALID_ARGUMENT, "rope: cos and sin tables must both be given");
+    if (!ts_host::valid_dtype(tab_dtype))
+      return fail(TS_ERR_UNSUPPORTED_DTYPE, "rope: bad table dtype");
+    if (tab_ld < D / 2 || table_rows <= 0)
+      return fail(TS_ERR_SHAPE, "rope: table must be [rows > 0, >= D/2] (ld=%lld rows=%lld)",
+                  (long long)tab_ld, (long long)table_rows);
+    if (position_ids == nullptr && S > 0 &&
+        (position_offset < 0 || position_offset + S > table_rows))
+      return fail(TS_ERR_SHAPE,
+                  "rope: positions [%lld, %lld) exceed the %lld-row cos/sin table",
+                  (long long)position_offset, (long long)(position_offset + S),
+                  (long long)table_rows);
+  } else {
+    if (inv_freq == nullptr)
+      return fail(TS_ERR_INVALID_ARGUMENT, "rope: need cos/sin tables or inv_freq");
+    if (!(pos_div > 0.f)) return fail(TS_ERR_INVALID_ARGUMENT, "rope: pos_div must be > 0");
+  }
+  const int64_t ntok = B * S;
+  if (ntok == 0 || Hq + Hk == 0) return TS_OK;
+  if (ntok > ((int64_t)1 << 40)) return fail(TS_ERR_SHAPE, "rope: too many tokens");
+
+  RopeArgs a{};
+  a.q_in = q_in; a.q_out = q_out;
+  a.q_in_sb = q_in_sb; a.q_in_ss = q_in_ss; a.q_in_sh = q_in_sh;
+  a.q_out_sb = q_out_sb; a.q_out_ss = q_out_ss; a.q_out_sh = q_out_sh;
+  a.k_in = k_in; a.k_out = k_out;
+  a.k_in_sb = k_in_sb; a.k_in_ss = k_in_ss; a.k_in_sh = k_in_sh;
+  a.k_out_sb = k_out_sb; a.k_out_ss = k_out_ss; a.k_out_sh = k_out_sh;
+  a.Hq = (int32_t)Hq; a.Hk = (int32_t)Hk;
+  a.S = S; a.ntok = ntok; a.half = (int32_t)(D / 2);
+  a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.tab_ld = tab_ld; a.table_rows = table_rows;
+  a.pos_div = pos_div > 0.f ? pos_div : 1.f;
+  a.position_ids = position_ids; a.pos_sb = pos_sb; a.pos_ss = pos_ss;
+  a.position_offset = position_offset;
+  a.backward = backward;
+  if (!table) {
+    for (int i = 0; i < a.half; ++i) a.inv_freq[i] = inv_freq[i];
+  }
+
+  const int V = dtype == TS_F32 ? 4 : 8;
+  bool vec = (a.half % V) == 0;
+  if (Hq > 0) {
+    vec = vec && ts_host::aligned16(q_in) && ts_host::aligned16(q_out) &&
+          strides_vec_ok(q_in_sb, q_in_ss, q_in_sh, V) &&
+          strides_vec_ok(q_out_sb, q_out_ss, q_out_sh, V);
+  }
+  if (Hk > 0) {
+    vec = vec && ts_host::aligned16(k_in) && ts_host::aligned16(k_out) &&
+          strides_vec_ok(k_in_sb, k_in_ss, k_in_sh, V) &&
+          strides_vec_ok(k_out_sb, k_out_ss, k_out_sh, V);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool il = interleaved != 0;
+  switch (dtype) {
+    case TS_BF16: return dispatch_tab<__bf16>(a, tab_dtype, table, il, vec, st);
+    case TS_F16: return dispatch_tab<_Float16>(a, tab_dtype, table, il, vec, st);
+    case TS_F32: return dispatch_tab<float>(a, tab_dtype, table, il, vec, st);
+  }
+  return fail(TS_ERR_UNSUPPORTED_DTYPE, "rope: bad dtype");
+}

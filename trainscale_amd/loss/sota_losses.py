@@ -1,0 +1,176 @@
+"""Drop-in counterparts of the cross-entropy classes of TrainScale's ``loss/sota_losses.py``.
+
+Reference (``data_pipeline/trainer/``):
+
+* ``FusedCrossEntropyFunction`` (loss/sota_losses.py:437-532):
+  apply(logits, labels, ignore_index, label_smoothing, reduction) -> reduced loss;
+* ``FusedCrossEntropyLoss`` (:539-617);
+* ``ChunkedCrossEntropyLoss`` (:620-744) — the trainer's configured loss on
+  ROCm (trainers/sota_trainer.py:1876-1883).
+
+All three compute the same quantity: per-row
+loss = (1-a)*(lse - x[label]) + a*(lse - mean(x)), zero on ignore_index rows,
+reduced by mean (over non-ignored rows, at least 1), sum, batchmean (over all
+rows) or none. Here every one runs the gfx950 kernels directly on the logits
+in their own dtype: one read in forward, one read plus one write in backward,
+fp32 arithmetic throughout. The reference's ChunkedCrossEntropyLoss builds an
+fp32 copy of the logits and differentiates through torch ops; its eval mode
+accumulates in the logits dtype, where this version stays in fp32.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from .. import ops
+
+__all__ = [
+    "CrossEntropyRowsFunction",
+    "FusedCrossEntropyFunction",
+    "FusedCrossEntropyLoss",
+    "ChunkedCrossEntropyLoss",
+    "reduce_rows",
+]
+
+_REDUCTIONS = ("mean", "sum", "batchmean", "none")
+
+
+class CrossEntropyRowsFunction(torch.autograd.Function):
+    """Per-row cross-entropy losses (fp32 [N]) of logits [N, V] with autograd.
+
+    backward returns a new gradient tensor in the logits dtype.
+    """
+
+    @staticmethod
+    def forward(ctx, logits: Tensor, labels: Tensor, ignore_index: int = -100,
+                label_smoothing: float = 0.0, logit_scale: float = 0.0,
+                softcap: float = 0.0) -> Tensor:
+        l2d, ld = ops.as_rows(logits)
+        loss, lse = ops.ce_forward(l2d, ld, labels, ignore_index, logit_scale, softcap,
+                                   label_smoothing)
+        ctx.save_for_backward(l2d, labels, lse)
+        ctx.ld = ld
+        ctx.cfg = (ignore_index, label_smoothing, logit_scale, softcap)
+        ctx.shape = logits.shape
+        return loss
+
+    @staticmethod
+    def backward(ctx, dloss: Tensor):
+        l2d, labels, lse = ctx.saved_tensors
+        ignore_index, label_smoothing, logit_scale, softcap = ctx.cfg
+        grad = torch.empty(l2d.shape, dtype=l2d.dtype, device=l2d.device)
+        ops.ce_backward(l2d, ctx.ld, labels, lse, dloss, grad, l2d.shape[1],
+                        ignore_index=ignore_index, logit_scale=logit_scale, softcap=softcap,
+                        label_smoothing=label_smoothing)
+        return grad.view(ctx.shape), None, None, None, None, None
+
+
+def reduce_rows(loss: Tensor, labels: Tensor, ignore_index: int, reduction: str) -> Tensor:
+    """Reduction of per-row losses as the reference's loss classes do it."""
+    if reduction == "mean":
+        valid = (labels.reshape(-1) != ignore_index).sum()
+        return loss.sum() / valid.clamp(min=1)
+    if reduction == "sum":
+        return loss.sum()
+    if reduction == "batchmean":
+        return loss.sum() / loss.shape[0] if loss.shape[0] > 0 else loss.sum()
+    return loss
+
+
+def _flatten(logits: Tensor, labels: Tensor) -> Tuple[Tensor, Tensor]:
+    if logits.dim() == 3:
+        logits = logits.reshape(-1, logits.size(-1))
+        labels = labels.reshape(-1)
+    return logits, labels
+
+
+class FusedCrossEntropyFunction(torch.autograd.Function):
+    """Reduced cross-entropy in one autograd node (reference: loss/sota_losses.py:437-532)."""
+
+    @staticmethod
+    def forward(ctx, logits: Tensor, labels: Tensor, ignore_index: int, label_smoothing: float,
+                reduction: str) -> Tensor:
+        if reduction not in _REDUCTIONS:
+            raise ValueError(f"Invalid reduction: {reduction}")
+        l2d, ld = ops.as_rows(logits)
+        loss, lse = ops.ce_forward(l2d, ld, labels, ignore_index, 0.0, 0.0, label_smoothing)
+        ctx.save_for_backward(l2d, labels, lse)
+        ctx.ld = ld
+        ctx.cfg = (ignore_index, label_smoothing, reduction)
+        return reduce_rows(loss, labels, ignore_index, reduction)
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        l2d, labels, lse = ctx.saved_tensors
+        ignore_index, label_smoothing, reduction = ctx.cfg
+        n = l2d.shape[0]
+        if reduction == "mean":
+            dloss = grad_output.float() / (labels != ignore_index).sum().clamp(min=1)
+        elif reduction == "batchmean":
+            dloss = grad_output.float() / max(n, 1)
+        else:
+            dloss = grad_output.float()
+        grad = torch.empty(l2d.shape, dtype=l2d.dtype, device=l2d.device)
+        ops.ce_backward(l2d, ctx.ld, labels, lse, dloss, grad, l2d.shape[1],
+                        ignore_index=ignore_index, label_smoothing=label_smoothing)
+        return grad, None, None, None, None
+
+
+class FusedCrossEntropyLoss(nn.Module):
+    """Cross-entropy module (reference: loss/sota_losses.py:539-617).
+
+    The reference casts the logits to fp32 before its kernel; the gfx950
+    kernel reads them in their own dtype and accumulates in fp32.
+    """
+
+    __constants__ = ["ignore_index", "label_smoothing", "reduction"]
+
+    def __init__(self, ignore_index: int = -100, label_smoothing: float = 0.0,
+                 reduction: str = "mean") -> None:
+        super().__init__()
+        if reduction not in _REDUCTIONS:
+            raise ValueError(f"Invalid reduction: {reduction}")
+        self.ignore_index = ignore_index
+        self.label_smoothing = label_smoothing
+        self.reduction = reduction
+
+    def forward(self, logits: Tensor, labels: Tensor) -> Tensor:
+        logits, labels = _flatten(logits, labels)
+        return FusedCrossEntropyFunction.apply(logits, labels, self.ignore_index,
+                                               self.label_smoothing, self.reduction)
+
+    def extra_repr(self) -> str:
+        return (f"ignore_index={self.ignore_index}, label_smoothing={self.label_smoothing}, "
+                f"reduction='{self.reduction}'")
+
+
+class ChunkedCrossEntropyLoss(nn.Module):
+    """Cross-entropy over large vocabularies (reference: loss/sota_losses.py:620-744).
+
+    ``chunk_size`` is kept for signature compatibility; the gfx950 kernel walks
+    the whole vocabulary row with an online max/sum and never materialises an
+    fp32 copy, so no chunking is needed.
+    """
+
+    __constants__ = ["ignore_index", "label_smoothing", "reduction", "chunk_size"]
+
+    def __init__(self, ignore_index: int = -100, label_smoothing: float = 0.0,
+                 reduction: str = "mean", chunk_size: int = 32768) -> None:
+        super().__init__()
+        if reduction not in _REDUCTIONS:
+            raise ValueError(f"Invalid reduction: {reduction}")
+        self.ignore_index = ignore_index
+        self.label_smoothing = label_smoothing
+        self.reduction = reduction
+        self.chunk_size = chunk_size
+
+    def forward(self, logits: Tensor, labels: Tensor) -> Tensor:
+        logits, labels = _flatten(logits, labels)
+        loss = CrossEntropyRowsFunction.apply(logits, labels, self.ignore_index,
+                                              self.label_smoothing)
+        if self.reduction == "batchmean":
+            return loss.mean()
+        return reduce_rows(loss, labels, self.ignore_index, self.reduction)

@@ -1,0 +1,79 @@
+"""RMSNorm patch boundary with TrainScale's registry API.
+
+Mirrors ``register_layer_patch``, ``LAYER_PATCHES``, ``auto_patch_layernorm``
+and the RMSNorm part of ``KernelPatcher`` (data_pipeline/trainer/registry/
+__init__.py:997-1077, :1331-1418): every module whose class name is registered
+gets its ``forward`` replaced by ``fast_rms_layernorm`` on the gfx950 kernels.
+As in the reference, the patched forward keeps calling the module's original
+forward for tensors that are not on a GPU (the module's own code, not a copy
+of the kernel math).
+"""
+from __future__ import annotations
+
+from typing import Callable, Dict, List, Tuple
+
+import torch
+import torch.nn as nn
+
+from .kernels.fused_kernels import fast_rms_layernorm
+
+__all__ = ["LAYER_PATCHES", "register_layer_patch", "auto_patch_layernorm", "KernelPatcher",
+           "patch_model"]
+
+LAYER_PATCHES: Dict[str, Callable[[nn.Module], None]] = {}
+
+
+def register_layer_patch(class_name: str, patch_fn: Callable[[nn.Module], None]) -> None:
+    """Registers `patch_fn` for modules of class `class_name` (registry/__init__.py:997-1000)."""
+    LAYER_PATCHES[class_name] = patch_fn
+
+
+def auto_patch_layernorm(module: nn.Module) -> None:
+    """Routes an RMSNorm module's forward to the gfx950 kernel (registry/__init__.py:1033-1054)."""
+    original_forward = module.forward
+    eps = getattr(module, "eps", getattr(module, "variance_epsilon", 1e-6))
+
+    def patched_forward(hidden_states):
+        weight = getattr(module, "weight", None)
+        if (not isinstance(hidden_states, torch.Tensor) or weight is None
+                or not isinstance(weight, torch.Tensor) or not hidden_states.is_cuda
+                or not weight.is_cuda):
+            return original_forward(hidden_states)
+        return fast_rms_layernorm(hidden_states, weight, eps)
+
+    module.forward = patched_forward
+    module._trainscale_amd_patched = True
+
+
+for _name in ("LlamaRMSNorm", "Qwen2RMSNorm", "Qwen3RMSNorm", "GemmaRMSNorm", "Gemma2RMSNorm",
+              "MistralRMSNorm", "Phi3RMSNorm", "Phi4RMSNorm", "YiRMSNorm", "FalconRMSNorm",
+              "FalconH1RMSNorm", "CohereLayerNorm", "GraniteRMSNorm", "StarcoderLayerNorm",
+              "DeepseekRMSNorm", "DeepseekV2RMSNorm", "MixtralRMSNorm", "DbrxLayerNorm",
+              "GrokRMSNorm", "InternVLRMSNorm"):
+    register_layer_patch(_name, auto_patch_layernorm)
+
+
+class KernelPatcher:
+    """Applies the registered layer patches to a model (registry/__init__.py:1331-1418)."""
+
+    def __init__(self, patch_layernorm: bool = True, verbose: bool = False):
+        self.patch_layernorm = patch_layernorm
+        self.verbose = verbose
+        self.patched_layers: List[Tuple[str, str]] = []
+
+    def patch(self, model: nn.Module) -> nn.Module:
+        if not self.patch_layernorm:
+            return model
+        for name, module in model.named_modules():
+            cls = module.__class__.__name__
+            fn = LAYER_PATCHES.get(cls)
+            if fn is not None and not getattr(module, "_trainscale_amd_patched", False):
+                fn(module)
+                self.patched_layers.append((name, cls))
+        if self.verbose and self.patched_layers:
+            print(f"patched {len(self.patched_layers)} layers")
+        return model
+
+
+def patch_model(model: nn.Module) -> nn.Module:
+    return KernelPatcher().patch(model)
