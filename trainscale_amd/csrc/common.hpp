@@ -1,12 +1,11 @@
 // Shared device and host helpers for the gfx950 kernels.
 //
 // Device side: 16-byte vector access with fp32 unpacking for bf16/fp16/fp32
-// elements, wave64 reductions built from DPP row operations plus the gfx950
-// permlane16/permlane32 swaps (no LDS round trip inside a wave), and
-// workgroup reductions that go through LDS once per wave.
+// elements, wave64 reductions built from DPP row operations plus lane reads
+// (no LDS round trip inside a wave), and workgroup reductions that go
+// through LDS once per wave.
 //
-// Host side: thread-local error reporting for the C ABI and a cached
-// compute-unit count per device.
+// Host side: thread-local error reporting for the C ABI.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -117,8 +116,13 @@ __device__ inline void st16_stream(T* p, const u32x4& v) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave64 reductions: DPP inside each 16-lane row, then permlane swaps across
-// rows. Every lane ends with the full result.
+// Wave64 reductions: DPP inside each 16-lane row (every lane of a row ends
+// with the row's result), then the four row results are read with
+// v_readlane_b32 and combined in a fixed order. Every lane gets the result.
+//
+// The gfx950 v_permlane16_swap/v_permlane32_swap builtins are not used: with
+// the same value passed as both operands, hipcc (ROCm 7.2) keeps only the
+// first of the two results, which turns the cross-row sum into a doubling.
 // ---------------------------------------------------------------------------
 
 template <int kCtrl>
@@ -127,43 +131,35 @@ __device__ inline float dpp_f(float v) {
       float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
 }
 
-// v_permlane16_swap / v_permlane32_swap exchange rows between their two
-// operands; passing v as both and combining both results gives every lane
-// op(own row, partner row).
-__device__ inline float wave_sum(float v) {
+__device__ inline float lane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ inline float row_sum(float v) {
   v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp_f<0x141>(v);  // row_half_mirror
   v += dpp_f<0x140>(v);  // row_mirror
-  {
-    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v),
-                                              __builtin_bit_cast(int, v), false, false);
-    v = __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-  }
-  {
-    auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v),
-                                              __builtin_bit_cast(int, v), false, false);
-    v = __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
-  }
   return v;
 }
 
-__device__ inline float wave_max(float v) {
+__device__ inline float row_max(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));
   v = fmaxf(v, dpp_f<0x4E>(v));
   v = fmaxf(v, dpp_f<0x141>(v));
   v = fmaxf(v, dpp_f<0x140>(v));
-  {
-    auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v),
-                                              __builtin_bit_cast(int, v), false, false);
-    v = fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
-  }
-  {
-    auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v),
-                                              __builtin_bit_cast(int, v), false, false);
-    v = fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
-  }
   return v;
+}
+
+// Requires all 64 lanes active.
+__device__ inline float wave_sum(float v) {
+  v = row_sum(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+
+__device__ inline float wave_max(float v) {
+  v = row_max(v);
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Sum over a workgroup of kWaves waves; `lds` holds kWaves floats. All
@@ -197,8 +193,6 @@ namespace ts_host {
 ts_status fail(ts_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Turns a launch error into TS_ERR_LAUNCH with the kernel name attached.
 ts_status check_launch(const char* kernel);
-// Number of compute units of the current device (cached per device).
-int cu_count();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline size_t dtype_size(ts_dtype t) { return t == TS_F32 ? 4 : 2; }

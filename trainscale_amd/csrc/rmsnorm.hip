@@ -6,8 +6,8 @@
 // of squares with DPP, and writes y from the same registers: x is read from
 // HBM exactly once. Four rows per 256-thread workgroup.
 //
-// Backward (register path): 8 waves per workgroup, one workgroup per compute
-// unit (grid capped at the CU count). Each wave walks rows with a grid stride:
+// Backward (register path): 8 waves per workgroup, at most kBwdMaxGrid
+// workgroups (plan.hpp). Each wave walks rows with a grid stride:
 // per row it reads dy and x once, reduces sum(dy*w*xhat) with DPP, writes dx,
 // and accumulates dy*xhat for dW in fp32 registers. At the end the 8 waves
 // fold their accumulators through LDS in a fixed order and the workgroup
@@ -19,10 +19,13 @@
 // pointers, or rows too long for registers): one workgroup per row with
 // element-wise loads and two passes over the row.
 #include "common.hpp"
+#include "plan.hpp"
 
 namespace {
 
 using namespace ts;
+using ts_plan::kBwdWaves;
+using ts_plan::kFwdWaves;
 
 // Loads kVec weights for the 16-byte data vector starting at element e.
 template <typename W, int kVec>
@@ -35,9 +38,6 @@ __device__ inline void load_w(const W* __restrict__ w, int64_t e, float* f) {
     Elt<W>::unpack(ld16(w + e), f);
   }
 }
-
-constexpr int kFwdWaves = 4;
-constexpr int kBwdWaves = 8;
 
 // ---------------------------------------------------------------------------
 // Forward, register path.
@@ -226,6 +226,13 @@ __global__ __launch_bounds__(kBwdWaves* kWave) void rms_bwd_reg(
   }
 }
 
+// Clears n bytes (a kernel rather than hipMemsetAsync, so a captured graph
+// replays it like any other node).
+__global__ __launch_bounds__(256) void zero_bytes(uint8_t* __restrict__ p, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 // dW[c] = sum over partial rows in a fixed order. 64 columns per workgroup,
 // 4 row-groups per column combined in a fixed order through LDS.
 template <typename W>
@@ -326,17 +333,9 @@ __global__ __launch_bounds__(256) void rms_bwd_dw_generic(
 }
 
 // ---------------------------------------------------------------------------
-// Host dispatch
+// Host dispatch. Grid sizes and the number of dW partial rows come from
+// ts_plan (plan.hpp), the same functions the workspace-size query uses.
 // ---------------------------------------------------------------------------
-constexpr int kMaxVecPerLane = 16;
-constexpr int kMaxBwdVec = 8;
-
-int pick_maxv(int64_t nvec) {
-  for (int m = 1; m <= kMaxVecPerLane; m *= 2)
-    if (nvec <= (int64_t)m * kWave) return m;
-  return 0;
-}
-
 template <typename T, typename W>
 bool vec_ok(const void* a, int64_t lda, int64_t cols, const void* w) {
   constexpr int V = sizeof(T) == 4 ? 4 : 8;
@@ -353,7 +352,7 @@ ts_status fwd_typed(const void* x, int64_t ldx, const void* w, void* y, int64_t 
   const W* wp = static_cast<const W*>(w);
   T* yp = static_cast<T*>(y);
   const int64_t nvec = cols / V;
-  const int maxv = pick_maxv(nvec);
+  const int maxv = ts_plan::rms_fwd_maxv(nvec);
   if (vec_ok<T, W>(x, ldx, cols, w) && vec_ok<T, W>(y, ldy, cols, nullptr) && maxv > 0) {
     const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
     const dim3 block(kFwdWaves * kWave);
@@ -368,6 +367,8 @@ ts_status fwd_typed(const void* x, int64_t ldx, const void* w, void* y, int64_t 
       TS_LAUNCH_FWD(4)
       TS_LAUNCH_FWD(8)
       TS_LAUNCH_FWD(16)
+      default:
+        return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_fwd: bad plan (maxv=%d)", maxv);
     }
 #undef TS_LAUNCH_FWD
     return ts_host::check_launch("rms_fwd_reg");
@@ -377,44 +378,33 @@ ts_status fwd_typed(const void* x, int64_t ldx, const void* w, void* y, int64_t 
   return ts_host::check_launch("rms_fwd_generic");
 }
 
-// Workgroups of the register-path backward: one per row-step, capped at the
-// CU count (each workgroup writes one dW partial row).
-int64_t bwd_reg_grid(int64_t rows, int split) {
-  const int64_t per_step = kBwdWaves / split;
-  const int64_t want = (rows + per_step - 1) / per_step;
-  const int64_t cap = ts_host::cu_count();
-  return want < cap ? want : cap;
-}
-
-constexpr int64_t kGenericRowsPerGroup = 64;
-
 template <typename T, typename W>
 ts_status bwd_typed(const void* dy, int64_t lddy, const void* x, int64_t ldx, const void* w,
                     const float* rstd, void* dx, int64_t lddx, void* dw, float* ws,
-                    int64_t rows, int64_t cols, hipStream_t st) {
+                    size_t ws_bytes, int64_t rows, int64_t cols, hipStream_t st) {
   constexpr int V = sizeof(T) == 4 ? 4 : 8;
   const T* dyp = static_cast<const T*>(dy);
   const T* xp = static_cast<const T*>(x);
   const W* wp = static_cast<const W*>(w);
   T* dxp = static_cast<T*>(dx);
   const int64_t nvec = cols / V;
-  // Up to 8 vectors per lane; longer rows are split across 2 or 4 waves.
-  int split = 1;
-  while (split <= 4 && nvec > (int64_t)kWave * kMaxBwdVec * split) split *= 2;
-  const int maxv = split == 1 ? pick_maxv(nvec) : kMaxBwdVec;
-  int64_t nparts = 0;
-  // The dW fold stages one fp32 row in LDS; keep it within 64 KiB.
-  const bool lds_ok = dw == nullptr || cols * (int64_t)sizeof(float) <= 65536 - 1024;
-  if (split <= 4 && lds_ok && maxv > 0 && maxv <= kMaxBwdVec && vec_ok<T, W>(x, ldx, cols, w) &&
-      vec_ok<T, W>(dy, lddy, cols, nullptr) && vec_ok<T, W>(dx, lddx, cols, nullptr)) {
-    const int64_t grid = bwd_reg_grid(rows, split);
+  const bool vec = vec_ok<T, W>(x, ldx, cols, w) && vec_ok<T, W>(dy, lddy, cols, nullptr) &&
+                   vec_ok<T, W>(dx, lddx, cols, nullptr);
+  const ts_plan::RmsBwdPlan plan =
+      ts_plan::rms_bwd_plan(rows, cols, (int)sizeof(T), vec, dw != nullptr);
+  if (dw != nullptr && (size_t)plan.nparts * (size_t)cols * sizeof(float) > ws_bytes)
+    return ts_host::fail(TS_ERR_WORKSPACE, "rmsnorm_bwd: plan needs %lld partial rows",
+                         (long long)plan.nparts);
+  if (plan.reg) {
     const size_t lds = dw != nullptr ? (size_t)cols * sizeof(float) : 0;
     float* part = dw != nullptr ? ws : nullptr;
+    bool launched = false;
 #define TS_LAUNCH_BWD(M, SP)                                                                    \
-  if (maxv == M && split == SP) {                                                               \
-    hipLaunchKernelGGL((rms_bwd_reg<T, W, M, SP>), dim3((unsigned)grid),                        \
+  if (plan.maxv == M && plan.split == SP) {                                                     \
+    hipLaunchKernelGGL((rms_bwd_reg<T, W, M, SP>), dim3((unsigned)plan.grid),                   \
                        dim3(kBwdWaves * kWave), lds, st, dyp, lddy, xp, ldx, wp, rstd, dxp,     \
                        lddx, part, rows, (int)nvec, (float)cols);                               \
+    launched = true;                                                                            \
   }
     TS_LAUNCH_BWD(1, 1)
     TS_LAUNCH_BWD(2, 1)
@@ -423,37 +413,31 @@ ts_status bwd_typed(const void* dy, int64_t lddy, const void* x, int64_t ldx, co
     TS_LAUNCH_BWD(8, 2)
     TS_LAUNCH_BWD(8, 4)
 #undef TS_LAUNCH_BWD
+    if (!launched)
+      return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: bad plan (maxv=%d split=%d)",
+                           plan.maxv, plan.split);
     ts_status s = ts_host::check_launch("rms_bwd_reg");
     if (s != TS_OK) return s;
-    nparts = grid;
   } else {
     hipLaunchKernelGGL((rms_bwd_dx_generic<T, W>), dim3((unsigned)rows), dim3(256), 0, st, dyp,
                        lddy, xp, ldx, wp, rstd, dxp, lddx, cols);
     ts_status s = ts_host::check_launch("rms_bwd_dx_generic");
     if (s != TS_OK) return s;
     if (dw != nullptr) {
-      nparts = (rows + kGenericRowsPerGroup - 1) / kGenericRowsPerGroup;
       hipLaunchKernelGGL((rms_bwd_dw_generic<T>), dim3((unsigned)((cols + 255) / 256),
-                                                       (unsigned)nparts),
+                                                       (unsigned)plan.nparts),
                          dim3(256), 0, st, dyp, lddy, xp, ldx, rstd, ws, rows, cols,
-                         kGenericRowsPerGroup);
+                         ts_plan::kGenericRowsPerGroup);
       s = ts_host::check_launch("rms_bwd_dw_generic");
       if (s != TS_OK) return s;
     }
   }
   if (dw != nullptr) {
     hipLaunchKernelGGL((rms_dw_reduce<W>), dim3((unsigned)((cols + 63) / 64)), dim3(256), 0, st,
-                       ws, nparts, cols, static_cast<W*>(dw));
+                       ws, plan.nparts, cols, static_cast<W*>(dw));
     return ts_host::check_launch("rms_dw_reduce");
   }
   return TS_OK;
-}
-
-// Number of partial rows either backward path produces (upper bound).
-int64_t bwd_partial_rows(int64_t rows) {
-  const int64_t reg = bwd_reg_grid(rows, 1);
-  const int64_t gen = (rows + kGenericRowsPerGroup - 1) / kGenericRowsPerGroup;
-  return reg > gen ? reg : gen;
 }
 
 ts_status check_common(const void* x, int64_t ldx, ts_dtype x_dtype, const void* w,
@@ -514,8 +498,8 @@ extern "C" ts_status ts_rmsnorm_fwd(const void* x, int64_t ldx, ts_dtype x_dtype
 }
 
 extern "C" size_t ts_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols) {
-  if (rows <= 0 || cols <= 0) return 0;
-  return (size_t)bwd_partial_rows(rows) * (size_t)cols * sizeof(float);
+  return (size_t)ts_plan::rms_bwd_workspace_rows(rows, cols) * (size_t)(cols > 0 ? cols : 0) *
+         sizeof(float);
 }
 
 extern "C" ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx,
@@ -543,28 +527,26 @@ extern "C" ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy, const void* x,
   if (rows == 0) {
     // Empty batch: dW is all zeros.
     if (dw != nullptr) {
-      if (hipMemsetAsync(dw, 0, (size_t)cols * ts_host::dtype_size(w_dtype), st) != hipSuccess)
-        return fail(TS_ERR_LAUNCH, "rmsnorm_bwd: memset of dw failed");
+      const size_t nbytes = (size_t)cols * ts_host::dtype_size(w_dtype);
+      hipLaunchKernelGGL(zero_bytes, dim3((unsigned)((nbytes + 255) / 256)), dim3(256), 0, st,
+                         static_cast<uint8_t*>(dw), nbytes);
+      return ts_host::check_launch("zero_bytes");
     }
     return TS_OK;
   }
   float* ws = static_cast<float*>(workspace);
+  const size_t wsb = workspace == nullptr ? 0 : workspace_bytes;
+  const bool w32 = w != nullptr && w_dtype == TS_F32;
+#define TS_BWD_ARGS dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, wsb, rows, cols, st
   switch (x_dtype) {
     case TS_BF16:
-      return w != nullptr && w_dtype == TS_F32
-                 ? bwd_typed<__bf16, float>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows,
-                                            cols, st)
-                 : bwd_typed<__bf16, __bf16>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows,
-                                             cols, st);
+      return w32 ? bwd_typed<__bf16, float>(TS_BWD_ARGS) : bwd_typed<__bf16, __bf16>(TS_BWD_ARGS);
     case TS_F16:
-      return w != nullptr && w_dtype == TS_F32
-                 ? bwd_typed<_Float16, float>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows,
-                                              cols, st)
-                 : bwd_typed<_Float16, _Float16>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws,
-                                                 rows, cols, st);
+      return w32 ? bwd_typed<_Float16, float>(TS_BWD_ARGS)
+                 : bwd_typed<_Float16, _Float16>(TS_BWD_ARGS);
     case TS_F32:
-      return bwd_typed<float, float>(dy, lddy, x, ldx, w, rstd, dx, lddx, dw, ws, rows, cols,
-                                     st);
+      return bwd_typed<float, float>(TS_BWD_ARGS);
   }
+#undef TS_BWD_ARGS
   return fail(TS_ERR_UNSUPPORTED_DTYPE, "rmsnorm_bwd: unsupported dtype");
 }

@@ -17,6 +17,7 @@
 #include <math.h>
 
 #include "common.hpp"
+#include "plan.hpp"
 
 namespace {
 
@@ -47,13 +48,16 @@ struct RopeArgs {
   int32_t backward;
   int32_t tasks_per_head;    // 16-byte tasks per head (vector path) or pairs per head
   int32_t tasks_per_token;   // tasks_per_head * (Hq + Hk)
-  uint32_t tpt_magic;        // ceil(2^32 / tasks_per_token)
-  uint32_t tph_magic;        // ceil(2^32 / tasks_per_head)
+  uint32_t tpt_magic;        // ts_plan::magic_for(tasks_per_token)
+  uint32_t tph_magic;        // ts_plan::magic_for(tasks_per_head)
   float inv_freq[kMaxHalf];
 };
 
-// Exact quotient for n < 2^16 and d < 2^16 (magic = ceil(2^32 / d)).
-__device__ inline uint32_t fast_div(uint32_t n, uint32_t magic) { return __umulhi(n, magic); }
+// n / d as umulhi(n, ceil(2^32 / d)), magic 0 meaning d == 1 (ts_plan::magic_for);
+// exact while n * d < 2^32, which the host checks for every launch.
+__device__ inline uint32_t fast_div(uint32_t n, uint32_t magic) {
+  return magic == 0 ? n : __umulhi(n, magic);
+}
 
 template <typename TabT>
 __device__ inline float tab_load(const void* p, int64_t idx) {
@@ -199,18 +203,20 @@ __global__ __launch_bounds__(kThreads) void rope_generic_kernel(const RopeArgs a
   }
 }
 
-uint32_t magic_for(uint32_t d) {
-  return (uint32_t)((((uint64_t)1 << 32) + d - 1) / d);
-}
-
 template <typename T, typename TabT, bool kTable, bool kInterleaved>
 ts_status launch_typed(RopeArgs& a, bool vec, hipStream_t st) {
   constexpr int V = sizeof(T) == 4 ? 4 : 8;
   const int ntask_head = vec ? (kInterleaved ? 2 * a.half / V : a.half / V) : a.half;
   a.tasks_per_head = ntask_head;
   a.tasks_per_token = ntask_head * (a.Hq + a.Hk);
-  a.tpt_magic = magic_for((uint32_t)a.tasks_per_token);
-  a.tph_magic = magic_for((uint32_t)a.tasks_per_head);
+  // Task indices stay below kTok * tasks_per_token; both divisions must be exact.
+  if (!ts_plan::magic_exact((uint64_t)kTok * a.tasks_per_token, (uint64_t)a.tasks_per_token) ||
+      !ts_plan::magic_exact((uint64_t)a.tasks_per_token, (uint64_t)a.tasks_per_head))
+    return ts_host::fail(TS_ERR_SHAPE,
+                         "rope: %d heads x %d tasks per head exceed the kernel's index range",
+                         a.Hq + a.Hk, a.tasks_per_head);
+  a.tpt_magic = ts_plan::magic_for((uint32_t)a.tasks_per_token);
+  a.tph_magic = ts_plan::magic_for((uint32_t)a.tasks_per_head);
   const dim3 grid((unsigned)((a.ntok + kTok - 1) / kTok));
   const size_t lds = 2 * sizeof(float) * kTok * a.half;
   if (vec) {

@@ -25,21 +25,6 @@ ts_status check_launch(const char* kernel) {
   return TS_OK;
 }
 
-int cu_count() {
-  constexpr int kMaxDevices = 64;
-  static int cached[kMaxDevices] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
-  if (dev < kMaxDevices && cached[dev] > 0) return cached[dev];
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n <= 0) {
-    n = 256;
-  }
-  if (dev < kMaxDevices) cached[dev] = n;
-  return n;
-}
-
 }  // namespace ts_host
 
 extern "C" const char* ts_last_error(void) { return ts_host::g_last_error; }
