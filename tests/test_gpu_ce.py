@@ -64,11 +64,15 @@ def test_c3_full(gpu):
     ref_g = oracle.ce_bwd(logits[sample].cpu(), lab_cpu[sample], torch.tensor(1.0 / n_valid))
     assert_ulp(grad[sample], ref_g, 1, tiny=TINY, what="grad")
     assert (grad[sample].float().cpu() - ref_g.float()).abs().max() <= 2e-2
-    # full-size properties: ignored rows are zero, valid rows sum to ~0
+    # full-size properties: ignored rows are zero; a valid row's exact gradient
+    # sums to 0, so its bf16-rounded sum is bounded by the rounding error of
+    # each element (half an ulp, <= 2^-9 relative): |sum g| <= 2^-8 * sum |g|
     ign = labels == -100
     assert torch.count_nonzero(grad[ign]) == 0
-    rs = grad[~ign].float().sum(-1)
-    assert rs.abs().max().item() <= 1e-3 / n_valid
+    gv = grad[~ign].float()
+    rs = gv.sum(-1).abs()
+    bound = gv.abs().sum(-1) * 2.0 ** -8
+    assert bool((rs <= bound).all()), float((rs / bound).max())
 
 
 def test_fast_ce_backward_is_in_place(gpu):
@@ -124,7 +128,11 @@ def test_modules_and_reductions(gpu):
                 out.sum().backward()
                 scale = {"mean": 1.0 / n_valid, "sum": 1.0, "none": 1.0, "batchmean": 1.0 / N}[red]
                 ref_g = oracle.ce_bwd(logits.cpu(), lab, torch.tensor(scale), label_smoothing=a)
-                assert_ulp(x.grad, ref_g, 1, tiny=TINY, what=f"{type(mod).__name__} {red} {a}")
+                # With smoothing a non-label gradient is dloss*(p - a/V): where p is
+                # close to a/V both fp32 computations cancel, so the floor is 32 fp32
+                # ulps of the dloss*a/V term rather than an ulp of the tiny result.
+                tiny = max(TINY, 32 * 2.0 ** -24 * scale * a / V)
+                assert_ulp(x.grad, ref_g, 1, tiny=tiny, what=f"{type(mod).__name__} {red} {a}")
         if True:
             ce = CrossEntropyLoss(label_smoothing=a)
             out = ce(logits, labels)

@@ -2,7 +2,9 @@
 
 Bar: forward and backward outputs within 1 bf16 ulp of the oracle, for table
 mode (bit-for-bit the reference's cos/sin tables) and in-register mode
-(sin/cos evaluated on the GPU from the same fp32 angle).
+(sin/cos evaluated on the GPU from the same fp32 angle). Where the two products
+of a rotation nearly cancel, the bar is 4 fp32 ulps of the products' size
+(assert_rope); the golden vectors are held to 1 ulp without that floor.
 """
 import numpy as np
 import pytest
@@ -47,6 +49,38 @@ def oracle_pair(x, cos, sin, pos, il=False, backward=False):
     return oracle.rope_apply(x, cos, sin, pos, interleaved=il, backward=backward)
 
 
+def term_mag(x, cos, sin, pos, il=False):
+    """|x1*c| + |x2*s| for every output element: the size of the two products a
+    rotated element is the sum (or difference) of."""
+    x = x.detach().cpu().float()
+    h = x.shape[-1] // 2
+    c = cos.float().cpu()[pos][:, :, None, :h].abs()
+    s = sin.float().cpu()[pos][:, :, None, :h].abs()
+    a, b = (x[..., 0::2], x[..., 1::2]) if il else (x[..., :h], x[..., h:])
+    m1 = a.abs() * c + b.abs() * s
+    m2 = b.abs() * c + a.abs() * s
+    return torch.stack([m1, m2], -1).flatten(-2) if il else torch.cat([m1, m2], -1)
+
+
+def assert_rope(actual, x, cos, sin, pos, il=False, backward=False, what=""):
+    """Within 1 ulp of the oracle, or within 4 fp32 ulps of the products' size:
+    where x1*c and x2*s nearly cancel, fused (GPU) and separately rounded (CPU)
+    products differ by an fp32 ulp of the terms, many ulps of the tiny result."""
+    ref = oracle_pair(x, cos, sin, pos, il, backward)
+    a = actual.detach().cpu()
+    d = (a.float() - ref.float()).abs()
+    ok_abs = d <= 4 * 2.0 ** -24 * term_mag(x, cos, sin, pos, il)
+    if a.dtype == torch.float32:
+        ok = (d <= 2.0 ** -22 * ref.abs()) | ok_abs
+    else:
+        from helpers import ulp_diff
+        ok = (ulp_diff(a, ref.to(a.dtype)) <= 1) | ok_abs
+    if not bool(ok.all()):
+        idx = (~ok).nonzero()[0].tolist()
+        raise AssertionError(f"{what}: {int((~ok).sum())} elements off; first at {idx}: "
+                             f"{a[tuple(idx)].item()!r} vs {ref[tuple(idx)].item()!r}")
+
+
 def test_c2_full_fast_rope(gpu):
     wl = workloads.rope_workload(gpu)
     q, k, dq, dk = (wl.tensors[n] for n in ("q", "k", "dq", "dk"))
@@ -57,10 +91,10 @@ def test_c2_full_fast_rope(gpu):
     torch.autograd.backward([qo, ko], [dq, dk])
     pos = oracle.rope_positions(B, S)
     c, s = cos.cpu(), sin.cpu()
-    assert_ulp(qo, oracle_pair(q, c, s, pos), 1, what="q")
-    assert_ulp(ko, oracle_pair(k, c, s, pos), 1, what="k")
-    assert_ulp(qg.grad, oracle_pair(dq, c, s, pos, backward=True), 1, what="dq")
-    assert_ulp(kg.grad, oracle_pair(dk, c, s, pos, backward=True), 1, what="dk")
+    assert_rope(qo, q, c, s, pos, what="q")
+    assert_rope(ko, k, c, s, pos, what="k")
+    assert_rope(qg.grad, dq, c, s, pos, backward=True, what="dq")
+    assert_rope(kg.grad, dk, c, s, pos, backward=True, what="dk")
 
 
 def test_c2_full_in_register(gpu):
@@ -69,7 +103,7 @@ def test_c2_full_in_register(gpu):
     B, S, _, D = q.shape
     y = apply_rope_theta(q, wl.params["theta"], inplace=False)
     cos, sin = oracle.rope_tables(D, S, wl.params["theta"])
-    assert_ulp(y, oracle_pair(q, cos, sin, oracle.rope_positions(B, S)), 1)
+    assert_rope(y, q, cos, sin, oracle.rope_positions(B, S))
 
 
 @pytest.mark.parametrize("mode", ["table", "theta"])
@@ -84,8 +118,7 @@ def test_c4_packed_position_ids(gpu, mode):
             y = apply_rope(x, cos.to(gpu), sin.to(gpu), position_ids=pos, inplace=False)
         else:
             y = apply_rope_theta(x, theta, position_ids=pos, inplace=False)
-        ref = oracle_pair(x, cos, sin, oracle.rope_positions(1, x.shape[1], pos))
-        assert_ulp(y, ref, 1, what=mode)
+        assert_rope(y, x, cos, sin, oracle.rope_positions(1, x.shape[1], pos), what=mode)
     # packed == per document, on the GPU, bit for bit
     y = apply_rope(q, cos.to(gpu), sin.to(gpu), position_ids=pos, inplace=False)
     start = 0
@@ -105,11 +138,7 @@ def test_layouts_and_dtypes(gpu, D, il, dtype):
     x = torch.randn(B, S, H, D, device=gpu).to(dtype)
     cos, sin = oracle.rope_tables(D, 64, 10000.0)
     y = apply_rope(x, cos.to(gpu), sin.to(gpu), position_offset=5, interleaved=il, inplace=False)
-    ref = oracle_pair(x, cos, sin, oracle.rope_positions(B, S, position_offset=5), il)
-    if dtype == torch.float32:
-        torch.testing.assert_close(y.cpu(), ref, rtol=1e-6, atol=1e-6)
-    else:
-        assert_ulp(y, ref, 1)
+    assert_rope(y, x, cos, sin, oracle.rope_positions(B, S, position_offset=5), il)
 
 
 def test_bf16_tables_rotary_embedding(gpu):
@@ -121,11 +150,11 @@ def test_bf16_tables_rotary_embedding(gpu):
     assert y.data_ptr() == x.data_ptr()
     c, s = rot.cos_cached.cpu(), rot.sin_cached.cpu()
     assert c.dtype == BF
-    assert_ulp(y, oracle_pair(x0, c, s, oracle.rope_positions(2, 300)), 1)
+    assert_rope(y, x0, c, s, oracle.rope_positions(2, 300))
     rot_r = RotaryEmbedding(128, max_seq_len=512, base=500000.0, in_register=True)
     y2 = rot_r(x0.clone())
     cos, sin = oracle.rope_tables(128, 512, 500000.0)
-    assert_ulp(y2, oracle_pair(x0, cos, sin, oracle.rope_positions(2, 300)), 1)
+    assert_rope(y2, x0, cos, sin, oracle.rope_positions(2, 300))
 
 
 def test_inplace_qk_and_offset(gpu):
@@ -137,14 +166,14 @@ def test_inplace_qk_and_offset(gpu):
     qo, ko = apply_rope_qk(q, k, cos.to(gpu), sin.to(gpu), position_offset=7)
     assert qo.data_ptr() == q.data_ptr() and ko.data_ptr() == k.data_ptr()
     pos = oracle.rope_positions(2, 16, position_offset=7)
-    assert_ulp(qo, oracle_pair(q0, cos, sin, pos), 1)
-    assert_ulp(ko, oracle_pair(k0, cos, sin, pos), 1)
+    assert_rope(qo, q0, cos, sin, pos)
+    assert_rope(ko, k0, cos, sin, pos)
     q1, k1 = q0.clone(), k0.clone()
     inplace_rope_embedding(q1, k1, cos.to(gpu)[None, None], sin.to(gpu)[None, None], 7)
     assert torch.equal(q1, qo) and torch.equal(k1, ko)
     q2 = q0.clone()
     fast_rope_embedding(q2, cos.to(gpu)[:16], sin.to(gpu)[:16])
-    assert_ulp(q2, oracle_pair(q0, cos, sin, oracle.rope_positions(2, 16)), 1)
+    assert_rope(q2, q0, cos, sin, oracle.rope_positions(2, 16))
 
 
 def test_strided_qkv_view(gpu):
@@ -154,7 +183,7 @@ def test_strided_qkv_view(gpu):
     q = qkv[:, :, 0]  # non-contiguous [B,S,H,D] view with unit last stride
     cos, sin = oracle.rope_tables(D, S, 10000.0)
     y = apply_rope(q, cos.to(gpu), sin.to(gpu), inplace=False)
-    assert_ulp(y, oracle_pair(q.contiguous(), cos, sin, oracle.rope_positions(B, S)), 1)
+    assert_rope(y, q.contiguous(), cos, sin, oracle.rope_positions(B, S))
 
 
 def test_out_of_range_positions_give_nan(gpu):

@@ -28,6 +28,11 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 // Elements per 16-byte vector and conversions to/from fp32. The bf16 store
 // path lowers to v_cvt_pk_bf16_f32 (round to nearest even, like torch).
+//
+// Note on vector elements: never pass an element of an ext_vector_type
+// (v[i]) directly as the operand of __builtin_bit_cast. hipcc (ROCm 7.2)
+// compiles that as a read of element 0 whatever i is; copy the element into
+// a scalar first.
 template <typename T> struct Elt;
 
 template <> struct Elt<__bf16> {
@@ -60,7 +65,8 @@ template <> struct Elt<_Float16> {
   __device__ static inline void unpack(const u32x4& v, float* f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f16x2_t h = __builtin_bit_cast(f16x2_t, v[i]);
+      const uint32_t u = v[i];  // see the note on vector elements above
+      f16x2_t h = __builtin_bit_cast(f16x2_t, u);
       f[2 * i] = (float)h[0];
       f[2 * i + 1] = (float)h[1];
     }
@@ -83,7 +89,10 @@ template <> struct Elt<float> {
   static constexpr int kVec = 4;
   __device__ static inline void unpack(const u32x4& v, float* f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t u = v[i];  // see the note on vector elements above
+      f[i] = __builtin_bit_cast(float, u);
+    }
   }
   __device__ static inline u32x4 pack(const float* f) {
     u32x4 v;
