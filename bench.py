@@ -40,6 +40,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="approximate CPU time budget of the baseline sample")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="before warm-up, copy a 1 GiB buffer 3 times (a plain copy of known "
+                        "size, the reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -145,6 +148,14 @@ def main():
     grad = torch.empty_like(logits)
     dloss = torch.full((1,), 1.0 / n_valid, device=dev)
     torch.cuda.synchronize()
+
+    if args.copy_probe:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     bytes_c1 = W.rmsnorm_bytes(x2d.shape[0], x2d.shape[1])
     bytes_c2 = W.rope_bytes(q.shape[0] * q.shape[1], q.shape[2] + k.shape[2], 128)

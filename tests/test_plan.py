@@ -9,6 +9,8 @@ indices. A small C++ driver compiled with g++ sweeps many shapes and checks:
   for the unsplit launch);
 * register plans cover every 16-byte vector of the row and stay within the
   template instantiations the launcher has;
+* RoPE workgroups are whole waves within 256..1024 threads and their cos/sin
+  staging fits the LDS bound;
 * umulhi(n, ceil(2^32/d)) == n / d wherever magic_exact(n_max, d) admits it,
   including d == 1 (regression: ceil(2^32/1) once truncated to 0, sending every
   RoPE task of a one-task-per-head shape to head 0 and past the tensor).
@@ -55,25 +57,45 @@ int main() {
             if (!dw) CHECK(p.nparts == 0, "nparts without dW");
             if (p.reg) {
               const long long nvec = cols / V;
+              const RmsRowPlan& r = p.row;
               CHECK(cols % V == 0 && vec, "reg path for unaligned row");
-              CHECK((long long)p.maxv * kWave * p.split >= nvec,
-                    "rows=%lld cols=%lld: reg plan covers %lld of %lld vectors", rows, cols,
-                    (long long)p.maxv * kWave * p.split, nvec);
-              const bool inst = (p.split == 1 && (p.maxv == 1 || p.maxv == 2 || p.maxv == 4 ||
-                                                  p.maxv == 8)) ||
-                                (p.maxv == 8 && (p.split == 2 || p.split == 4));
-              CHECK(inst, "no instantiation for maxv=%d split=%d", p.maxv, p.split);
-              CHECK(p.grid >= (rows > 0 ? 1 : 0) && p.grid <= kBwdMaxGrid, "grid %lld", (long long)p.grid);
-              CHECK(rows == 0 || p.grid * (kBwdWaves / p.split) <= rows + kBwdWaves,
-                    "grid larger than the rows need");
-              if (dw) CHECK(cols * 4 <= kBwdLdsLimit, "LDS fold row too long");
+              CHECK((long long)r.tpr * r.kv >= nvec, "rows=%lld cols=%lld: plan covers %d of %lld vectors",
+                    rows, cols, r.tpr * r.kv, nvec);
+              const bool inst = (r.kv == 1 && (r.tpr == 64 || r.tpr == 128 || r.tpr == 256 ||
+                                                r.tpr == 512)) ||
+                                (r.tpr == 512 && (r.kv == 2 || r.kv == 4));
+              CHECK(inst, "no bwd instantiation for tpr=%d kv=%d", r.tpr, r.kv);
+              CHECK(r.block == 512 && r.rpb * r.tpr == 512, "bwd block shape");
+              CHECK(p.steps >= 1 && p.grid >= (rows > 0 ? 1 : 0), "grid %lld steps %lld",
+                    (long long)p.grid, (long long)p.steps);
+              // every row is covered by exactly one (workgroup, step, slot)
+              CHECK(p.grid * p.steps * r.rpb >= rows, "rows=%lld not covered", rows);
+              CHECK(rows == 0 || (p.grid - 1) * p.steps * r.rpb < rows, "empty workgroup");
+              CHECK(p.grid < (1ll << 31), "grid too large");
+              if (dw) CHECK(p.nparts == p.grid * r.rpb, "nparts != grid * rpb");
             }
           }
         }
         const long long nvec = cols / V;
-        const int m = rms_fwd_maxv(nvec);
-        if (m) CHECK((long long)m * kWave >= nvec && m <= kFwdMaxVec, "fwd maxv %d for %lld", m, nvec);
+        RmsRowPlan f = rms_fwd_plan(nvec);
+        if (f.reg) {
+          CHECK((long long)f.tpr * f.kv >= nvec, "fwd plan covers %d of %lld", f.tpr * f.kv, nvec);
+          const bool inst = (f.tpr == 64 && (f.kv == 1 || f.kv == 2)) || (f.tpr == 128 && f.kv == 2) ||
+                            (f.tpr == 256 && f.kv == 2) || (f.tpr == 512 && (f.kv == 2 || f.kv == 4));
+          CHECK(inst, "no fwd instantiation for tpr=%d kv=%d", f.tpr, f.kv);
+          CHECK(f.block == (f.tpr > 256 ? f.tpr : 256) && f.rpb * f.tpr == f.block, "fwd block shape");
+        }
       }
+    }
+  }
+  // RoPE workgroup shapes
+  for (long long tpt = 1; tpt <= 40000; tpt += (tpt < 600 ? 1 : 37)) {
+    for (int half : {1, 2, 8, 10, 32, 64, 128, 256}) {
+      RopeBlock b = rope_block(tpt, half, 1024, 4096);
+      CHECK(b.tpb >= 1 && (long long)b.tpb * half <= 4096, "rope tpb %d half %d", b.tpb, half);
+      CHECK(b.threads % 64 == 0 && b.threads >= 256 && b.threads <= 1024, "rope threads %d", b.threads);
+      if (tpt >= 256) CHECK(b.tpb == 1, "rope tpb %d for %lld tasks", b.tpb, tpt);
+      else CHECK((long long)b.tpb * tpt <= 256 || b.tpb == 1, "rope over-filled block");
     }
   }
   // magic-number division
@@ -110,14 +132,12 @@ def test_plan_bounds(driver):
     assert proc.returncode == 0, proc.stdout + proc.stderr
 
 
-def test_workspace_query_matches_split_launches():
+def test_workspace_query_covers_every_partial_row():
     lib = _lib.load()
-    # shapes whose backward splits a row over 2 or 4 waves with few rows: the
-    # case the old sizing got wrong
-    for rows, cols in [(37, 8192), (37, 12288), (5, 8192), (129, 12288), (1, 8192)]:
-        per_step = {8192: 4, 12288: 2}[cols]  # rows per workgroup step for bf16
-        need_rows = -(-rows // per_step)
+    # one partial row per row slot of every backward workgroup: rows small
+    # enough that each row group gets its own workgroup
+    for rows, cols in [(37, 8192), (37, 12288), (5, 8192), (129, 12288), (1, 8192), (300, 512)]:
         got = lib.ts_rmsnorm_bwd_workspace_size(rows, cols)
-        assert got >= need_rows * cols * 4, (rows, cols, got, need_rows)
+        assert got >= rows * cols * 4 or got >= 512 * cols * 4, (rows, cols, got)
     assert lib.ts_rmsnorm_bwd_workspace_size(0, 4096) == 0
     assert lib.ts_rmsnorm_bwd_workspace_size(16, 0) == 0

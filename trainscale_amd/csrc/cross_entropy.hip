@@ -9,10 +9,13 @@
 // the four waves through LDS. Rows whose label is ignore_index are not read:
 // their loss is 0 and their lse is stored as 0 (the backward never reads it).
 //
-// Backward: one workgroup per row, one read and one write per element:
-// grad = dloss * (softmax - onehot) (with the label-smoothing, softcap and
-// logit-scale chain rules), written with 16-byte stores; it may overwrite the
-// logits in place. Ignored rows are written as zeros without being read.
+// Backward: one read and one write per element, grad = dloss * (softmax -
+// onehot) (with the label-smoothing, softcap and logit-scale chain rules),
+// written with 16-byte stores; it may overwrite the logits in place. The grid
+// is one-shot over (row, chunk of 512 vectors) with two vectors per thread:
+// on MI355X a streaming kernel with few accesses per thread keeps more of HBM
+// busy than one that loops along a row. Ignored rows are written as zeros
+// without being read.
 #include <math.h>
 
 #include "common.hpp"
@@ -23,7 +26,9 @@ using namespace ts;
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 4;   // vectors in flight per lane in the forward's row loop
+constexpr int kBwdKv = 2;    // vectors per thread in the backward's one-shot grid
+constexpr int64_t kMaxGridY = 65535;  // rows per backward launch
 
 struct Xform {
   float scale;    // 0 = off
@@ -231,26 +236,37 @@ __device__ inline float ce_grad(float x, int64_t j, const BwdRow& r, const Xform
   return r.dl * g;
 }
 
+// Stores one vector of VE gradients (as one or two 16-byte stores).
+template <typename G, int VE>
+__device__ inline void store_grad(G* p, const float* g) {
+  if constexpr (sizeof(G) == 4 && VE == 8) {
+    st16_stream(p, Elt<float>::pack(g));
+    st16_stream(p + 4, Elt<float>::pack(g + 4));
+  } else {
+    st16_stream(p, Elt<G>::pack(g));
+  }
+}
+
+// One-shot grid: blockIdx.y is the row (offset by row0), blockIdx.x a chunk
+// of kThreads * kBwdKv vectors of it; each thread handles kBwdKv vectors.
 template <typename T, typename G, bool kXform, bool kSmooth>
 __global__ __launch_bounds__(kThreads) void ce_bwd_vec(
     const T* logits, int64_t ld, const int64_t* __restrict__ labels,
     const float* __restrict__ lse, const float* __restrict__ dloss, int64_t dloss_stride,
     float dloss_scale, G* grad, int64_t ld_grad, int64_t V, int64_t nvec, int64_t ignore_index,
-    Xform xf, float smoothing) {
+    Xform xf, float smoothing, int64_t row0) {
   constexpr int VE = Elt<T>::kVec;
   static_assert(Elt<G>::kVec == VE || sizeof(G) == 4, "grad vector width");
-  const int64_t row = blockIdx.x;
+  const int64_t row = row0 + blockIdx.y;
   const int64_t label = labels[row];
   G* gr = grad + row * ld_grad;
+  const int64_t base = (int64_t)blockIdx.x * kThreads * kBwdKv + threadIdx.x;
   if (label == ignore_index) {
     const float zero[VE] = {};
-    for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
-      if constexpr (sizeof(G) == 4 && VE == 8) {
-        st16_stream(gr + v * VE, Elt<float>::pack(zero));
-        st16_stream(gr + v * VE + 4, Elt<float>::pack(zero));
-      } else {
-        st16_stream(gr + v * VE, Elt<G>::pack(zero));
-      }
+#pragma unroll
+    for (int k = 0; k < kBwdKv; ++k) {
+      const int64_t v = base + (int64_t)k * kThreads;
+      if (v < nvec) store_grad<G, VE>(gr + v * VE, zero);
     }
     return;
   }
@@ -260,37 +276,22 @@ __global__ __launch_bounds__(kThreads) void ce_bwd_vec(
   r.label = label;
   const float inv_v = 1.f / (float)V;
   const T* xr = logits + row * ld;
-  const int64_t step = (int64_t)kThreads * kUnroll;
-  int64_t base = 0;
-  for (; base + step <= nvec; base += step) {
-    u32x4 buf[kUnroll];
+  u32x4 buf[kBwdKv];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) buf[u] = ld16_stream(xr + (base + u * kThreads + threadIdx.x) * VE);
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t v = base + u * kThreads + threadIdx.x;
-      float x[VE], g[VE];
-      Elt<T>::unpack(buf[u], x);
-#pragma unroll
-      for (int i = 0; i < VE; ++i) g[i] = ce_grad<kXform, kSmooth>(x[i], v * VE + i, r, xf, smoothing, inv_v);
-      if constexpr (sizeof(G) == 4 && VE == 8) {
-        st16_stream(gr + v * VE, Elt<float>::pack(g));
-        st16_stream(gr + v * VE + 4, Elt<float>::pack(g + 4));
-      } else {
-        st16_stream(gr + v * VE, Elt<G>::pack(g));
-      }
-    }
+  for (int k = 0; k < kBwdKv; ++k) {
+    const int64_t v = base + (int64_t)k * kThreads;
+    buf[k] = v < nvec ? ld16_stream(xr + v * VE) : u32x4{0, 0, 0, 0};
   }
-  for (int64_t v = base + threadIdx.x; v < nvec; v += kThreads) {
-    float x[VE], g[VE];
-    Elt<T>::unpack(ld16_stream(xr + v * VE), x);
 #pragma unroll
-    for (int i = 0; i < VE; ++i) g[i] = ce_grad<kXform, kSmooth>(x[i], v * VE + i, r, xf, smoothing, inv_v);
-    if constexpr (sizeof(G) == 4 && VE == 8) {
-      st16_stream(gr + v * VE, Elt<float>::pack(g));
-      st16_stream(gr + v * VE + 4, Elt<float>::pack(g + 4));
-    } else {
-      st16_stream(gr + v * VE, Elt<G>::pack(g));
+  for (int k = 0; k < kBwdKv; ++k) {
+    const int64_t v = base + (int64_t)k * kThreads;
+    if (v < nvec) {
+      float x[VE], g[VE];
+      Elt<T>::unpack(buf[k], x);
+#pragma unroll
+      for (int i = 0; i < VE; ++i)
+        g[i] = ce_grad<kXform, kSmooth>(x[i], v * VE + i, r, xf, smoothing, inv_v);
+      store_grad<G, VE>(gr + v * VE, g);
     }
   }
 }
@@ -367,10 +368,17 @@ ts_status bwd_typed(const void* logits, int64_t ld, const int64_t* labels, const
 #define TS_CE_BWD(X, S)                                                                        \
   if (xform_on == X && smooth == S) {                                                          \
     if (vec) {                                                                                 \
-      hipLaunchKernelGGL((ce_bwd_vec<T, G, X, S>), grid, block, 0, st, lp, ld, labels, lse,    \
-                         dloss, dloss_stride, dloss_scale, gp, ld_grad, V, V / VE,             \
-                         ignore_index, xf, smoothing);                                         \
-      return ts_host::check_launch("ce_bwd_vec");                                              \
+      const int64_t nvec = V / VE;                                                             \
+      const unsigned gx = (unsigned)((nvec + kThreads * kBwdKv - 1) / (kThreads * kBwdKv));    \
+      for (int64_t r0 = 0; r0 < N; r0 += kMaxGridY) {                                          \
+        const unsigned gy = (unsigned)(N - r0 < kMaxGridY ? N - r0 : kMaxGridY);               \
+        hipLaunchKernelGGL((ce_bwd_vec<T, G, X, S>), dim3(gx, gy), block, 0, st, lp, ld,       \
+                           labels, lse, dloss, dloss_stride, dloss_scale, gp, ld_grad, V,      \
+                           nvec, ignore_index, xf, smoothing, r0);                             \
+        ts_status s_ = ts_host::check_launch("ce_bwd_vec");                                    \
+        if (s_ != TS_OK) return s_;                                                            \
+      }                                                                                        \
+      return TS_OK;                                                                            \
     }                                                                                          \
     hipLaunchKernelGGL((ce_bwd_generic<T, G, X, S>), grid, block, 0, st, lp, ld, labels, lse,  \
                        dloss, dloss_stride, dloss_scale, gp, ld_grad, V, ignore_index, xf,     \

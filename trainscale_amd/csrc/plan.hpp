@@ -15,59 +15,91 @@ constexpr int kWave = 64;
 
 // ---------------------------------------------------------------------------
 // RMSNorm
+//
+// Register path: a row is owned by `tpr` threads (a power of two, whole
+// waves), each holding `kv` 16-byte vectors spaced tpr vectors apart, so one
+// load instruction of a wave covers 1 KiB of contiguous row. A workgroup holds
+// rpb = block / tpr rows at a time. Few vectors per thread and many small
+// workgroups keep the HBM queues full; loops over many vectors per thread do
+// not (measured on MI355X: one 16-byte load per thread copies at ~6.4 TB/s,
+// eight per thread at ~4.2 TB/s).
+//
+// Backward: each workgroup walks `steps` consecutive row groups and keeps the
+// dW contributions of its threads' columns in registers; it writes rpb fp32
+// partial rows at the end, which a second kernel sums in a fixed order.
 // ---------------------------------------------------------------------------
-constexpr int kFwdWaves = 4;          // rows per forward workgroup (one per wave)
-constexpr int kFwdMaxVec = 16;        // 16-byte vectors per lane held in registers
-constexpr int kBwdWaves = 8;          // waves per backward workgroup
-constexpr int kBwdMaxVec = 8;         // 16-byte vectors per lane held in registers
-constexpr int kBwdMaxSplit = 4;       // waves that may share one row
-constexpr int64_t kBwdMaxGrid = 512;  // backward workgroups (2 per CU on 256 CUs)
-constexpr int64_t kBwdLdsLimit = 65536 - 1024;  // bytes of the fp32 dW fold row
+constexpr int kMaxKv = 4;                 // vectors per thread on the register path
+constexpr int64_t kBwdGridTarget = 512;   // backward workgroups (2 per CU on 256 CUs)
 constexpr int64_t kGenericRowsPerGroup = 64;
 
 // Elements per 16-byte vector.
 inline int vec_elems(int elt_bytes) { return 16 / elt_bytes; }
 
-// Vectors per lane of the forward register path (power of two), or 0 when
-// the row is too long for registers.
-inline int rms_fwd_maxv(int64_t nvec) {
-  for (int m = 1; m <= kFwdMaxVec; m *= 2)
-    if (nvec <= (int64_t)m * kWave) return m;
-  return 0;
+struct RmsRowPlan {
+  bool reg;    // register path possible
+  int tpr;     // threads per row (64..512)
+  int kv;      // vectors per thread (1, 2 or 4)
+  int block;   // threads per workgroup
+  int rpb;     // rows per workgroup step (block / tpr)
+};
+
+// Forward: two vectors per thread where the row allows it.
+inline RmsRowPlan rms_fwd_plan(int64_t nvec) {
+  RmsRowPlan p{false, 0, 0, 0, 0};
+  if (nvec <= 0 || nvec > 512 * kMaxKv) return p;
+  if (nvec <= 64) { p.tpr = 64; p.kv = 1; }
+  else if (nvec <= 128) { p.tpr = 64; p.kv = 2; }
+  else if (nvec <= 256) { p.tpr = 128; p.kv = 2; }
+  else if (nvec <= 512) { p.tpr = 256; p.kv = 2; }
+  else if (nvec <= 1024) { p.tpr = 512; p.kv = 2; }
+  else { p.tpr = 512; p.kv = 4; }
+  p.reg = true;
+  p.block = p.tpr > 256 ? p.tpr : 256;
+  p.rpb = p.block / p.tpr;
+  return p;
+}
+
+// Backward: one vector per thread where the row allows it (x and dy are both
+// read, so a thread already has two loads in flight).
+inline RmsRowPlan rms_bwd_row_plan(int64_t nvec) {
+  RmsRowPlan p{false, 0, 0, 0, 0};
+  if (nvec <= 0 || nvec > 512 * kMaxKv) return p;
+  if (nvec <= 64) { p.tpr = 64; p.kv = 1; }
+  else if (nvec <= 128) { p.tpr = 128; p.kv = 1; }
+  else if (nvec <= 256) { p.tpr = 256; p.kv = 1; }
+  else if (nvec <= 512) { p.tpr = 512; p.kv = 1; }
+  else if (nvec <= 1024) { p.tpr = 512; p.kv = 2; }
+  else { p.tpr = 512; p.kv = 4; }
+  p.reg = true;
+  p.block = 512;
+  p.rpb = p.block / p.tpr;
+  return p;
 }
 
 struct RmsBwdPlan {
   bool reg;        // register path (else the generic element-wise kernels)
-  int maxv;        // vectors per lane (register path)
-  int split;       // waves per row (register path)
+  RmsRowPlan row;  // register-path shape
+  int64_t steps;   // row groups (of rpb rows) per workgroup
   int64_t grid;    // workgroups of the dx kernel
   int64_t nparts;  // dW partial rows written (== rows of fp32 workspace used)
 };
 
-// Register-path feasibility given the row length in vectors; `vec_ok` says
-// whether pointers/strides allow 16-byte access at all.
+// `vec_ok` says whether pointers and strides allow 16-byte access.
 inline RmsBwdPlan rms_bwd_plan(int64_t rows, int64_t cols, int elt_bytes, bool vec_ok,
                                bool need_dw) {
-  RmsBwdPlan p{false, 0, 0, 0, 0};
+  RmsBwdPlan p{false, RmsRowPlan{false, 0, 0, 0, 0}, 0, 0, 0};
   const int V = vec_elems(elt_bytes);
-  const int64_t nvec = cols / V;
-  int split = 1;
-  while (split <= kBwdMaxSplit && nvec > (int64_t)kWave * kBwdMaxVec * split) split *= 2;
-  const bool lds_ok = !need_dw || cols * 4 <= kBwdLdsLimit;
-  if (vec_ok && cols % V == 0 && split <= kBwdMaxSplit && lds_ok && nvec > 0) {
-    p.reg = true;
-    p.split = split;
-    p.maxv = split == 1 ? rms_fwd_maxv(nvec) : kBwdMaxVec;
-    if (p.maxv > kBwdMaxVec || p.maxv == 0) p.reg = false;
-  }
+  if (vec_ok && cols % V == 0) p.row = rms_bwd_row_plan(cols / V);
+  p.reg = p.row.reg;
   if (p.reg) {
-    const int64_t per_step = kBwdWaves / p.split;
-    const int64_t want = (rows + per_step - 1) / per_step;
-    p.grid = want < kBwdMaxGrid ? want : kBwdMaxGrid;
-    p.nparts = need_dw ? p.grid : 0;
+    const int64_t groups = (rows + p.row.rpb - 1) / p.row.rpb;
+    int64_t steps = (groups + kBwdGridTarget - 1) / kBwdGridTarget;
+    if (steps < 1) steps = 1;
+    p.steps = steps;
+    p.grid = (groups + steps - 1) / steps;
+    p.nparts = need_dw ? p.grid * p.row.rpb : 0;
   } else {
-    p.split = 0;
-    p.maxv = 0;
+    p.steps = 0;
     p.grid = rows;
     p.nparts = need_dw ? (rows + kGenericRowsPerGroup - 1) / kGenericRowsPerGroup : 0;
   }
@@ -84,6 +116,32 @@ inline int64_t rms_bwd_workspace_rows(int64_t rows, int64_t cols) {
     if (p.nparts > m) m = p.nparts;
   }
   return m;
+}
+
+// ---------------------------------------------------------------------------
+// RoPE workgroup shape: about one thread per task (a task is a 16-byte vector
+// pair of one head, or one pair on the generic path), whole waves, at least
+// 256 threads, at most max_threads; `tpb` tokens per workgroup, bounded so the
+// cos/sin staging (tpb * half floats each) fits max_angles.
+// ---------------------------------------------------------------------------
+struct RopeBlock {
+  int tpb;      // tokens per workgroup
+  int threads;  // threads per workgroup (multiple of 64)
+};
+
+inline RopeBlock rope_block(int64_t tasks_per_token, int half, int max_threads, int max_angles) {
+  RopeBlock b{1, 64};
+  int64_t tpb = tasks_per_token >= 256 ? 1 : 256 / (tasks_per_token > 0 ? tasks_per_token : 1);
+  const int64_t cap = max_angles / (half > 0 ? half : 1);
+  if (tpb > cap) tpb = cap;
+  if (tpb < 1) tpb = 1;
+  int64_t threads = tpb * tasks_per_token;
+  threads = (threads + kWave - 1) / kWave * kWave;
+  if (threads < 256) threads = 256;
+  if (threads > max_threads) threads = max_threads;
+  b.tpb = (int)tpb;
+  b.threads = (int)threads;
+  return b;
 }
 
 // ---------------------------------------------------------------------------

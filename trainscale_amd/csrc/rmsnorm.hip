@@ -1,85 +1,109 @@
 // RMSNorm forward/backward for gfx950.
 //
-// Forward (register path): one row per wave64. Each lane loads its share of
-// the row with 16-byte loads (lane-interleaved, so every load instruction of a
-// wave covers one contiguous 1 KiB span), keeps it in VGPRs, reduces the sum
-// of squares with DPP, and writes y from the same registers: x is read from
-// HBM exactly once. Four rows per 256-thread workgroup.
+// Register path (ts_plan::rms_fwd_plan / rms_bwd_row_plan): a row is owned by
+// TPR threads (whole waves), each holding KV 16-byte vectors spaced TPR
+// vectors apart, so every load instruction of a wave covers 1 KiB of
+// contiguous row and each thread has only one or two loads in flight per
+// tensor; the row stays in VGPRs between the reduction and the output, so x
+// (and dy) are read from HBM exactly once. The sum of squares (forward) and
+// sum(dy*w*xhat) (backward) are reduced with DPP inside each wave and through
+// LDS across the row's waves.
 //
-// Backward (register path): 8 waves per workgroup, at most kBwdMaxGrid
-// workgroups (plan.hpp). Each wave walks rows with a grid stride:
-// per row it reads dy and x once, reduces sum(dy*w*xhat) with DPP, writes dx,
-// and accumulates dy*xhat for dW in fp32 registers. At the end the 8 waves
-// fold their accumulators through LDS in a fixed order and the workgroup
-// writes one fp32 partial row; a second kernel sums the partial rows in a
-// fixed order. dW is therefore bit-reproducible run to run (no float atomics),
+// Backward: each workgroup walks `steps` consecutive groups of rows and keeps
+// dy*xhat for its threads' columns in fp32 registers, then writes one fp32
+// partial row per row slot; rms_dw_reduce4 sums the partial rows in a fixed
+// order. dW is therefore bit-reproducible run to run (no float atomics),
 // unlike the reference's atomic_add variant.
 //
 // Generic path (row length not a multiple of the 16-byte vector, unaligned
-// pointers, or rows too long for registers): one workgroup per row with
-// element-wise loads and two passes over the row.
+// pointers, or rows longer than the register plans): one workgroup per row
+// with element-wise loads and two passes over the row.
 #include "common.hpp"
 #include "plan.hpp"
 
 namespace {
 
 using namespace ts;
-using ts_plan::kBwdWaves;
-using ts_plan::kFwdWaves;
 
-// Loads kVec weights for the 16-byte data vector starting at element e.
-template <typename W, int kVec>
+// Loads V weights for the 16-byte data vector starting at element e.
+template <typename W, int V>
 __device__ inline void load_w(const W* __restrict__ w, int64_t e, float* f) {
   if constexpr (sizeof(W) == 4) {
 #pragma unroll
-    for (int h = 0; h < kVec / 4; ++h) Elt<float>::unpack(ld16(w + e + 4 * h), f + 4 * h);
+    for (int h = 0; h < V / 4; ++h) Elt<float>::unpack(ld16(w + e + 4 * h), f + 4 * h);
   } else {
-    static_assert(Elt<W>::kVec == kVec, "16-bit weight vector must match data vector");
+    static_assert(Elt<W>::kVec == V, "16-bit weight vector must match data vector");
     Elt<W>::unpack(ld16(w + e), f);
+  }
+}
+
+// Sum of v over the TPR threads that own one row. `red` holds one float per
+// wave of the workgroup; contains one barrier when TPR > 64 (every thread of
+// the workgroup must call it).
+template <int TPR, int kBlock>
+__device__ inline float row_reduce(float v, float* red) {
+  v = wave_sum(v);
+  if constexpr (TPR == kWave) {
+    return v;
+  } else {
+    constexpr int kWavesPerRow = TPR / kWave;
+    const int wid = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) red[wid] = v;
+    __syncthreads();
+    const int first = (wid / kWavesPerRow) * kWavesPerRow;
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWavesPerRow; ++i) t += red[first + i];
+    return t;
   }
 }
 
 // ---------------------------------------------------------------------------
 // Forward, register path.
 // ---------------------------------------------------------------------------
-template <typename T, typename W, int kMaxV>
-__global__ __launch_bounds__(kFwdWaves* kWave) void rms_fwd_reg(
+template <typename T, typename W, int TPR, int KV>
+__global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
     const T* __restrict__ x, int64_t ldx, const W* __restrict__ w, T* __restrict__ y,
     int64_t ldy, float* __restrict__ rstd_out, int64_t rows, int nvec, float fcols, float eps,
     int twice) {
   constexpr int V = Elt<T>::kVec;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * kFwdWaves + threadIdx.x / kWave;
-  if (row >= rows) return;  // wave-uniform; no workgroup barrier below
+  constexpr int kBlock = TPR > 256 ? TPR : 256;
+  constexpr int kRpb = kBlock / TPR;
+  __shared__ float red[kBlock / kWave];
+  const int sub = threadIdx.x / TPR;
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * kRpb + sub;
+  const bool valid = row < rows;
 
   const T* xr = x + row * ldx;
-  u32x4 xv[kMaxV];
+  u32x4 xv[KV];
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
-    const int v = lane + j * kWave;
-    xv[j] = v < nvec ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+  for (int k = 0; k < KV; ++k) {
+    const int v = t + k * TPR;
+    xv[k] = valid && v < nvec ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
   }
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
+  for (int k = 0; k < KV; ++k) {
     float f[V];
-    Elt<T>::unpack(xv[j], f);
+    Elt<T>::unpack(xv[k], f);
 #pragma unroll
     for (int i = 0; i < V; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
   }
-  ss = wave_sum(ss);
+  ss = row_reduce<TPR, kBlock>(ss, red);
   // mean(x^2) = sum / n (a division, as the reference divides by n_cols), then
   // 1/sqrt with correctly rounded sqrt and divide.
   const float rstd = 1.0f / __builtin_sqrtf(ss / fcols + eps);
-  if (lane == 0) rstd_out[row] = rstd;
+  if (!valid) return;  // no barrier below
+  if (t == 0) rstd_out[row] = rstd;
 
   T* yr = y + row * ldy;
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j) {
-    const int v = lane + j * kWave;
+  for (int k = 0; k < KV; ++k) {
+    const int v = t + k * TPR;
     if (v < nvec) {
       float f[V];
-      Elt<T>::unpack(xv[j], f);
+      Elt<T>::unpack(xv[k], f);
       if (w != nullptr) {
         float wf[V];
         load_w<W, V>(w, (int64_t)v * V, wf);
@@ -100,129 +124,95 @@ __global__ __launch_bounds__(kFwdWaves* kWave) void rms_fwd_reg(
 }
 
 // ---------------------------------------------------------------------------
-// Backward, register path: dx plus per-workgroup dW partial rows.
-// kSplit waves share one row (each holds kMaxV vectors per lane); their
-// partial row sums meet in double-buffered LDS slots, one barrier per step.
+// Backward, register path: dx plus one fp32 dW partial row per row slot.
+// Workgroup b handles row groups [b*steps, (b+1)*steps), each of kRpb rows.
 // ---------------------------------------------------------------------------
-template <typename T, typename W, int kMaxV, int kSplit>
-__global__ __launch_bounds__(kBwdWaves* kWave) void rms_bwd_reg(
+template <typename T, typename W, int TPR, int KV>
+__global__ __launch_bounds__(512) void rms_bwd_reg(
     const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x, int64_t ldx,
     const W* __restrict__ w, const float* __restrict__ rstd_in, T* __restrict__ dx,
-    int64_t lddx, float* __restrict__ partial, int64_t rows, int nvec, float fcols) {
+    int64_t lddx, float* __restrict__ partial, int64_t rows, int64_t steps, int nvec,
+    float fcols) {
   constexpr int V = Elt<T>::kVec;
-  constexpr int kRowsPerStep = kBwdWaves / kSplit;
-  extern __shared__ float lds_acc[];  // [nvec * V] fp32
-  __shared__ float red[2][kBwdWaves];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wid = threadIdx.x / kWave;
-  const int sub = wid % kSplit;
-  const int vbase = sub * kWave + lane;
+  constexpr int kBlock = 512;
+  constexpr int kRpb = kBlock / TPR;
+  __shared__ float red[2][kBlock / kWave];
+  const int sub = threadIdx.x / TPR;
+  const int t = threadIdx.x % TPR;
 
-  float acc[kMaxV][V];
+  float wf[KV][V];
+  float acc[KV][V];
 #pragma unroll
-  for (int j = 0; j < kMaxV; ++j)
+  for (int k = 0; k < KV; ++k) {
+    const int v = t + k * TPR;
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[j][i] = 0.f;
+    for (int i = 0; i < V; ++i) {
+      acc[k][i] = 0.f;
+      wf[k][i] = 1.f;
+    }
+    if (w != nullptr && v < nvec) load_w<W, V>(w, (int64_t)v * V, wf[k]);
+  }
 
-  const int64_t nsteps = (rows + kRowsPerStep - 1) / kRowsPerStep;
-  int it = 0;
-  // The loop bound is uniform over the workgroup (barriers inside when kSplit > 1).
-  for (int64_t g = blockIdx.x; g < nsteps; g += gridDim.x, ++it) {
-    const int64_t row = g * kRowsPerStep + wid / kSplit;
+  // `steps` is uniform over the workgroup (barriers inside when TPR > 64).
+  for (int64_t st = 0; st < steps; ++st) {
+    const int64_t row = ((int64_t)blockIdx.x * steps + st) * kRpb + sub;
     const bool valid = row < rows;
     const T* xr = x + row * ldx;
     const T* dyr = dy + row * lddy;
-    u32x4 xv[kMaxV], dv[kMaxV];
+    u32x4 xv[KV], dv[KV];
 #pragma unroll
-    for (int j = 0; j < kMaxV; ++j) {
-      const int v = vbase + j * kWave * kSplit;
+    for (int k = 0; k < KV; ++k) {
+      const int v = t + k * TPR;
       const bool ok = valid && v < nvec;
-      xv[j] = ok ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
-      dv[j] = ok ? ld16_stream(dyr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+      xv[k] = ok ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+      dv[k] = ok ? ld16_stream(dyr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
     }
     const float rstd = valid ? rstd_in[row] : 0.f;
-    // c1 = mean(dy * w * xhat)
+    // c1 = mean(dy * w * xhat); rows that are not valid hold zeros.
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxV; ++j) {
-      const int v = vbase + j * kWave * kSplit;
-      if (v < nvec) {
-        float xf[V], df[V], wf[V];
-        Elt<T>::unpack(xv[j], xf);
-        Elt<T>::unpack(dv[j], df);
-        if (w != nullptr) {
-          load_w<W, V>(w, (int64_t)v * V, wf);
-        } else {
+    for (int k = 0; k < KV; ++k) {
+      float xf[V], df[V];
+      Elt<T>::unpack(xv[k], xf);
+      Elt<T>::unpack(dv[k], df);
 #pragma unroll
-          for (int i = 0; i < V; ++i) wf[i] = 1.f;
-        }
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-          const float xh = xf[i] * rstd;
-          s = __builtin_fmaf(df[i] * wf[i], xh, s);
-          acc[j][i] = __builtin_fmaf(df[i], xh, acc[j][i]);
-        }
+      for (int i = 0; i < V; ++i) {
+        const float xh = xf[i] * rstd;
+        s = __builtin_fmaf(df[i] * wf[k][i], xh, s);
+        acc[k][i] = __builtin_fmaf(df[i], xh, acc[k][i]);
       }
     }
-    float c1;
-    if constexpr (kSplit == 1) {
-      c1 = wave_sum(s) / fcols;
-    } else {
-      const float sw = wave_sum(s);
-      if (lane == 0) red[it & 1][wid] = sw;
-      __syncthreads();
-      const int first = (wid / kSplit) * kSplit;
-      float t = 0.f;
-#pragma unroll
-      for (int k = 0; k < kSplit; ++k) t += red[it & 1][first + k];
-      c1 = t / fcols;
-    }
+    const float c1 = row_reduce<TPR, kBlock>(s, red[st & 1]) / fcols;
     if (valid) {
       T* dxr = dx + row * lddx;
 #pragma unroll
-      for (int j = 0; j < kMaxV; ++j) {
-        const int v = vbase + j * kWave * kSplit;
+      for (int k = 0; k < KV; ++k) {
+        const int v = t + k * TPR;
         if (v < nvec) {
-          float xf[V], df[V], wf[V], o[V];
-          Elt<T>::unpack(xv[j], xf);
-          Elt<T>::unpack(dv[j], df);
-          if (w != nullptr) {
-            load_w<W, V>(w, (int64_t)v * V, wf);
-          } else {
+          float xf[V], df[V], o[V];
+          Elt<T>::unpack(xv[k], xf);
+          Elt<T>::unpack(dv[k], df);
 #pragma unroll
-            for (int i = 0; i < V; ++i) wf[i] = 1.f;
-          }
-#pragma unroll
-          for (int i = 0; i < V; ++i) o[i] = rstd * (df[i] * wf[i] - (xf[i] * rstd) * c1);
+          for (int i = 0; i < V; ++i) o[i] = rstd * (df[i] * wf[k][i] - (xf[i] * rstd) * c1);
           st16_stream(dxr + (int64_t)v * V, Elt<T>::pack(o));
         }
       }
     }
   }
 
-  if (partial == nullptr) return;  // dW not requested (uniform over the grid)
-  // Fold the waves' accumulators in wave order through one LDS row.
-  for (int wv = 0; wv < kBwdWaves; ++wv) {
-    if (wid == wv) {
+  if (partial == nullptr) return;  // dW not requested
+  const int ncols = nvec * V;
+  float* prow = partial + ((int64_t)blockIdx.x * kRpb + sub) * ncols;
 #pragma unroll
-      for (int j = 0; j < kMaxV; ++j) {
-        const int v = vbase + j * kWave * kSplit;
-        if (v < nvec) {
+  for (int k = 0; k < KV; ++k) {
+    const int v = t + k * TPR;
+    if (v < nvec) {
 #pragma unroll
-          for (int i = 0; i < V; ++i) {
-            float* p = lds_acc + v * V + i;
-            *p = (wv < kSplit ? 0.f : *p) + acc[j][i];
-          }
-        }
+      for (int h = 0; h < V / 4; ++h) {
+        *reinterpret_cast<float4*>(prow + v * V + 4 * h) =
+            make_float4(acc[k][4 * h], acc[k][4 * h + 1], acc[k][4 * h + 2], acc[k][4 * h + 3]);
       }
     }
-    __syncthreads();
-  }
-  const int ncols = nvec * V;
-  float* prow = partial + (int64_t)blockIdx.x * ncols;
-  for (int c = threadIdx.x * 4; c < ncols; c += kBwdWaves * kWave * 4) {
-    // ncols is a multiple of 4 on this path (16-byte vectors of >= 2-byte data)
-    *reinterpret_cast<float4*>(prow + c) = *reinterpret_cast<const float4*>(lds_acc + c);
   }
 }
 
@@ -233,12 +223,57 @@ __global__ __launch_bounds__(256) void zero_bytes(uint8_t* __restrict__ p, size_
   if (i < n) p[i] = 0;
 }
 
-// dW[c] = sum over partial rows in a fixed order. 64 columns per workgroup,
-// 4 row-groups per column combined in a fixed order through LDS.
+// dW[c] = sum over partial rows, in a fixed order. cols % 4 == 0: a workgroup
+// takes 16 columns (4 float4 quads) x 64 row groups, then a fixed tree over
+// the 64 groups in LDS.
 template <typename W>
-__global__ __launch_bounds__(256) void rms_dw_reduce(const float* __restrict__ partial,
-                                                     int64_t nparts, int64_t cols,
-                                                     W* __restrict__ dw) {
+__global__ __launch_bounds__(256) void rms_dw_reduce4(const float* __restrict__ partial,
+                                                      int64_t nparts, int64_t cols,
+                                                      W* __restrict__ dw) {
+  __shared__ float4 red[64][4];
+  const int cq = threadIdx.x & 3;
+  const int g = threadIdx.x >> 2;
+  const int64_t c = (int64_t)blockIdx.x * 16 + cq * 4;
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < cols) {
+    for (int64_t b = g; b < nparts; b += 64) {
+      const float4 v = *reinterpret_cast<const float4*>(partial + b * cols + c);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+  }
+  red[g][cq] = s;
+  __syncthreads();
+#pragma unroll
+  for (int h = 32; h >= 1; h >>= 1) {
+    if (g < h) {
+      const float4 o = red[g + h][cq];
+      float4 m = red[g][cq];
+      m.x += o.x;
+      m.y += o.y;
+      m.z += o.z;
+      m.w += o.w;
+      red[g][cq] = m;
+    }
+    __syncthreads();
+  }
+  if (g == 0 && c < cols) {
+    const float4 t = red[0][cq];
+    Elt<W>::store1(dw + c, t.x);
+    Elt<W>::store1(dw + c + 1, t.y);
+    Elt<W>::store1(dw + c + 2, t.z);
+    Elt<W>::store1(dw + c + 3, t.w);
+  }
+}
+
+// dW[c] for any column count: 64 columns per workgroup, 4 row groups per
+// column combined in a fixed order through LDS.
+template <typename W>
+__global__ __launch_bounds__(256) void rms_dw_reduce1(const float* __restrict__ partial,
+                                                      int64_t nparts, int64_t cols,
+                                                      W* __restrict__ dw) {
   __shared__ float red[4][64];
   const int cl = threadIdx.x & 63;
   const int g = threadIdx.x >> 6;
@@ -352,25 +387,27 @@ ts_status fwd_typed(const void* x, int64_t ldx, const void* w, void* y, int64_t 
   const W* wp = static_cast<const W*>(w);
   T* yp = static_cast<T*>(y);
   const int64_t nvec = cols / V;
-  const int maxv = ts_plan::rms_fwd_maxv(nvec);
-  if (vec_ok<T, W>(x, ldx, cols, w) && vec_ok<T, W>(y, ldy, cols, nullptr) && maxv > 0) {
-    const dim3 grid((unsigned)((rows + kFwdWaves - 1) / kFwdWaves));
-    const dim3 block(kFwdWaves * kWave);
-#define TS_LAUNCH_FWD(M)                                                                       \
-  case M:                                                                                      \
-    hipLaunchKernelGGL((rms_fwd_reg<T, W, M>), grid, block, 0, st, xp, ldx, wp, yp, ldy, rstd, \
-                       rows, (int)nvec, (float)cols, eps, twice);                              \
-    break;
-    switch (maxv) {
-      TS_LAUNCH_FWD(1)
-      TS_LAUNCH_FWD(2)
-      TS_LAUNCH_FWD(4)
-      TS_LAUNCH_FWD(8)
-      TS_LAUNCH_FWD(16)
-      default:
-        return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_fwd: bad plan (maxv=%d)", maxv);
-    }
+  const ts_plan::RmsRowPlan plan = ts_plan::rms_fwd_plan(nvec);
+  if (vec_ok<T, W>(x, ldx, cols, w) && vec_ok<T, W>(y, ldy, cols, nullptr) && plan.reg) {
+    const dim3 grid((unsigned)((rows + plan.rpb - 1) / plan.rpb));
+    const dim3 block(plan.block);
+    bool launched = false;
+#define TS_LAUNCH_FWD(TPR, KV)                                                                 \
+  if (plan.tpr == TPR && plan.kv == KV) {                                                      \
+    hipLaunchKernelGGL((rms_fwd_reg<T, W, TPR, KV>), grid, block, 0, st, xp, ldx, wp, yp, ldy, \
+                       rstd, rows, (int)nvec, (float)cols, eps, twice);                        \
+    launched = true;                                                                           \
+  }
+    TS_LAUNCH_FWD(64, 1)
+    TS_LAUNCH_FWD(64, 2)
+    TS_LAUNCH_FWD(128, 2)
+    TS_LAUNCH_FWD(256, 2)
+    TS_LAUNCH_FWD(512, 2)
+    TS_LAUNCH_FWD(512, 4)
 #undef TS_LAUNCH_FWD
+    if (!launched)
+      return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_fwd: bad plan (tpr=%d kv=%d)",
+                           plan.tpr, plan.kv);
     return ts_host::check_launch("rms_fwd_reg");
   }
   hipLaunchKernelGGL((rms_fwd_generic<T, W>), dim3((unsigned)rows), dim3(256), 0, st, xp, ldx,
@@ -396,26 +433,25 @@ ts_status bwd_typed(const void* dy, int64_t lddy, const void* x, int64_t ldx, co
     return ts_host::fail(TS_ERR_WORKSPACE, "rmsnorm_bwd: plan needs %lld partial rows",
                          (long long)plan.nparts);
   if (plan.reg) {
-    const size_t lds = dw != nullptr ? (size_t)cols * sizeof(float) : 0;
     float* part = dw != nullptr ? ws : nullptr;
     bool launched = false;
-#define TS_LAUNCH_BWD(M, SP)                                                                    \
-  if (plan.maxv == M && plan.split == SP) {                                                     \
-    hipLaunchKernelGGL((rms_bwd_reg<T, W, M, SP>), dim3((unsigned)plan.grid),                   \
-                       dim3(kBwdWaves * kWave), lds, st, dyp, lddy, xp, ldx, wp, rstd, dxp,     \
-                       lddx, part, rows, (int)nvec, (float)cols);                               \
+#define TS_LAUNCH_BWD(TPR, KV)                                                                  \
+  if (plan.row.tpr == TPR && plan.row.kv == KV) {                                               \
+    hipLaunchKernelGGL((rms_bwd_reg<T, W, TPR, KV>), dim3((unsigned)plan.grid), dim3(512), 0,   \
+                       st, dyp, lddy, xp, ldx, wp, rstd, dxp, lddx, part, rows, plan.steps,     \
+                       (int)nvec, (float)cols);                                                 \
     launched = true;                                                                            \
   }
-    TS_LAUNCH_BWD(1, 1)
-    TS_LAUNCH_BWD(2, 1)
-    TS_LAUNCH_BWD(4, 1)
-    TS_LAUNCH_BWD(8, 1)
-    TS_LAUNCH_BWD(8, 2)
-    TS_LAUNCH_BWD(8, 4)
+    TS_LAUNCH_BWD(64, 1)
+    TS_LAUNCH_BWD(128, 1)
+    TS_LAUNCH_BWD(256, 1)
+    TS_LAUNCH_BWD(512, 1)
+    TS_LAUNCH_BWD(512, 2)
+    TS_LAUNCH_BWD(512, 4)
 #undef TS_LAUNCH_BWD
     if (!launched)
-      return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: bad plan (maxv=%d split=%d)",
-                           plan.maxv, plan.split);
+      return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: bad plan (tpr=%d kv=%d)",
+                           plan.row.tpr, plan.row.kv);
     ts_status s = ts_host::check_launch("rms_bwd_reg");
     if (s != TS_OK) return s;
   } else {
@@ -433,9 +469,14 @@ ts_status bwd_typed(const void* dy, int64_t lddy, const void* x, int64_t ldx, co
     }
   }
   if (dw != nullptr) {
-    hipLaunchKernelGGL((rms_dw_reduce<W>), dim3((unsigned)((cols + 63) / 64)), dim3(256), 0, st,
+    if (cols % 4 == 0) {
+      hipLaunchKernelGGL((rms_dw_reduce4<W>), dim3((unsigned)((cols + 15) / 16)), dim3(256), 0,
+                         st, ws, plan.nparts, cols, static_cast<W*>(dw));
+      return ts_host::check_launch("rms_dw_reduce4");
+    }
+    hipLaunchKernelGGL((rms_dw_reduce1<W>), dim3((unsigned)((cols + 63) / 64)), dim3(256), 0, st,
                        ws, plan.nparts, cols, static_cast<W*>(dw));
-    return ts_host::check_launch("rms_dw_reduce");
+    return ts_host::check_launch("rms_dw_reduce1");
   }
   return TS_OK;
 }

@@ -1,19 +1,22 @@
 // Rotary position embedding (RoPE) forward/backward for gfx950.
 //
-// One 256-thread workgroup handles kTok consecutive tokens (b, s) and every
-// head of both tensors (Q heads then K heads) at those tokens. Phase 1 fills
-// LDS with cos/sin for the workgroup's tokens: either gathered from the
-// caller's tables at pos(b, s), or evaluated in registers from the fp32 angle
-// fp32(pos / pos_div) * inv_freq[i] (the product torch.outer forms on the
-// host), so each (token, frequency) pair is evaluated once and reused across
-// all Hq + Hk heads. Phase 2 streams the heads: a task is one 16-byte vector
+// A workgroup handles `tpb` consecutive tokens (b, s) and every head of both
+// tensors (Q heads then K heads) at those tokens. A task is one 16-byte vector
 // from each half of a head (NeoX layout: pairs (i, i + D/2)) or one 16-byte
-// vector of adjacent pairs (interleaved layout), so Q and K are read and
-// written exactly once with 128-bit accesses. Backward is the same kernel
-// with sin negated (the transpose rotation).
+// vector of adjacent pairs (interleaved layout); the workgroup has about one
+// thread per task (320 threads for 32 + 8 heads of 128), so each thread keeps
+// two 16-byte loads in flight and Q and K are read and written exactly once.
 //
-// A generic element-wise kernel covers unaligned tensors and head dims whose
-// half is not a multiple of the vector width.
+// Each thread issues the loads of its first task, then the workgroup fills
+// LDS with cos/sin for its tokens: gathered from the caller's tables at
+// pos(b, s), or evaluated from the fp32 angle fp32(pos / pos_div) * inv_freq[i]
+// (the product torch.outer forms on the host), once per (token, frequency)
+// and shared by all Hq + Hk heads. After one barrier the thread rotates and
+// stores. Backward is the same kernel with sin negated (the transpose
+// rotation).
+//
+// A generic element-wise kernel (a task is one pair) covers unaligned tensors
+// and head dims whose half is not a multiple of the vector width.
 #include <math.h>
 
 #include "common.hpp"
@@ -23,9 +26,9 @@ namespace {
 
 using namespace ts;
 
-constexpr int kTok = 4;           // tokens per workgroup
-constexpr int kThreads = 256;
-constexpr int kMaxHalf = 256;     // head_dim <= 512
+constexpr int kMaxThreads = 1024;
+constexpr int kMaxHalf = 256;        // head_dim <= 512
+constexpr int kLdsAngles = 4096;     // max tpb * half (cos + sin = 32 KiB of LDS)
 
 struct RopeArgs {
   const void* q_in;
@@ -46,6 +49,7 @@ struct RopeArgs {
   const int64_t* position_ids;
   int64_t pos_sb, pos_ss, position_offset;
   int32_t backward;
+  int32_t tpb;               // tokens per workgroup
   int32_t tasks_per_head;    // 16-byte tasks per head (vector path) or pairs per head
   int32_t tasks_per_token;   // tasks_per_head * (Hq + Hk)
   uint32_t tpt_magic;        // ts_plan::magic_for(tasks_per_token)
@@ -64,11 +68,11 @@ __device__ inline float tab_load(const void* p, int64_t idx) {
   return Elt<TabT>::load1(static_cast<const TabT*>(p) + idx);
 }
 
-// Phase 1: cos/sin of the workgroup's tokens into LDS ([kTok][half] each).
+// cos/sin of the workgroup's tokens into LDS ([tpb][half] each).
 template <typename TabT, bool kTable>
 __device__ inline void fill_angles(const RopeArgs& a, int64_t tok0, float* cs, float* sn) {
-  const int n = kTok * a.half;
-  for (int idx = threadIdx.x; idx < n; idx += kThreads) {
+  const int n = a.tpb * a.half;
+  for (int idx = threadIdx.x; idx < n; idx += blockDim.x) {
     const int i = idx / a.half;
     const int f = idx - i * a.half;
     const int64_t t = tok0 + i;
@@ -97,109 +101,135 @@ __device__ inline void fill_angles(const RopeArgs& a, int64_t tok0, float* cs, f
   }
 }
 
-template <typename T, typename TabT, bool kTable, bool kInterleaved>
-__global__ __launch_bounds__(kThreads) void rope_vec_kernel(const RopeArgs a) {
+// Task f of the workgroup starting at token tok0: source/destination head
+// pointers, token slot i and index j of the task within its head.
+template <typename T>
+struct Task {
+  const T* src;
+  T* dst;
+  int i;
+  int j;
+};
+
+template <typename T>
+__device__ inline Task<T> task_at(const RopeArgs& a, int64_t tok0, int f) {
+  Task<T> k;
+  k.i = (int)fast_div((uint32_t)f, a.tpt_magic);
+  const int r = f - k.i * a.tasks_per_token;
+  const int hh = (int)fast_div((uint32_t)r, a.tph_magic);
+  k.j = r - hh * a.tasks_per_head;
+  const int64_t t = tok0 + k.i;
+  const int64_t b = t / a.S;
+  const int64_t sq = t - b * a.S;
+  if (hh < a.Hq) {
+    k.src = static_cast<const T*>(a.q_in) + b * a.q_in_sb + sq * a.q_in_ss + hh * a.q_in_sh;
+    k.dst = static_cast<T*>(a.q_out) + b * a.q_out_sb + sq * a.q_out_ss + hh * a.q_out_sh;
+  } else {
+    const int kh = hh - a.Hq;
+    k.src = static_cast<const T*>(a.k_in) + b * a.k_in_sb + sq * a.k_in_ss + kh * a.k_in_sh;
+    k.dst = static_cast<T*>(a.k_out) + b * a.k_out_sb + sq * a.k_out_ss + kh * a.k_out_sh;
+  }
+  return k;
+}
+
+// Loads of one vector task: NeoX reads one vector from each half, the
+// interleaved layout one vector of adjacent pairs (v2 unused).
+template <typename T, bool kInterleaved>
+__device__ inline void task_load(const RopeArgs& a, const Task<T>& k, u32x4& v1, u32x4& v2) {
   constexpr int V = Elt<T>::kVec;
+  if constexpr (!kInterleaved) {
+    v1 = ld16_stream(k.src + k.j * V);
+    v2 = ld16_stream(k.src + a.half + k.j * V);
+  } else {
+    v1 = ld16_stream(k.src + k.j * V);
+    v2 = u32x4{0, 0, 0, 0};
+  }
+}
+
+template <typename T, bool kInterleaved>
+__device__ inline void task_rotate_store(const RopeArgs& a, const Task<T>& k, const u32x4& v1,
+                                         const u32x4& v2, const float* cs, const float* sn) {
+  constexpr int V = Elt<T>::kVec;
+  const float* crow = cs + k.i * a.half;
+  const float* srow = sn + k.i * a.half;
+  if constexpr (!kInterleaved) {
+    const int e1 = k.j * V;
+    float x1[V], x2[V], o1[V], o2[V];
+    Elt<T>::unpack(v1, x1);
+    Elt<T>::unpack(v2, x2);
+#pragma unroll
+    for (int p = 0; p < V; ++p) {
+      const float c = crow[e1 + p];
+      const float s = srow[e1 + p];
+      o1[p] = x1[p] * c - x2[p] * s;
+      o2[p] = x2[p] * c + x1[p] * s;
+    }
+    st16_stream(k.dst + e1, Elt<T>::pack(o1));
+    st16_stream(k.dst + a.half + e1, Elt<T>::pack(o2));
+  } else {
+    const int e = k.j * V;
+    float x[V], o[V];
+    Elt<T>::unpack(v1, x);
+#pragma unroll
+    for (int p = 0; p < V / 2; ++p) {
+      const float c = crow[e / 2 + p];
+      const float s = srow[e / 2 + p];
+      o[2 * p] = x[2 * p] * c - x[2 * p + 1] * s;
+      o[2 * p + 1] = x[2 * p + 1] * c + x[2 * p] * s;
+    }
+    st16_stream(k.dst + e, Elt<T>::pack(o));
+  }
+}
+
+template <typename T, typename TabT, bool kTable, bool kInterleaved>
+__global__ __launch_bounds__(kMaxThreads) void rope_vec_kernel(const RopeArgs a) {
   extern __shared__ float lds[];
   float* cs = lds;
-  float* sn = lds + kTok * a.half;
-  const int64_t tok0 = (int64_t)blockIdx.x * kTok;
+  float* sn = lds + a.tpb * a.half;
+  const int64_t tok0 = (int64_t)blockIdx.x * a.tpb;
+  const int64_t ntok_here = a.ntok - tok0 < a.tpb ? a.ntok - tok0 : a.tpb;
+  const int total = (int)ntok_here * a.tasks_per_token;
+
+  // First task's loads go out before the angle phase.
+  int f = threadIdx.x;
+  Task<T> k0{};
+  u32x4 v1{0, 0, 0, 0}, v2{0, 0, 0, 0};
+  if (f < total) {
+    k0 = task_at<T>(a, tok0, f);
+    task_load<T, kInterleaved>(a, k0, v1, v2);
+  }
   fill_angles<TabT, kTable>(a, tok0, cs, sn);
   __syncthreads();
-
-  const int64_t ntok_here = a.ntok - tok0 < kTok ? a.ntok - tok0 : kTok;
-  const int total = (int)ntok_here * a.tasks_per_token;
-  for (int f = threadIdx.x; f < total; f += kThreads) {
-    const int i = (int)fast_div((uint32_t)f, a.tpt_magic);
-    const int r = f - i * a.tasks_per_token;
-    const int hh = (int)fast_div((uint32_t)r, a.tph_magic);
-    const int j = r - hh * a.tasks_per_head;
-    const int64_t t = tok0 + i;
-    const int64_t b = t / a.S;
-    const int64_t sq = t - b * a.S;
-    const T* src;
-    T* dst;
-    if (hh < a.Hq) {
-      src = static_cast<const T*>(a.q_in) + b * a.q_in_sb + sq * a.q_in_ss + hh * a.q_in_sh;
-      dst = static_cast<T*>(a.q_out) + b * a.q_out_sb + sq * a.q_out_ss + hh * a.q_out_sh;
-    } else {
-      const int kh = hh - a.Hq;
-      src = static_cast<const T*>(a.k_in) + b * a.k_in_sb + sq * a.k_in_ss + kh * a.k_in_sh;
-      dst = static_cast<T*>(a.k_out) + b * a.k_out_sb + sq * a.k_out_ss + kh * a.k_out_sh;
-    }
-    const float* crow = cs + i * a.half;
-    const float* srow = sn + i * a.half;
-    if constexpr (!kInterleaved) {
-      const int e1 = j * V;
-      const int e2 = a.half + j * V;
-      const u32x4 v1 = ld16_stream(src + e1);
-      const u32x4 v2 = ld16_stream(src + e2);
-      float x1[V], x2[V], o1[V], o2[V];
-      Elt<T>::unpack(v1, x1);
-      Elt<T>::unpack(v2, x2);
-#pragma unroll
-      for (int p = 0; p < V; ++p) {
-        const float c = crow[e1 + p];
-        const float s = srow[e1 + p];
-        o1[p] = x1[p] * c - x2[p] * s;
-        o2[p] = x2[p] * c + x1[p] * s;
-      }
-      st16_stream(dst + e1, Elt<T>::pack(o1));
-      st16_stream(dst + e2, Elt<T>::pack(o2));
-    } else {
-      const int e = j * V;
-      const u32x4 v = ld16_stream(src + e);
-      float x[V], o[V];
-      Elt<T>::unpack(v, x);
-#pragma unroll
-      for (int p = 0; p < V / 2; ++p) {
-        const float c = crow[e / 2 + p];
-        const float s = srow[e / 2 + p];
-        o[2 * p] = x[2 * p] * c - x[2 * p + 1] * s;
-        o[2 * p + 1] = x[2 * p + 1] * c + x[2 * p] * s;
-      }
-      st16_stream(dst + e, Elt<T>::pack(o));
-    }
+  if (f < total) task_rotate_store<T, kInterleaved>(a, k0, v1, v2, cs, sn);
+  for (f += blockDim.x; f < total; f += blockDim.x) {
+    const Task<T> k = task_at<T>(a, tok0, f);
+    task_load<T, kInterleaved>(a, k, v1, v2);
+    task_rotate_store<T, kInterleaved>(a, k, v1, v2, cs, sn);
   }
 }
 
 // Element-wise fallback: a task is one rotation pair.
 template <typename T, typename TabT, bool kTable, bool kInterleaved>
-__global__ __launch_bounds__(kThreads) void rope_generic_kernel(const RopeArgs a) {
+__global__ __launch_bounds__(kMaxThreads) void rope_generic_kernel(const RopeArgs a) {
   extern __shared__ float lds[];
   float* cs = lds;
-  float* sn = lds + kTok * a.half;
-  const int64_t tok0 = (int64_t)blockIdx.x * kTok;
+  float* sn = lds + a.tpb * a.half;
+  const int64_t tok0 = (int64_t)blockIdx.x * a.tpb;
   fill_angles<TabT, kTable>(a, tok0, cs, sn);
   __syncthreads();
-  const int64_t ntok_here = a.ntok - tok0 < kTok ? a.ntok - tok0 : kTok;
+  const int64_t ntok_here = a.ntok - tok0 < a.tpb ? a.ntok - tok0 : a.tpb;
   const int total = (int)ntok_here * a.tasks_per_token;
-  for (int f = threadIdx.x; f < total; f += kThreads) {
-    const int i = (int)fast_div((uint32_t)f, a.tpt_magic);
-    const int r = f - i * a.tasks_per_token;
-    const int hh = (int)fast_div((uint32_t)r, a.tph_magic);
-    const int p = r - hh * a.tasks_per_head;  // pair index
-    const int64_t t = tok0 + i;
-    const int64_t b = t / a.S;
-    const int64_t sq = t - b * a.S;
-    const T* src;
-    T* dst;
-    if (hh < a.Hq) {
-      src = static_cast<const T*>(a.q_in) + b * a.q_in_sb + sq * a.q_in_ss + hh * a.q_in_sh;
-      dst = static_cast<T*>(a.q_out) + b * a.q_out_sb + sq * a.q_out_ss + hh * a.q_out_sh;
-    } else {
-      const int kh = hh - a.Hq;
-      src = static_cast<const T*>(a.k_in) + b * a.k_in_sb + sq * a.k_in_ss + kh * a.k_in_sh;
-      dst = static_cast<T*>(a.k_out) + b * a.k_out_sb + sq * a.k_out_ss + kh * a.k_out_sh;
-    }
+  for (int f = threadIdx.x; f < total; f += blockDim.x) {
+    const Task<T> k = task_at<T>(a, tok0, f);
+    const int p = k.j;  // pair index
     const int e1 = kInterleaved ? 2 * p : p;
     const int e2 = kInterleaved ? 2 * p + 1 : p + a.half;
-    const float x1 = Elt<T>::load1(src + e1);
-    const float x2 = Elt<T>::load1(src + e2);
-    const float c = cs[i * a.half + p];
-    const float s = sn[i * a.half + p];
-    Elt<T>::store1(dst + e1, x1 * c - x2 * s);
-    Elt<T>::store1(dst + e2, x2 * c + x1 * s);
+    const float x1 = Elt<T>::load1(k.src + e1);
+    const float x2 = Elt<T>::load1(k.src + e2);
+    const float c = cs[k.i * a.half + p];
+    const float s = sn[k.i * a.half + p];
+    Elt<T>::store1(k.dst + e1, x1 * c - x2 * s);
+    Elt<T>::store1(k.dst + e2, x2 * c + x1 * s);
   }
 }
 
@@ -209,23 +239,26 @@ ts_status launch_typed(RopeArgs& a, bool vec, hipStream_t st) {
   const int ntask_head = vec ? (kInterleaved ? 2 * a.half / V : a.half / V) : a.half;
   a.tasks_per_head = ntask_head;
   a.tasks_per_token = ntask_head * (a.Hq + a.Hk);
-  // Task indices stay below kTok * tasks_per_token; both divisions must be exact.
-  if (!ts_plan::magic_exact((uint64_t)kTok * a.tasks_per_token, (uint64_t)a.tasks_per_token) ||
+  const ts_plan::RopeBlock blk =
+      ts_plan::rope_block(a.tasks_per_token, a.half, kMaxThreads, kLdsAngles);
+  a.tpb = blk.tpb;
+  // Task indices stay below tpb * tasks_per_token; both divisions must be exact.
+  if (!ts_plan::magic_exact((uint64_t)a.tpb * a.tasks_per_token, (uint64_t)a.tasks_per_token) ||
       !ts_plan::magic_exact((uint64_t)a.tasks_per_token, (uint64_t)a.tasks_per_head))
     return ts_host::fail(TS_ERR_SHAPE,
                          "rope: %d heads x %d tasks per head exceed the kernel's index range",
                          a.Hq + a.Hk, a.tasks_per_head);
   a.tpt_magic = ts_plan::magic_for((uint32_t)a.tasks_per_token);
   a.tph_magic = ts_plan::magic_for((uint32_t)a.tasks_per_head);
-  const dim3 grid((unsigned)((a.ntok + kTok - 1) / kTok));
-  const size_t lds = 2 * sizeof(float) * kTok * a.half;
+  const dim3 grid((unsigned)((a.ntok + a.tpb - 1) / a.tpb));
+  const size_t lds = 2 * sizeof(float) * (size_t)a.tpb * a.half;
   if (vec) {
-    hipLaunchKernelGGL((rope_vec_kernel<T, TabT, kTable, kInterleaved>), grid, dim3(kThreads),
-                       lds, st, a);
+    hipLaunchKernelGGL((rope_vec_kernel<T, TabT, kTable, kInterleaved>), grid,
+                       dim3(blk.threads), lds, st, a);
     return ts_host::check_launch("rope_vec_kernel");
   }
-  hipLaunchKernelGGL((rope_generic_kernel<T, TabT, kTable, kInterleaved>), grid, dim3(kThreads),
-                     lds, st, a);
+  hipLaunchKernelGGL((rope_generic_kernel<T, TabT, kTable, kInterleaved>), grid,
+                     dim3(blk.threads), lds, st, a);
   return ts_host::check_launch("rope_generic_kernel");
 }
 
