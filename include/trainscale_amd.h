@@ -191,6 +191,54 @@ ts_status ts_ce_bwd(const void* logits, int64_t ld, ts_dtype dtype,
                     float logit_scale, float softcap, float label_smoothing,
                     ts_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Fused linear cross-entropy                                                */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Bytes of workspace ts_flce_fwd_bwd needs for hidden [N, H], weight [V, H]
+ * and a token chunk of `chunk` rows (chunk <= 0 or >= N: one chunk), with
+ * (with_grads != 0) or without the backward scratch.
+ */
+size_t ts_flce_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk,
+                              int32_t with_grads);
+
+/*
+ * Loss and gradients of logits = hidden @ weight^T without a library GEMM:
+ *   loss_rows[r] = lse_r - logits[r, labels[r]]   (0 where labels[r] == ignore_index,
+ *                                                   NaN for other labels outside [0, V))
+ *   *loss = sum(loss_rows) * scale,  scale = 1/max(n_valid, 1) (reduction 0, mean)
+ *                                    or 1 (reduction 1, sum)
+ *   grad_hidden = dlogits @ weight,  grad_weight = dlogits^T @ hidden,
+ *   dlogits = (softmax(logits) - onehot(labels)) * scale, 0 on ignored rows,
+ * i.e. the gradients of *loss for an upstream gradient of 1.
+ * hidden, weight, grad_hidden, grad_weight: bf16, row-major, 16-byte aligned,
+ * row strides ldh/ldw (elements, multiples of 8; the gradients are dense).
+ * N, H, V multiples of 8. Logits are formed in fp32 by MFMA and rounded to
+ * bf16 (the rounding a bf16 matmul applies); softmax statistics, lse and loss
+ * are fp32. loss_rows, lse ([N] fp32) may be NULL. grad_hidden and
+ * grad_weight may be NULL (then their GEMM is skipped; both NULL: forward
+ * only). Deterministic: every reduction has a fixed order.
+ * Has no counterpart in the reference, which has no fused linear-CE; it
+ * replaces the composition logits = hidden @ lm_head.t() (rl_training.py:177,
+ * chunked_log_softmax :138-191) followed by cross-entropy
+ * (kernels/triton_kernels.py:427-467) and autograd's matmul backward.
+ */
+ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                          const int64_t* labels, int64_t N, int64_t H, int64_t V,
+                          int64_t ignore_index, int32_t reduction,
+                          float* loss, float* loss_rows, float* lse,
+                          void* grad_hidden, void* grad_weight, int64_t chunk,
+                          void* workspace, size_t workspace_bytes, ts_stream_t stream);
+
+/*
+ * x[i] *= *scale for n bf16 values (n a multiple of 8, x 16-byte aligned);
+ * scale is a device pointer, and when *scale == 1 nothing is written. Used to
+ * apply an upstream gradient other than 1 to ts_flce_fwd_bwd's gradients
+ * without a host synchronisation.
+ */
+ts_status ts_scale_bf16(void* x, int64_t n, const float* scale, ts_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -213,21 +213,33 @@ def ce_bwd(logits: Tensor, labels: Tensor, dloss: Tensor, ignore_index: int = -1
 
 
 def linear_ce(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
-              reduction: str = "mean") -> Tuple[Tensor, Tensor, Tensor]:
+              reduction: str = "mean", bf16_logits: bool = False,
+              return_rows: bool = False):
     """Fused linear cross-entropy as its composition: logits = hidden @ weight.T -> CE.
 
     hidden [N, H], weight [V, H] (the lm_head layout of rl_training.py:156-177),
-    fp32 products. Returns (loss fp32 scalar, grad_hidden, grad_weight) in the
-    input dtypes, for mean (over non-ignored rows) or sum reduction.
+    fp32 products. With bf16_logits the logits are rounded to bf16 as the
+    reference's bf16 matmul rounds them (rl_training.py:177, bf16 operands), the
+    loss is the fp32 CE of those bf16 logits (kernels/triton_kernels.py:328-337),
+    and dlogits are rounded to bf16 as autograd hands them to the bf16 matmul's
+    backward. Returns (loss fp32 scalar, grad_hidden, grad_weight) in the input
+    dtypes for mean (over non-ignored rows) or sum reduction; with return_rows
+    also (loss_rows, lse).
     """
     hidden, weight, labels = _cpu(hidden), _cpu(weight), _cpu(labels).reshape(-1)
     h32, w32 = hidden.float(), weight.float()
     logits = h32 @ w32.t()
-    loss_rows, _ = ce_fwd(logits, labels, ignore_index)
+    if bf16_logits:
+        logits = logits.to(torch.bfloat16).float()
+    loss_rows, lse = ce_fwd(logits, labels, ignore_index)
     n_valid = max(int((labels != ignore_index).sum()), 1)
     scale = 1.0 / n_valid if reduction == "mean" else 1.0
     loss = loss_rows.sum() * scale
     g = ce_bwd(logits, labels, torch.tensor(scale), ignore_index, out_dtype=torch.float32)
+    if bf16_logits:
+        g = g.to(torch.bfloat16).float()
     grad_h = (g @ w32).to(hidden.dtype)
     grad_w = (g.t() @ h32).to(weight.dtype)
+    if return_rows:
+        return loss, grad_h, grad_w, loss_rows, lse
     return loss, grad_h, grad_w

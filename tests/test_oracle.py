@@ -289,3 +289,27 @@ def test_mutation_ce_label_is_caught():
     with pytest.raises(AssertionError):
         assert_ulp(grad_bad, round_to(g["grad"], BF), 1)
     assert n_valid > 1
+
+
+def test_linear_ce_bf16_logits_mode():
+    """bf16_logits restates a bf16 matmul: it agrees with torch's own bf16 matmul
+    within 1 ulp, and equals the fp32 composition when the logits are exact in bf16."""
+    torch.manual_seed(8)
+    N, H, V = 16, 64, 40
+    h = torch.randn(N, H).to(BF)
+    w = (0.1 * torch.randn(V, H)).to(BF)
+    labels = torch.randint(0, V, (N,))
+    labels[3] = -100
+    ref_logits = h @ w.t()  # torch's bf16 matmul (fp32 accumulate, bf16 result)
+    ours = (h.float() @ w.float().t()).to(BF)
+    assert max_ulp(ours, ref_logits) <= 1
+    # exact logits: entries in {-1, 0, 1} x {0, +-0.5, +-1}, H = 16 -> multiples of 0.5 <= 16
+    he = torch.randint(-1, 2, (N, 16)).float().to(BF)
+    we = (torch.randint(-2, 3, (V, 16)).float() / 2).to(BF)
+    a = oracle.linear_ce(he, we, labels, bf16_logits=True)
+    b = oracle.linear_ce(he, we, labels, bf16_logits=False)
+    assert float(a[0]) == float(b[0])
+    # mean vs sum differ exactly by n_valid
+    s = oracle.linear_ce(he, we, labels, reduction="sum", bf16_logits=True)
+    n_valid = int((labels != -100).sum())
+    assert abs(float(s[0]) - n_valid * float(a[0])) <= 1e-4 * abs(float(s[0]))

@@ -1,0 +1,225 @@
+// bf16 MFMA GEMM core for gfx950: C[M, N] = A[M, K] * B[N, K]^T, fp32 accumulation.
+//
+// Both operands are row-major with K contiguous (the layout of hidden [N, H]
+// and of the LM head [V, H]), 16-byte aligned, row strides and K multiples of
+// 8 elements.
+//
+// Workgroup tile 256 x 256, k-block 32, 256 threads = 4 waves in a 2 x 2 grid;
+// each wave owns a 128 x 128 block of C as 4 x 4 tiles of
+// v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane).
+//
+// Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds
+// (no staging registers): a wave's load instruction fills 1 KiB of LDS, lane i
+// at the wave's base + 16 * i. Four LDS stages of 32 KiB (A + B) keep two to
+// three k-blocks of loads in flight while the MFMAs consume one; one barrier
+// per k-block, and the MFMA operand fragments are double-buffered in registers
+// so every LDS read overlaps MFMAs (see mainloop). Buffer resources make
+// out-of-range rows (and the k tail) read as zeros, so partial tiles need no
+// branches.
+//
+// LDS rows are 64 B (32 bf16) with the four 16-byte chunks XOR-swizzled by
+// (row >> 1) & 3, so the ds_read_b128 of 8 consecutive lanes (8 consecutive
+// rows, same logical chunk) hit 8 disjoint groups of banks.
+//
+// MFMA 32x32x16 bf16 lane layout (checked on the device): A lane l holds row
+// l % 32, k = (l / 32) * 8 + e for e < 8; B lane l holds column l % 32 with the
+// same k; accumulator element 4 * i + j is C[8 * i + 4 * (l / 32) + j][l % 32].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.hpp"
+
+namespace ts_gemm {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint32_t* lds_ptr_t;
+
+constexpr int BM = 256;
+constexpr int BN = 256;
+constexpr int BK = 32;
+constexpr int kStages = 4;
+constexpr int kThreads = 256;
+constexpr int kRowBytes = BK * 2;                       // 64
+constexpr int kTileBytes = BM * kRowBytes;              // 16 KiB per operand per stage
+constexpr int kStageBytes = 2 * kTileBytes;             // A + B
+constexpr size_t kLdsBytes = (size_t)kStages * kStageBytes;  // 128 KiB
+constexpr int kLoadsPerWave = BM * kRowBytes / 1024 / 4;      // 1 KiB loads per wave per operand
+constexpr uint32_t kOob = 0x80000000u;  // voffset beyond every resource's range -> reads 0
+
+struct Acc {
+  f32x16 t[4][4];
+};
+
+__device__ void buffer_load_lds(i32x4 rsrc, lds_ptr_t lds, int size, int voffset, int soffset,
+                                int offset, int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+// Raw buffer resource over [base, base + bytes) (gfx9 word 3).
+__device__ inline i32x4 make_rsrc(const void* base, uint64_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 r;
+  r[0] = (int32_t)(uint32_t)a;
+  r[1] = (int32_t)((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = (int32_t)(bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Per-thread byte offsets (relative to the tile's first row) of this lane's
+// loads for logical chunk c of LDS row r: row * ld * 2 + chunk * 16.
+struct TileLoader {
+  i32x4 rsrc;
+  uint32_t off[kLoadsPerWave];  // byte offset of this lane's chunk at k0 = 0
+  int lds_row0;                 // first LDS row of the wave's first load
+};
+
+// Sets up the loads of one operand: rows [row0, row0 + 256) of a [nrows, ld]
+// matrix; out-of-range rows read zeros.
+__device__ inline TileLoader make_loader(const __bf16* g, int64_t ld, int64_t nrows,
+                                         int64_t row0) {
+  TileLoader t;
+  const int wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int64_t valid = nrows - row0;
+  if (valid > BM) valid = BM;
+  if (valid < 0) valid = 0;
+  t.rsrc = make_rsrc(g + row0 * ld, (uint64_t)valid * (uint64_t)ld * 2);
+#pragma unroll
+  for (int u = 0; u < kLoadsPerWave; ++u) {
+    const int row = (u * 4 + wid) * 16 + (lane >> 2);
+    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    t.off[u] = (uint32_t)(row * ld * 2 + chunk * 16);
+  }
+  t.lds_row0 = wid * 16;
+  return t;
+}
+
+// Issues this wave's loads of k-block [k0, k0 + 32) into the LDS tile.
+__device__ inline void issue_loads(const TileLoader& t, int64_t k0, int64_t K, uint8_t* lds_tile) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int u = 0; u < kLoadsPerWave; ++u) {
+    // logical chunk of this lane for the load's row (same swizzle as make_loader)
+    const int row = (u * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
+    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    const bool in_k = k0 + chunk * 8 < K;
+    const uint32_t voff = in_k ? t.off[u] + (uint32_t)(k0 * 2) : kOob;
+    uint8_t* dst = lds_tile + (u * 4 + (threadIdx.x >> 6)) * 16 * kRowBytes;
+    buffer_load_lds(t.rsrc, (lds_ptr_t)dst, 16, (int)voff, 0, 0, 0);
+  }
+}
+
+struct Frags {
+  bf16x8 a[4];
+  bf16x8 b[4];
+};
+
+// Operand fragments of k-step ks (0 or 1) of a staged k-block.
+__device__ inline void read_frags(const uint8_t* As, const uint8_t* Bs, int wm, int wn, int lane,
+                                  int ks, Frags& f) {
+  const int r = lane & 31;
+  const int c = ks * 2 + (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = wm * 128 + i * 32 + r;
+    f.a[i] = *reinterpret_cast<const bf16x8*>(As + row * kRowBytes + ((c ^ ((row >> 1) & 3)) << 4));
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = wn * 128 + j * 32 + r;
+    f.b[j] = *reinterpret_cast<const bf16x8*>(Bs + row * kRowBytes + ((c ^ ((row >> 1) & 3)) << 4));
+  }
+}
+
+__device__ inline void mma_frags(const Frags& f, Acc& acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc.t[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.t[i][j], 0, 0, 0);
+}
+
+// Main loop for the tile at (m0, n0). `smem` holds kLdsBytes (16-byte aligned).
+//
+// Per k-block kt (two 16-deep k-steps):
+//   read fragments (kt, 1)            | MFMAs (kt, 0)
+//   wait for stage kt+1, barrier, issue global loads of stage kt+3 into the
+//   buffer of stage kt-1 (consumed by every wave before the barrier)
+//   read fragments (kt+1, 0)          | MFMAs (kt, 1)
+// so LDS reads always overlap MFMAs of the other fragment set, and global
+// loads run two to three k-blocks ahead.
+__device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64_t M,
+                                const __bf16* __restrict__ B, int64_t ldb, int64_t N, int64_t K,
+                                int64_t m0, int64_t n0, uint8_t* smem, Acc& acc) {
+  const int wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wm = wid >> 1;
+  const int wn = wid & 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc.t[i][j][e] = 0.f;
+
+  const TileLoader la = make_loader(A, lda, M, m0);
+  const TileLoader lb = make_loader(B, ldb, N, n0);
+  const int64_t KT = (K + BK - 1) / BK;
+  constexpr int kPerStage = 2 * kLoadsPerWave;  // loads per wave per stage
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) {
+    if (s < KT) {
+      issue_loads(la, (int64_t)s * BK, K, smem + s * kStageBytes);
+      issue_loads(lb, (int64_t)s * BK, K, smem + s * kStageBytes + kTileBytes);
+    }
+  }
+  // stage 0 landed (stages 1 and 2 may still be in flight)
+  if (KT >= 3) wait_vmcnt<2 * kPerStage>();
+  else if (KT == 2) wait_vmcnt<kPerStage>();
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  Frags f0, f1;
+  read_frags(smem, smem + kTileBytes, wm, wn, lane, 0, f0);
+
+  for (int64_t kt = 0; kt < KT; ++kt) {
+    const uint8_t* As = smem + (kt % kStages) * kStageBytes;
+    read_frags(As, As + kTileBytes, wm, wn, lane, 1, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_frags(f0, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < KT) {
+      // stage kt+1 landed: at most stage kt+2's loads remain in flight
+      if (kt + 2 < KT) wait_vmcnt<kPerStage>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      if (kt + 3 < KT) {
+        const int s = (int)((kt + 3) % kStages);
+        issue_loads(la, (kt + 3) * BK, K, smem + s * kStageBytes);
+        issue_loads(lb, (kt + 3) * BK, K, smem + s * kStageBytes + kTileBytes);
+      }
+      const uint8_t* An = smem + ((kt + 1) % kStages) * kStageBytes;
+      read_frags(An, An + kTileBytes, wm, wn, lane, 0, f0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma_frags(f1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Row / column (within the workgroup tile) of accumulator element e of tile (i, j).
+__device__ inline int acc_row(int wm, int i, int e, int lane) {
+  return wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+}
+__device__ inline int acc_col(int wn, int j, int lane) { return wn * 128 + j * 32 + (lane & 31); }
+
+}  // namespace ts_gemm

@@ -1,0 +1,535 @@
+// Fused linear cross-entropy for gfx950: loss, grad_hidden and grad_weight of
+//   logits = hidden [N, H] @ weight[V, H]^T,  loss = reduce_rows(lse - logits[label])
+// without a library GEMM and without autograd.
+//
+// Token-chunked: for each chunk of Nc rows of hidden,
+//   1. logits GEMM (MFMA, gemm.hpp). Its epilogue rounds the fp32 accumulators
+//      to bf16 (the logits the reference's bf16 matmul produces,
+//      rl_training.py:177), stores them to an [Nc, V] scratch, and from the
+//      same bf16 values writes per (row, 128-column slice) max and sum of
+//      exp, and the logit at the row's label.
+//   2. row statistics -> lse, per-row loss (0 on ignore_index rows).
+//   3. dlogits = (softmax - onehot) * scale in bf16, written over the logits
+//      scratch and transposed into a [V, Nc] scratch (scale = 1/n_valid for
+//      the mean, 1 for the sum).
+//   4. grad_hidden[chunk] = dlogits @ weight   (MFMA, B = weight^T [H, V])
+//   5. grad_weight      += dlogits^T @ hidden  (MFMA, B = hidden^T [H, N]);
+//      with several chunks the sum is carried in fp32 and rounded once.
+// Every reduction has a fixed order, so results are bit-reproducible.
+//
+// Scratch lives in a caller workspace (ts_flce_workspace_size): with one chunk
+// the full [N, V] logits are staged (2.1 GB at N = 8192, V = 128256); the
+// chunk size bounds that at Nc x V x 2 bytes.
+#include <math.h>
+
+#include "common.hpp"
+#include "gemm.hpp"
+
+namespace {
+
+using namespace ts;
+using ts_gemm::Acc;
+using ts_gemm::BM;
+using ts_gemm::BN;
+
+constexpr int kStagePitch = 256;  // bytes per staged epilogue row (128 bf16)
+
+enum EpiMode : int {
+  kEpiLogits = 0,     // bf16 C + row statistics + label logit
+  kEpiBf16 = 1,       // bf16 C
+  kEpiF32 = 2,        // fp32 C32 = acc
+  kEpiAccF32 = 3,     // fp32 C32 += acc
+  kEpiAccBf16 = 4     // bf16 C = C32 + acc
+};
+
+struct GemmArgs {
+  const __bf16* A;
+  int64_t lda;
+  const __bf16* B;
+  int64_t ldb;
+  int64_t M, N, K;
+  __bf16* C;      // bf16 output (modes 0, 1, 4)
+  int64_t ldc;
+  float* C32;     // fp32 accumulator (modes 2, 3, 4)
+  int64_t ldc32;
+  // logits epilogue
+  const int64_t* labels;  // labels of rows [0, M) of this chunk
+  float2* stats;          // [2 * NT][M] (max, sum exp) per 128-column slice
+  float* zlab;            // [M] logit at the label (written by the slice holding it)
+};
+
+// Writes the wave's 128 x 128 accumulator block, rounded to bf16, into its
+// private 32 KiB LDS region as [row][col] with 256-byte rows.
+__device__ inline void stage_bf16(const Acc& acc, uint8_t* region, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int col = j * 32 + (lane & 31);
+        *reinterpret_cast<__bf16*>(region + row * kStagePitch + col * 2) = (__bf16)acc.t[i][j][e];
+      }
+}
+
+template <int kMode>
+__global__ __launch_bounds__(ts_gemm::kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void flce_gemm(const GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[ts_gemm::kLdsBytes];
+  const int64_t MT = (a.M + BM - 1) / BM;
+  const int64_t mt = blockIdx.x % MT;
+  const int64_t nt = blockIdx.x / MT;
+  const int64_t m0 = mt * BM;
+  const int64_t n0 = nt * BN;
+  Acc acc;
+  ts_gemm::mainloop(a.A, a.lda, a.M, a.B, a.ldb, a.N, a.K, m0, n0, smem, acc);
+
+  const int wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wm = wid >> 1;
+  const int wn = wid & 1;
+  const int64_t mb = m0 + wm * 128;  // first row of this wave's block
+  const int64_t nb = n0 + wn * 128;  // first column
+
+  if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t r = mb + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+          const int64_t c = nb + j * 32 + (lane & 31);
+          if (r < a.M && c < a.N) {
+            float* p = a.C32 + r * a.ldc32 + c;
+            *p = kMode == kEpiAccF32 ? *p + acc.t[i][j][e] : acc.t[i][j][e];
+          }
+        }
+    return;
+  } else {
+    if constexpr (kMode == kEpiAccBf16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int64_t r = mb + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const int64_t c = nb + j * 32 + (lane & 31);
+            if (r < a.M && c < a.N) acc.t[i][j][e] += a.C32[r * a.ldc32 + c];
+          }
+    }
+    // Every wave is done with the pipeline's LDS before it is reused.
+    __syncthreads();
+    uint8_t* region = smem + wid * (128 * kStagePitch);
+    stage_bf16(acc, region, lane);
+    // The wave reads back only its own region: LDS operations of one wave
+    // complete in order, so no barrier is needed here.
+    const int c16 = lane & 15;  // 16-byte chunk of the 256-byte row
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+      const int lrow = it * 4 + (lane >> 4);
+      const int64_t gm = mb + lrow;
+      const int64_t gc = nb + c16 * 8;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(region + lrow * kStagePitch + c16 * 16);
+      const bool in = gm < a.M && gc < a.N;  // N % 8 == 0: a chunk is all in or all out
+      if (in) st16(a.C + gm * a.ldc + gc, v);
+      if constexpr (kMode == kEpiLogits) {
+        float f[8];
+        Elt<__bf16>::unpack(v, f);
+        float lm = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) lm = in ? fmaxf(lm, f[q]) : lm;
+        const float m = row_max(lm);  // over the 16 lanes of this row
+        float ls = 0.f;
+        if (in) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) ls += fast_exp2((f[q] - m) * kLog2e);
+        }
+        const float s = row_sum(ls);
+        if (gm < a.M) {
+          if (c16 == 0) a.stats[(nt * 2 + wn) * a.M + gm] = make_float2(m, s);
+          const int64_t lab = a.labels[gm];
+          if (in && lab >= gc && lab < gc + 8) a.zlab[gm] = f[lab - gc];
+        }
+      }
+    }
+  }
+}
+
+// n_valid = #labels != ignore_index over all N rows (one workgroup, fixed order).
+__global__ __launch_bounds__(256) void flce_count(const int64_t* __restrict__ labels, int64_t N,
+                                                  int64_t ignore_index, int* __restrict__ n_valid) {
+  __shared__ float red[4];
+  float c = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += 256) c += labels[i] != ignore_index ? 1.f : 0.f;
+  c = block_sum<4>(c, red);
+  if (threadIdx.x == 0) *n_valid = (int)c;
+}
+
+// Per row of a chunk: lse from the slice statistics, loss = lse - z[label].
+__global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stats, int64_t nparts,
+                                                 const float* __restrict__ zlab,
+                                                 const int64_t* __restrict__ labels, int64_t M,
+                                                 int64_t V, int64_t ignore_index,
+                                                 float* __restrict__ lse_out,
+                                                 float* __restrict__ loss_rows) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= M) return;
+  float m = -INFINITY;
+  for (int64_t p = 0; p < nparts; ++p) m = fmaxf(m, stats[p * M + r].x);
+  float s = 0.f;
+  for (int64_t p = 0; p < nparts; ++p) {
+    const float2 st = stats[p * M + r];
+    s += st.y == 0.f ? 0.f : st.y * fast_exp2((st.x - m) * kLog2e);
+  }
+  const float l = m + logf(s);
+  const int64_t lab = labels[r];
+  float out;
+  if (lab == ignore_index) out = 0.f;
+  else if (lab < 0 || lab >= V) out = __builtin_nanf("");
+  else out = l - zlab[r];
+  lse_out[r] = l;
+  loss_rows[r] = out;
+}
+
+// loss = scale * sum(loss_rows) over all N rows (one workgroup, fixed order);
+// scale = 1/max(n_valid, 1) for the mean, 1 for the sum. Also stores the scale.
+__global__ __launch_bounds__(256) void flce_loss(const float* __restrict__ loss_rows, int64_t N,
+                                                 const int* __restrict__ n_valid, int mean,
+                                                 float* __restrict__ loss,
+                                                 float* __restrict__ scale_out) {
+  __shared__ float red[4];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < N; i += 256) s += loss_rows[i];
+  s = block_sum<4>(s, red);
+  if (threadIdx.x == 0) {
+    const float scale = mean ? 1.f / (float)(*n_valid > 0 ? *n_valid : 1) : 1.f;
+    *loss = s * scale;
+    *scale_out = scale;
+  }
+}
+
+// dlogits of a chunk, 64 x 64 tiles: D = (exp(z - lse) - onehot) * scale in
+// bf16, written over the logits [M, V] and transposed into Dt [V, M].
+__global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int64_t ldl,
+                                                    __bf16* __restrict__ Dt, int64_t lddt,
+                                                    const float* __restrict__ lse,
+                                                    const int64_t* __restrict__ labels,
+                                                    int64_t M, int64_t V, int64_t ignore_index,
+                                                    const float* __restrict__ scale_p) {
+  __shared__ __bf16 tile[64][64 + 8];  // [v][m]
+  const int64_t v0 = (int64_t)blockIdx.x * 64;
+  const int64_t r0 = (int64_t)blockIdx.y * 64;
+  const float scale = *scale_p;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int q = threadIdx.x + 256 * h;  // 512 chunks of 8
+    const int lr = q >> 3;
+    const int lc = (q & 7) * 8;
+    const int64_t r = r0 + lr;
+    const int64_t c = v0 + lc;
+    float g[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (r < M && c < V) {
+      const int64_t lab = labels[r];
+      __bf16* p = L + r * ldl + c;
+      if (lab != ignore_index) {
+        float z[8];
+        Elt<__bf16>::unpack(ld16(p), z);
+        const float l2 = lse[r] * kLog2e;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pr = fast_exp2(__builtin_fmaf(z[e], kLog2e, -l2));
+          g[e] = scale * (c + e == lab ? pr - 1.f : pr);
+        }
+      }
+      st16(p, Elt<__bf16>::pack(g));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[lc + e][lr] = (__bf16)g[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int q = threadIdx.x + 256 * h;
+    const int lv = q >> 3;
+    const int lm = (q & 7) * 8;
+    const int64_t vv = v0 + lv;
+    const int64_t mm = r0 + lm;
+    if (vv < V && mm < M) {
+      // M % 8 == 0: the 8 rows of a chunk are all in range together
+      st16(Dt + vv * lddt + mm, *reinterpret_cast<const u32x4*>(&tile[lv][lm]));
+    }
+  }
+}
+
+// out[c][r] = in[r][c] for a bf16 [R, C] matrix, 64 x 64 tiles; R, C multiples of 8.
+__global__ __launch_bounds__(256) void transpose_bf16(const __bf16* __restrict__ in, int64_t ldi,
+                                                      __bf16* __restrict__ out, int64_t ldo,
+                                                      int64_t R, int64_t C) {
+  __shared__ __bf16 tile[64][64 + 8];  // [c][r]
+  const int64_t c0 = (int64_t)blockIdx.x * 64;
+  const int64_t r0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int q = threadIdx.x + 256 * h;
+    const int lr = q >> 3;
+    const int lc = (q & 7) * 8;
+    float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (r0 + lr < R && c0 + lc < C) Elt<__bf16>::unpack(ld16(in + (r0 + lr) * ldi + c0 + lc), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[lc + e][lr] = (__bf16)f[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int q = threadIdx.x + 256 * h;
+    const int lc = q >> 3;
+    const int lr = (q & 7) * 8;
+    if (c0 + lc < C && r0 + lr < R)
+      st16(out + (c0 + lc) * ldo + r0 + lr, *reinterpret_cast<const u32x4*>(&tile[lc][lr]));
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_zero_u32(uint32_t* __restrict__ p, int64_t n,
+                                                     float* __restrict__ loss) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+  if (i == 0 && loss != nullptr) *loss = 0.f;
+}
+
+// x[i] *= *scale unless *scale == 1 (then the kernel only reads the scalar).
+__global__ __launch_bounds__(256) void scale_bf16(__bf16* __restrict__ x, int64_t nvec,
+                                                  const float* __restrict__ scale_p) {
+  const float s = *scale_p;
+  if (s == 1.f) return;
+  for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < nvec;
+       v += (int64_t)gridDim.x * 256) {
+    float f[8];
+    Elt<__bf16>::unpack(ld16(x + v * 8), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] *= s;
+    st16(x + v * 8, Elt<__bf16>::pack(f));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+struct Layout {
+  int64_t chunk, nchunks, nparts;
+  size_t off_logits, off_dt, off_wt, off_ht, off_stats, off_zlab, off_lse, off_rows, off_misc,
+      off_acc, total;
+};
+
+Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
+  Layout l{};
+  l.chunk = chunk <= 0 || chunk >= N ? round_up(N, 8) : round_up(chunk, 256);
+  if (l.chunk > round_up(N, 8)) l.chunk = round_up(N, 8);
+  l.nchunks = (N + l.chunk - 1) / l.chunk;
+  l.nparts = 2 * ((V + BN - 1) / BN);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  l.off_logits = take((size_t)l.chunk * V * 2);
+  l.off_dt = grads ? take((size_t)V * l.chunk * 2) : 0;
+  l.off_wt = grads ? take((size_t)H * V * 2) : 0;
+  l.off_ht = grads ? take((size_t)H * N * 2) : 0;
+  l.off_stats = take((size_t)l.nparts * l.chunk * sizeof(float2));
+  l.off_zlab = take((size_t)N * 4);
+  l.off_lse = take((size_t)N * 4);
+  l.off_rows = take((size_t)N * 4);
+  l.off_misc = take(64);
+  l.off_acc = grads && l.nchunks > 1 ? take((size_t)V * H * 4) : 0;
+  l.total = off;
+  return l;
+}
+
+template <int kMode>
+ts_status launch_gemm(const GemmArgs& a, hipStream_t st, const char* name) {
+  const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  if (tiles <= 0) return TS_OK;
+  if (tiles > 0x7fffffffLL) return ts_host::fail(TS_ERR_SHAPE, "%s: too many tiles", name);
+  hipLaunchKernelGGL((flce_gemm<kMode>), dim3((unsigned)tiles), dim3(ts_gemm::kThreads), 0, st, a);
+  return ts_host::check_launch(name);
+}
+
+ts_status launch_transpose(const __bf16* in, int64_t ldi, __bf16* out, int64_t ldo, int64_t R,
+                           int64_t C, hipStream_t st) {
+  const dim3 grid((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64));
+  hipLaunchKernelGGL(transpose_bf16, grid, dim3(256), 0, st, in, ldi, out, ldo, R, C);
+  return ts_host::check_launch("transpose_bf16");
+}
+
+}  // namespace
+
+#define TS_TRY(x)                  \
+  do {                             \
+    const ts_status s_ = (x);      \
+    if (s_ != TS_OK) return s_;    \
+  } while (0)
+
+extern "C" size_t ts_flce_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk,
+                                         int32_t with_grads) {
+  if (N <= 0 || H <= 0 || V <= 0) return 0;
+  return layout(N, H, V, chunk, with_grads != 0).total;
+}
+
+extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight,
+                                     int64_t ldw, const int64_t* labels, int64_t N, int64_t H,
+                                     int64_t V, int64_t ignore_index, int32_t reduction,
+                                     float* loss, float* loss_rows, float* lse,
+                                     void* grad_hidden, void* grad_weight, int64_t chunk,
+                                     void* workspace, size_t workspace_bytes,
+                                     ts_stream_t stream) {
+  using ts_host::fail;
+  if (N < 0 || H <= 0 || V <= 0)
+    return fail(TS_ERR_SHAPE, "flce: bad shape N=%lld H=%lld V=%lld", (long long)N, (long long)H,
+                (long long)V);
+  if (N % 8 != 0 || H % 8 != 0 || V % 8 != 0)
+    return fail(TS_ERR_SHAPE, "flce: N, H and V must be multiples of 8 (N=%lld H=%lld V=%lld)",
+                (long long)N, (long long)H, (long long)V);
+  if (ldh < H || ldw < H || ldh % 8 != 0 || ldw % 8 != 0)
+    return fail(TS_ERR_SHAPE, "flce: row strides must be >= H and multiples of 8");
+  // 32-bit buffer offsets per 256-row tile, and 64-row tile grids within 65535 in y
+  if (V > ((int64_t)1 << 22) || H > ((int64_t)1 << 20) || N > ((int64_t)1 << 22))
+    return fail(TS_ERR_SHAPE, "flce: shape beyond the kernel's index range");
+  if (reduction != 0 && reduction != 1)
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce: reduction must be 0 (mean) or 1 (sum)");
+  if (loss == nullptr) return fail(TS_ERR_INVALID_ARGUMENT, "flce: loss is NULL");
+  if (N > 0 && (hidden == nullptr || weight == nullptr || labels == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce: hidden, weight or labels is NULL");
+  if (!ts_host::aligned16(hidden) || !ts_host::aligned16(weight) ||
+      (grad_hidden != nullptr && !ts_host::aligned16(grad_hidden)) ||
+      (grad_weight != nullptr && !ts_host::aligned16(grad_weight)))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce: tensors must be 16-byte aligned");
+  const bool grads = grad_hidden != nullptr || grad_weight != nullptr;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (N == 0) {
+    // no rows: loss 0, grad_weight 0 (grad_hidden is empty); no workspace needed
+    const int64_t words = grad_weight != nullptr ? V * H / 2 : 1;
+    hipLaunchKernelGGL(fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                       grad_weight != nullptr ? static_cast<uint32_t*>(grad_weight) : nullptr,
+                       grad_weight != nullptr ? words : 0, loss);
+    return ts_host::check_launch("fill_zero_u32");
+  }
+  const Layout lay = layout(N, H, V, chunk, grads);
+  if (workspace == nullptr || workspace_bytes < lay.total || !ts_host::aligned16(workspace))
+    return fail(TS_ERR_WORKSPACE, "flce: workspace needs %zu bytes (16-byte aligned), got %zu",
+                lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  __bf16* Lc = reinterpret_cast<__bf16*>(ws + lay.off_logits);
+  __bf16* Dt = reinterpret_cast<__bf16*>(ws + lay.off_dt);
+  __bf16* Wt = reinterpret_cast<__bf16*>(ws + lay.off_wt);
+  __bf16* Ht = reinterpret_cast<__bf16*>(ws + lay.off_ht);
+  float2* stats = reinterpret_cast<float2*>(ws + lay.off_stats);
+  float* zlab = reinterpret_cast<float*>(ws + lay.off_zlab);
+  float* lse_ws = lse != nullptr ? lse : reinterpret_cast<float*>(ws + lay.off_lse);
+  float* rows_ws = loss_rows != nullptr ? loss_rows : reinterpret_cast<float*>(ws + lay.off_rows);
+  int* n_valid = reinterpret_cast<int*>(ws + lay.off_misc);
+  float* scale = reinterpret_cast<float*>(ws + lay.off_misc + 16);
+  float* acc32 = reinterpret_cast<float*>(ws + lay.off_acc);
+  const __bf16* Hd = static_cast<const __bf16*>(hidden);
+  const __bf16* Wd = static_cast<const __bf16*>(weight);
+
+  hipLaunchKernelGGL(flce_count, dim3(1), dim3(256), 0, st, labels, N, ignore_index, n_valid);
+  TS_TRY(ts_host::check_launch("flce_count"));
+  if (grads) {
+    TS_TRY(launch_transpose(Wd, ldw, Wt, V, V, H, st));  // Wt [H, V]
+    TS_TRY(launch_transpose(Hd, ldh, Ht, N, N, H, st));  // Ht [H, N]
+  }
+  // Pass 1 over chunks: logits, statistics, per-row loss (and lse).
+  // With gradients the dlogits of a chunk are consumed right away, so the
+  // loss scale (which needs every row's label) is computed up front.
+  if (grads) {
+    hipLaunchKernelGGL(flce_loss, dim3(1), dim3(256), 0, st, rows_ws, (int64_t)0, n_valid,
+                       reduction == 0 ? 1 : 0, loss, scale);
+    TS_TRY(ts_host::check_launch("flce_loss"));
+  }
+  for (int64_t c = 0; c < lay.nchunks; ++c) {
+    const int64_t r0 = c * lay.chunk;
+    const int64_t Mc = N - r0 < lay.chunk ? N - r0 : lay.chunk;
+    GemmArgs g{};
+    g.A = Hd + r0 * ldh;
+    g.lda = ldh;
+    g.B = Wd;
+    g.ldb = ldw;
+    g.M = Mc;
+    g.N = V;
+    g.K = H;
+    g.C = Lc;
+    g.ldc = V;
+    g.labels = labels + r0;
+    g.stats = stats;
+    g.zlab = zlab + r0;
+    TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_gemm_logits"));
+    hipLaunchKernelGGL(flce_rows, dim3((unsigned)((Mc + 255) / 256)), dim3(256), 0, st, stats,
+                       lay.nparts, zlab + r0, labels + r0, Mc, V, ignore_index, lse_ws + r0,
+                       rows_ws + r0);
+    TS_TRY(ts_host::check_launch("flce_rows"));
+    if (!grads) continue;
+    const dim3 dgrid((unsigned)((V + 63) / 64), (unsigned)((Mc + 63) / 64));
+    hipLaunchKernelGGL(flce_dlogits, dgrid, dim3(256), 0, st, Lc, V, Dt, Mc, lse_ws + r0,
+                       labels + r0, Mc, V, ignore_index, scale);
+    TS_TRY(ts_host::check_launch("flce_dlogits"));
+    if (grad_hidden != nullptr) {
+      GemmArgs d{};
+      d.A = Lc;  // dlogits [Mc, V]
+      d.lda = V;
+      d.B = Wt;  // weight^T [H, V]
+      d.ldb = V;
+      d.M = Mc;
+      d.N = H;
+      d.K = V;
+      d.C = static_cast<__bf16*>(grad_hidden) + r0 * H;
+      d.ldc = H;
+      TS_TRY(launch_gemm<kEpiBf16>(d, st, "flce_gemm_dhidden"));
+    }
+    if (grad_weight != nullptr) {
+      GemmArgs d{};
+      d.A = Dt;       // dlogits^T [V, Mc]
+      d.lda = Mc;
+      d.B = Ht + r0;  // hidden^T [H, N], columns r0 .. r0 + Mc
+      d.ldb = N;
+      d.M = V;
+      d.N = H;
+      d.K = Mc;
+      d.C = static_cast<__bf16*>(grad_weight);
+      d.ldc = H;
+      d.C32 = acc32;
+      d.ldc32 = H;
+      if (lay.nchunks == 1) {
+        TS_TRY(launch_gemm<kEpiBf16>(d, st, "flce_gemm_dweight"));
+      } else if (c == 0) {
+        TS_TRY(launch_gemm<kEpiF32>(d, st, "flce_gemm_dweight"));
+      } else if (c + 1 < lay.nchunks) {
+        TS_TRY(launch_gemm<kEpiAccF32>(d, st, "flce_gemm_dweight"));
+      } else {
+        TS_TRY(launch_gemm<kEpiAccBf16>(d, st, "flce_gemm_dweight"));
+      }
+    }
+  }
+  hipLaunchKernelGGL(flce_loss, dim3(1), dim3(256), 0, st, rows_ws, N, n_valid,
+                     reduction == 0 ? 1 : 0, loss, scale);
+  return ts_host::check_launch("flce_loss");
+}
+
+extern "C" ts_status ts_scale_bf16(void* x, int64_t n, const float* scale, ts_stream_t stream) {
+  if (n < 0 || n % 8 != 0)
+    return ts_host::fail(TS_ERR_SHAPE, "scale_bf16: n must be a non-negative multiple of 8");
+  if (n > 0 && (x == nullptr || scale == nullptr || !ts_host::aligned16(x)))
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "scale_bf16: bad pointer");
+  if (n == 0) return TS_OK;
+  const int64_t nvec = n / 8;
+  int64_t blocks = (nvec + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(scale_bf16, dim3((unsigned)blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<__bf16*>(x), nvec, scale);
+  return ts_host::check_launch("scale_bf16");
+}

@@ -1,34 +1,138 @@
-"""Fused linear cross-entropy: loss of (hidden @ weight.T) without materialising the logits.
+"""Fused linear cross-entropy: loss of (hidden @ weight.T) without materialising all logits.
 
 TrainScale has no such op; its nearest relative is
 ``chunked_log_softmax(hidden, lm_head[V, H], input_ids)`` (rl_training.py:138-191),
-whose weight layout and softcap/scale keywords this API follows.
+whose weight layout this API follows, with the keywords of
+``fast_cross_entropy_loss`` (kernels/triton_kernels.py:427-467).
+
+One call of the gfx950 kernel (``ts_flce_fwd_bwd``) computes the loss and both
+gradients for an upstream gradient of 1, token chunk by token chunk (a chunk's
+bf16 logits are the only [rows, V] scratch). The forward keeps the gradients;
+the backward scales them in place by the upstream gradient on the device
+(nothing is written when it is 1). Numerics follow the reference's bf16 path:
+logits are rounded to bf16 as a bf16 matmul rounds them, softmax statistics
+and the loss are fp32, dlogits are bf16, and the gradient GEMMs accumulate in
+fp32.
 """
 from __future__ import annotations
+
+from typing import Optional
 
 import torch
 from torch import Tensor
 
-__all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy"]
+from .. import _lib
+from .._lib import check, ptr
+
+__all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy", "DEFAULT_LOGITS_SCRATCH"]
+
+# Upper bound on the bf16 logits scratch of one token chunk.
+DEFAULT_LOGITS_SCRATCH = 1 << 30
+
+_REDUCTIONS = {"mean": 0, "sum": 1}
+
+
+def _chunk_rows(N: int, V: int, chunk_tokens: Optional[int]) -> int:
+    if chunk_tokens is not None:
+        return int(chunk_tokens)
+    rows = DEFAULT_LOGITS_SCRATCH // (2 * V)
+    rows = max(256, rows // 256 * 256)
+    return 0 if rows >= N else rows
+
+
+def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
+                               ignore_index: int = -100, reduction: str = "mean",
+                               need_grad_hidden: bool = True, need_grad_weight: bool = True,
+                               chunk_tokens: Optional[int] = None):
+    """Runs ts_flce_fwd_bwd; returns (loss fp32 0-d, loss_rows [N], lse [N],
+    grad_hidden or None, grad_weight or None) for an upstream gradient of 1."""
+    dev = _lib.require_gpu("fused_linear_cross_entropy", hidden, weight, labels)
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("fused_linear_cross_entropy: hidden and weight must be bfloat16")
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError(f"fused_linear_cross_entropy: hidden {tuple(hidden.shape)} and weight "
+                         f"{tuple(weight.shape)} must be [N, H] and [V, H]")
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f"fused_linear_cross_entropy: reduction must be 'mean' or 'sum', "
+                         f"got {reduction!r}")
+    if hidden.stride(1) != 1 or (hidden.shape[0] > 1 and hidden.stride(0) % 8 != 0):
+        hidden = hidden.contiguous()
+    if weight.stride(1) != 1 or (weight.shape[0] > 1 and weight.stride(0) % 8 != 0):
+        weight = weight.contiguous()
+    N, H = hidden.shape
+    V = weight.shape[0]
+    labels = labels.reshape(-1)
+    if labels.shape[0] != N:
+        raise ValueError(f"fused_linear_cross_entropy: {labels.shape[0]} labels for {N} rows")
+    labels = labels.to(torch.int64).contiguous()
+    ldh = hidden.stride(0) if N > 1 else H
+    ldw = weight.stride(0) if V > 1 else H
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    loss_rows = torch.empty((N,), dtype=torch.float32, device=dev)
+    lse = torch.empty((N,), dtype=torch.float32, device=dev)
+    gh = torch.empty((N, H), dtype=torch.bfloat16, device=dev) if need_grad_hidden else None
+    gw = torch.empty((V, H), dtype=torch.bfloat16, device=dev) if need_grad_weight else None
+    chunk = _chunk_rows(N, V, chunk_tokens)
+    lib = _lib.load()
+    grads = gh is not None or gw is not None
+    ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk, int(grads)))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.ts_flce_fwd_bwd(
+            ptr(hidden), ldh, ptr(weight), ldw, ptr(labels), N, H, V, int(ignore_index),
+            _REDUCTIONS[reduction], ptr(loss), ptr(loss_rows), ptr(lse), ptr(gh), ptr(gw),
+            chunk, ptr(ws), ws_bytes, _lib.stream_handle(dev)), "ts_flce_fwd_bwd")
+    return loss, loss_rows, lse, gh, gw
+
+
+def _scale_(t: Optional[Tensor], scale: Tensor) -> None:
+    if t is None or t.numel() == 0:
+        return
+    lib = _lib.load()
+    with torch.cuda.device(t.device):
+        check(lib.ts_scale_bf16(ptr(t), t.numel(), ptr(scale), _lib.stream_handle(t.device)),
+              "ts_scale_bf16")
 
 
 class LinearCrossEntropyFunction(torch.autograd.Function):
-    """Placeholder until the MFMA kernel lands; raises instead of falling back."""
+    """loss = CE(hidden @ weight.T, labels) with the gradients formed in the forward."""
 
     @staticmethod
     def forward(ctx, hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
-                reduction: str = "mean") -> Tensor:
-        raise NotImplementedError("fused linear cross-entropy kernel is not built yet")
+                reduction: str = "mean", chunk_tokens: Optional[int] = None) -> Tensor:
+        shape = hidden.shape
+        h2 = hidden.reshape(-1, shape[-1])
+        loss, _, _, gh, gw = linear_ce_forward_backward(
+            h2, weight, labels, ignore_index, reduction,
+            need_grad_hidden=ctx.needs_input_grad[0], need_grad_weight=ctx.needs_input_grad[1],
+            chunk_tokens=chunk_tokens)
+        ctx.hidden_shape = shape
+        ctx.save_for_backward(gh, gw)
+        return loss
 
     @staticmethod
-    def backward(ctx, grad_output: Tensor):  # pragma: no cover
-        raise NotImplementedError
+    def backward(ctx, grad_output: Tensor):
+        gh, gw = ctx.saved_tensors
+        scale = grad_output.detach().float().reshape(1).contiguous()
+        _scale_(gh, scale)
+        _scale_(gw, scale)
+        gh = gh.view(ctx.hidden_shape) if gh is not None else None
+        return gh, gw, None, None, None, None
 
 
 def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
                                ignore_index: int = -100, reduction: str = "mean",
                                logit_softcapping: float = 0.0,
-                               logit_scaling: float = 0.0) -> Tensor:
+                               logit_scaling: float = 0.0,
+                               chunk_tokens: Optional[int] = None) -> Tensor:
+    """Mean (or sum) cross-entropy of hidden @ weight.T against labels.
+
+    hidden [..., H] and weight [V, H] in bfloat16 (the lm_head layout of
+    rl_training.py:156-162); labels [...] int64 with ignore_index rows skipped.
+    """
     if logit_softcapping != 0.0 or logit_scaling != 0.0:
-        raise NotImplementedError("softcap/scale are not supported by fused linear CE yet")
-    return LinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index, reduction)
+        raise NotImplementedError(
+            "fused_linear_cross_entropy: logit softcapping/scaling are not implemented by the "
+            "fused kernel; apply them with fast_cross_entropy_loss on explicit logits")
+    return LinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index, reduction,
+                                            chunk_tokens)
