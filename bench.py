@@ -1,18 +1,24 @@
 """Benchmark of the fused kernel layer on one MI355X.
 
-One step = forward of C1 (RMSNorm x[8,2048,4096]), C2 (RoPE Q[8,2048,32,128] +
-K[8,2048,8,128], theta 500000, in-register sin/cos) and C3 (cross-entropy over
-logits[16384,128256] with 10% ignored labels), then their backwards in reverse
-order (C3, C2, C1), as a training step runs them. Between the forward and the
-backward of one op the other ops move gigabytes, so no op re-reads its inputs
-from the 256 MB last-level cache. All inputs are synthetic, seeded and resident
-in HBM before timing.
+Headline step (the metric's value): forward of C1 (RMSNorm x[8,2048,4096]),
+C2 (RoPE Q[8,2048,32,128] + K[8,2048,8,128], theta 500000, in-register sin/cos)
+and C3 (cross-entropy over logits[16384,128256] with 10% ignored labels), then
+their backwards in reverse order (C3, C2, C1), as a training step runs them.
+Between the forward and the backward of one op the other ops move gigabytes,
+so no op re-reads its inputs from the 256 MB last-level cache. All inputs are
+synthetic, seeded and resident in HBM before timing.
 
-value = algorithmic bytes of the step / step time (GB/s); the roofline object is
-computed for the dominant kernel from HIP-event durations taken on torch's
-current stream (the stream every kernel is launched on).
+value = algorithmic bytes of the step / step time (GB/s). The roofline object is
+for the dominant kernel of the step, from HIP-event durations taken on torch's
+current stream (the stream every kernel is launched on); its `traffic` is the
+HBM bytes per launch that rocprofv3 --pmc measured (profiles/pmc_traffic.txt).
+
+Also reported, outside the timed step: C4 (packed varlen RMSNorm + RoPE with
+position_ids at 70B shapes, GB/s) and C5 (fused linear cross-entropy, TFLOP/s
+against the bf16 MFMA peak), each with its own timing.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--no-extra] [--copy-probe]
 """
 from __future__ import annotations
 
@@ -30,6 +36,7 @@ if str(ROOT) not in sys.path:
 
 METRIC = "achieved HBM GB/s (% of 8TB/s) for RMSNorm/RoPE/CE fwd+bwd at 8B shapes"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse():
@@ -38,6 +45,7 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true", help="skip the C4 and C5 sections")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="approximate CPU time budget of the baseline sample")
     p.add_argument("--copy-probe", action="store_true",
@@ -47,14 +55,19 @@ def parse():
 
 
 def load_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 --pmc summary."""
-    f = ROOT / "profiles" / "ce_bwd_c3_pmc.json"
+    """{kernel: HBM bytes per launch} from the committed rocprofv3 --pmc summary."""
+    f = ROOT / "profiles" / "pmc_traffic.txt"
+    out = {}
     if not f.exists():
-        return None
-    try:
-        return json.loads(f.read_text())
-    except Exception:
-        return None
+        return out
+    for line in f.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "hbm_bytes_per_launch":
+            try:
+                out[parts[1]] = int(parts[2])
+            except ValueError:
+                pass
+    return out
 
 
 def cpu_baseline(budget_s: float):
@@ -117,6 +130,147 @@ def cpu_baseline(budget_s: float):
     }
 
 
+def cpu_baseline_linear_ce(budget_s: float):
+    """The oracle's linear CE (fp32 matmuls + CE) on 64 tokens of C5, in TFLOP/s."""
+    import torch
+
+    import oracle
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(4)
+    n, h, v = 64, 4096, 128256
+    hid = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    wt = (0.02 * torch.randn(v, h, generator=g)).to(torch.bfloat16)
+    lab = torch.randint(0, v, (n,), generator=g)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        oracle.linear_ce(hid, wt, lab, bf16_logits=True)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
+            break
+    times.sort()
+    t = times[len(times) // 2]
+    flops = 3 * 2 * n * h * v
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle linear_ce fwd+bwd on 64 tokens of C5 (H 4096, V 128256); "
+                      f"median of {len(times)} runs, {t:.2f} s per sample"}
+
+
+def time_ms(fn, steps: int, warmup: int) -> float:
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
+
+
+def bench_packed(dev, steps: int, warmup: int):
+    """C4: packed varlen RMSNorm [32768, 8192] and RoPE (64q + 8k heads) with position_ids."""
+    import torch
+
+    from trainscale_amd import ops
+    from trainscale_amd import workloads as W
+    from trainscale_amd.kernels.rope_kernels import _base_inv_freq
+
+    c4 = W.packed_workload(dev)
+    t = c4.tensors
+    x2d, ldx = ops.as_rows(t["x"])
+    dy2d, lddy = ops.as_rows(t["dy"])
+    q, k, dq, dk, pos = t["q"], t["k"], t["dq"], t["dk"], t["position_ids"]
+    inv = _base_inv_freq(c4.params["theta"], 128, "cpu")
+    qo, ko, dqo, dko = (torch.empty_like(a) for a in (q, k, dq, dk))
+    state = {}
+
+    def norm_fwd():
+        state["y"], state["rstd"] = ops.rmsnorm_forward(x2d, ldx, t["w"], 1e-6)
+
+    norm_fwd()
+
+    def norm_bwd():
+        ops.rmsnorm_backward(dy2d, lddy, x2d, ldx, t["w"], state["rstd"], need_dw=True)
+
+    def rope_fwd():
+        ops.rope_apply(q, qo, k, ko, inv_freq=inv, position_ids=pos)
+
+    def rope_bwd():
+        ops.rope_apply(dq, dqo, dk, dko, inv_freq=inv, position_ids=pos, backward=True)
+
+    T, Hd = x2d.shape
+    nb = W.rmsnorm_bytes(T, Hd)
+    rb = W.rope_bytes(T, q.shape[2] + k.shape[2], 128, pos_bytes=T * 8)
+    res = {}
+    for name, fn, b in (("rmsnorm_fwd", norm_fwd, nb["fwd"]), ("rmsnorm_bwd", norm_bwd, nb["bwd"]),
+                        ("rope_fwd", rope_fwd, rb["fwd"]), ("rope_bwd", rope_bwd, rb["bwd"])):
+        ms = time_ms(fn, steps, warmup)
+        gbs = b / (ms * 1e-3) / 1e9
+        res[name] = {"ms": round(ms, 4), "bytes": b, "GB_s": round(gbs, 1),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    tot_b = sum(v["bytes"] for v in res.values())
+    tot_ms = sum(v["ms"] for v in res.values())
+    return {"workload": ("C4 packed varlen: 32768 tokens, docs U[64,4096], position_ids reset per "
+                         "doc; RMSNorm H 8192; RoPE 64q+8k heads x 128, theta 5e5 in-register"),
+            "GB_s": round(tot_b / (tot_ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round(tot_b / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "ms": round(tot_ms, 4), "tokens_per_s": round(T / (tot_ms * 1e-3), 1),
+            "kernels": res}
+
+
+def bench_linear_ce(dev, steps: int, warmup: int, cpu: bool, cpu_seconds: float):
+    """C5: fused linear CE fwd+bwd (loss, grad_hidden, grad_weight) in one call."""
+    import torch
+
+    from trainscale_amd import _lib
+    from trainscale_amd import workloads as W
+    from trainscale_amd.loss.linear_ce import _chunk_rows
+
+    c5 = W.linear_ce_workload(dev)
+    h, w, labels = c5.tensors["hidden"], c5.tensors["weight"], c5.tensors["labels"]
+    N, H = h.shape
+    V = w.shape[0]
+    lib = _lib.load()
+    chunk = _chunk_rows(N, V, None)
+    ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk, 1))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    rows = torch.empty((N,), dtype=torch.float32, device=dev)
+    lse = torch.empty((N,), dtype=torch.float32, device=dev)
+    gh = torch.empty_like(h)
+    gw = torch.empty_like(w)
+    stream = _lib.stream_handle(dev)
+
+    def step():
+        _lib.check(lib.ts_flce_fwd_bwd(
+            _lib.ptr(h), H, _lib.ptr(w), H, _lib.ptr(labels), N, H, V, -100, 0, _lib.ptr(loss),
+            _lib.ptr(rows), _lib.ptr(lse), _lib.ptr(gh), _lib.ptr(gw), chunk, _lib.ptr(ws),
+            ws_bytes, stream), "ts_flce_fwd_bwd")
+
+    ms = time_ms(step, max(3, steps // 2), max(1, warmup // 2))
+    flops = W.linear_ce_flops(N, H, V)
+    tf = flops / (ms * 1e-3) / 1e12
+    out = {"workload": (f"C5 fused linear CE: hidden [{N},{H}] bf16, lm_head [{V},{H}] bf16, "
+                        f"5% ignored, mean; loss + grad_hidden + grad_weight; token chunk "
+                        f"{chunk or N} rows"),
+           "ms": round(ms, 4), "algorithmic_flop": flops, "TFLOP_s": round(tf, 1),
+           "roofline": {"bound": "mfma", "achieved": round(tf, 1),
+                        "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)},
+           "tokens_per_s": round(N / (ms * 1e-3), 1)}
+    if cpu:
+        out["cpu_baseline"] = cpu_baseline_linear_ce(cpu_seconds)
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -164,6 +318,9 @@ def main():
         "rmsnorm_fwd": bytes_c1["fwd"], "rope_fwd": bytes_c2["fwd"], "ce_fwd": bytes_c3["fwd"],
         "ce_bwd": bytes_c3["bwd"], "rope_bwd": bytes_c2["bwd"], "rmsnorm_bwd": bytes_c1["bwd"],
     }
+    kernel_names = {"rmsnorm_fwd": "rms_fwd_reg", "rope_fwd": "rope_vec_kernel",
+                    "ce_fwd": "ce_fwd_vec", "ce_bwd": "ce_bwd_vec",
+                    "rope_bwd": "rope_vec_kernel", "rmsnorm_bwd": "rms_bwd_reg+rms_dw_reduce4"}
     step_bytes = sum(op_bytes.values())
     order = list(op_bytes)
     state = {}
@@ -209,15 +366,14 @@ def main():
     for name in order:
         ms = sum(per_op[name]) / len(per_op[name])
         gbs = op_bytes[name] / (ms * 1e-3) / 1e9
-        kernels[name] = {"ms": round(ms, 4), "bytes": op_bytes[name], "GB_s": round(gbs, 1),
+        kernels[name] = {"kernel": kernel_names[name], "ms": round(ms, 4),
+                         "bytes": op_bytes[name], "GB_s": round(gbs, 1),
                          "frac": round(gbs / HBM_PEAK_GBS, 4)}
     dom = max(order, key=lambda n: kernels[n]["ms"])
-    pmc = load_traffic()
-    traffic = None
-    if pmc and pmc.get("kernel_op") == dom:
-        traffic = pmc.get("hbm_bytes_per_launch")
+    traffic = load_traffic().get(kernel_names[dom])
     roofline = {
-        "kernel": dom,
+        "kernel": kernel_names[dom],
+        "op": dom,
         "bound": "hbm",
         "achieved": kernels[dom]["GB_s"],
         "peak": HBM_PEAK_GBS,
@@ -242,7 +398,8 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": ("C1 RMSNorm x[8,2048,4096] + C2 RoPE Q[8,2048,32,128]/K[8,2048,8,128] "
-                         "theta 5e5 in-register + C3 CE logits[16384,128256] 10% ignored; "
+                         "theta 5e5 in-register + C3 CE logits[16384,128256] 10% ignored "
+                         "(schedule A: forward reads, backward reads + writes); "
                          "fwd C1,C2,C3 then bwd C3,C2,C1"),
             "step_bytes": step_bytes,
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
@@ -253,6 +410,15 @@ def main():
         "kernels": kernels,
         "device": torch.cuda.get_device_name(dev),
     }
+    # free the headline step's buffers before the extra sections
+    del c1, c2, c3, x, w, dy, x2d, dy2d, q, k, dq, dk, q_out, k_out, dq_out, dk_out
+    del logits, labels, grad, state
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        out["c4_packed"] = bench_packed(dev, args.steps, args.warmup)
+        out["c5_linear_ce"] = bench_linear_ce(dev, args.steps, args.warmup,
+                                              cpu=not args.no_cpu_baseline,
+                                              cpu_seconds=args.cpu_seconds)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

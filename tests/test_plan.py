@@ -9,6 +9,7 @@ indices. A small C++ driver compiled with g++ sweeps many shapes and checks:
   for the unsplit launch);
 * register plans cover every 16-byte vector of the row and stay within the
   template instantiations the launcher has;
+* the grouped GEMM tile order visits every output tile exactly once;
 * RoPE workgroups are whole waves within 256..1024 threads and their cos/sin
   staging fits the LDS bound;
 * umulhi(n, ceil(2^32/d)) == n / d wherever magic_exact(n_max, d) admits it,
@@ -33,6 +34,7 @@ DRIVER = r"""
 #include <cstdio>
 #include <cstdlib>
 #include <initializer_list>
+#include <vector>
 #include "plan.hpp"
 using namespace ts_plan;
 
@@ -96,6 +98,22 @@ int main() {
       CHECK(b.threads % 64 == 0 && b.threads >= 256 && b.threads <= 1024, "rope threads %d", b.threads);
       if (tpt >= 256) CHECK(b.tpb == 1, "rope tpb %d for %lld tasks", b.tpb, tpt);
       else CHECK((long long)b.tpb * tpt <= 256 || b.tpb == 1, "rope over-filled block");
+    }
+  }
+  // GEMM tile order is a bijection onto the MT x NT tiles
+  for (long long MT : {1, 2, 15, 16, 17, 32, 33, 501}) {
+    for (long long NT : {1, 3, 16, 501}) {
+      std::vector<char> seen(MT * NT, 0);
+      for (long long b = 0; b < MT * NT; ++b) {
+        int64_t mt, nt;
+        gemm_tile_of(b, MT, NT, mt, nt);
+        const bool ok = mt >= 0 && mt < MT && nt >= 0 && nt < NT;
+        CHECK(ok, "tile_of(%lld) out of range for %lld x %lld", b, MT, NT);
+        if (ok) {
+          CHECK(!seen[mt * NT + nt], "tile (%lld, %lld) twice", (long long)mt, (long long)nt);
+          seen[mt * NT + nt] = 1;
+        }
+      }
     }
   }
   // magic-number division

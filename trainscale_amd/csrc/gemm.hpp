@@ -11,15 +11,16 @@
 // Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds
 // (no staging registers): a wave's load instruction fills 1 KiB of LDS, lane i
 // at the wave's base + 16 * i. Four LDS stages of 32 KiB (A + B) keep two to
-// three k-blocks of loads in flight while the MFMAs consume one; one barrier
+// three k-blocks of loads in flight while the MFMAs consume one (a fifth
+// stage, the whole 160 KiB of a CU, measured slower on MI355X); one barrier
 // per k-block, and the MFMA operand fragments are double-buffered in registers
 // so every LDS read overlaps MFMAs (see mainloop). Buffer resources make
 // out-of-range rows (and the k tail) read as zeros, so partial tiles need no
 // branches.
 //
 // LDS rows are 64 B (32 bf16) with the four 16-byte chunks XOR-swizzled by
-// (row >> 1) & 3, so the ds_read_b128 of 8 consecutive lanes (8 consecutive
-// rows, same logical chunk) hit 8 disjoint groups of banks.
+// (row >> 2) & 3 (see swz), which makes the MFMA operand ds_read_b128s free of
+// bank conflicts.
 //
 // MFMA 32x32x16 bf16 lane layout (checked on the device): A lane l holds row
 // l % 32, k = (l / 32) * 8 + e for e < 8; B lane l holds column l % 32 with the
@@ -30,6 +31,7 @@
 #include <stdint.h>
 
 #include "common.hpp"
+#include "plan.hpp"
 
 namespace ts_gemm {
 
@@ -41,12 +43,16 @@ typedef __attribute__((address_space(3))) uint32_t* lds_ptr_t;
 constexpr int BM = 256;
 constexpr int BN = 256;
 constexpr int BK = 32;
-constexpr int kStages = 4;
+#ifndef TS_GEMM_STAGES
+#define TS_GEMM_STAGES 4
+#endif
+constexpr int kStages = TS_GEMM_STAGES;  // LDS stages of 32 KiB
+static_assert(kStages >= 3 && kStages <= 5, "pipeline depth");
 constexpr int kThreads = 256;
 constexpr int kRowBytes = BK * 2;                       // 64
 constexpr int kTileBytes = BM * kRowBytes;              // 16 KiB per operand per stage
 constexpr int kStageBytes = 2 * kTileBytes;             // A + B
-constexpr size_t kLdsBytes = (size_t)kStages * kStageBytes;  // 128 KiB
+constexpr size_t kLdsBytes = (size_t)kStages * kStageBytes;
 constexpr int kLoadsPerWave = BM * kRowBytes / 1024 / 4;      // 1 KiB loads per wave per operand
 constexpr uint32_t kOob = 0x80000000u;  // voffset beyond every resource's range -> reads 0
 
@@ -75,6 +81,24 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// LDS position of logical 16-byte chunk c (0..3) of LDS row `row` (64-byte
+// rows). XOR with bits 2-3 of the row: among the rows one ds_read_b128 pass
+// serves, rows that share a 128-byte bank line pair up with distinct chunk
+// positions. Measured on MI355X with SQ_LDS_BANK_CONFLICT: 0 conflict cycles
+// (XOR with bits 1-2 instead costs 12% of the main loop's cycles).
+__device__ inline int swz(int row, int c) { return c ^ ((row >> 2) & 3); }
+
+// Waits until at most `later` stages of this wave's loads are outstanding
+// (each stage is 2 * kLoadsPerWave loads; vmcnt counts loads in issue order).
+__device__ inline void wait_stage(int64_t later) {
+  constexpr int kPer = 2 * kLoadsPerWave;
+  static_assert(kPer * 3 < 64, "vmcnt range");
+  if (later >= 3) wait_vmcnt<3 * kPer>();
+  else if (later == 2) wait_vmcnt<2 * kPer>();
+  else if (later == 1) wait_vmcnt<kPer>();
+  else wait_vmcnt<0>();
+}
+
 // Per-thread byte offsets (relative to the tile's first row) of this lane's
 // loads for logical chunk c of LDS row r: row * ld * 2 + chunk * 16.
 struct TileLoader {
@@ -97,7 +121,7 @@ __device__ inline TileLoader make_loader(const __bf16* g, int64_t ld, int64_t nr
 #pragma unroll
   for (int u = 0; u < kLoadsPerWave; ++u) {
     const int row = (u * 4 + wid) * 16 + (lane >> 2);
-    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    const int chunk = swz(row, lane & 3);  // the logical chunk LDS position lane&3 holds
     t.off[u] = (uint32_t)(row * ld * 2 + chunk * 16);
   }
   t.lds_row0 = wid * 16;
@@ -111,7 +135,7 @@ __device__ inline void issue_loads(const TileLoader& t, int64_t k0, int64_t K, u
   for (int u = 0; u < kLoadsPerWave; ++u) {
     // logical chunk of this lane for the load's row (same swizzle as make_loader)
     const int row = (u * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
-    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    const int chunk = swz(row, lane & 3);
     const bool in_k = k0 + chunk * 8 < K;
     const uint32_t voff = in_k ? t.off[u] + (uint32_t)(k0 * 2) : kOob;
     uint8_t* dst = lds_tile + (u * 4 + (threadIdx.x >> 6)) * 16 * kRowBytes;
@@ -132,12 +156,12 @@ __device__ inline void read_frags(const uint8_t* As, const uint8_t* Bs, int wm, 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = wm * 128 + i * 32 + r;
-    f.a[i] = *reinterpret_cast<const bf16x8*>(As + row * kRowBytes + ((c ^ ((row >> 1) & 3)) << 4));
+    f.a[i] = *reinterpret_cast<const bf16x8*>(As + row * kRowBytes + (swz(row, c) << 4));
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = wn * 128 + j * 32 + r;
-    f.b[j] = *reinterpret_cast<const bf16x8*>(Bs + row * kRowBytes + ((c ^ ((row >> 1) & 3)) << 4));
+    f.b[j] = *reinterpret_cast<const bf16x8*>(Bs + row * kRowBytes + (swz(row, c) << 4));
   }
 }
 
@@ -175,7 +199,6 @@ __device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64
   const TileLoader la = make_loader(A, lda, M, m0);
   const TileLoader lb = make_loader(B, ldb, N, n0);
   const int64_t KT = (K + BK - 1) / BK;
-  constexpr int kPerStage = 2 * kLoadsPerWave;  // loads per wave per stage
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s) {
     if (s < KT) {
@@ -183,10 +206,8 @@ __device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64
       issue_loads(lb, (int64_t)s * BK, K, smem + s * kStageBytes + kTileBytes);
     }
   }
-  // stage 0 landed (stages 1 and 2 may still be in flight)
-  if (KT >= 3) wait_vmcnt<2 * kPerStage>();
-  else if (KT == 2) wait_vmcnt<kPerStage>();
-  else wait_vmcnt<0>();
+  // stage 0 landed (stages 1 .. kStages-2 may still be in flight)
+  wait_stage(KT - 1 < kStages - 2 ? KT - 1 : kStages - 2);
   __builtin_amdgcn_s_barrier();
   Frags f0, f1;
   read_frags(smem, smem + kTileBytes, wm, wn, lane, 0, f0);
@@ -198,14 +219,14 @@ __device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64
     mma_frags(f0, acc);
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < KT) {
-      // stage kt+1 landed: at most stage kt+2's loads remain in flight
-      if (kt + 2 < KT) wait_vmcnt<kPerStage>();
-      else wait_vmcnt<0>();
+      // stage kt+1 landed: stages kt+2 .. kt+kStages-2 may remain in flight
+      const int64_t later = KT - 2 - kt;
+      wait_stage(later < kStages - 3 ? later : kStages - 3);
       __builtin_amdgcn_s_barrier();
-      if (kt + 3 < KT) {
-        const int s = (int)((kt + 3) % kStages);
-        issue_loads(la, (kt + 3) * BK, K, smem + s * kStageBytes);
-        issue_loads(lb, (kt + 3) * BK, K, smem + s * kStageBytes + kTileBytes);
+      if (kt + kStages - 1 < KT) {
+        const int s = (int)((kt + kStages - 1) % kStages);
+        issue_loads(la, (kt + kStages - 1) * BK, K, smem + s * kStageBytes);
+        issue_loads(lb, (kt + kStages - 1) * BK, K, smem + s * kStageBytes + kTileBytes);
       }
       const uint8_t* An = smem + ((kt + 1) % kStages) * kStageBytes;
       read_frags(An, An + kTileBytes, wm, wn, lane, 0, f0);

@@ -54,7 +54,7 @@ struct GemmArgs {
   int64_t ldc32;
   // logits epilogue
   const int64_t* labels;  // labels of rows [0, M) of this chunk
-  float2* stats;          // [2 * NT][M] (max, sum exp) per 128-column slice
+  float2* stats;          // [M][2 * NT] (max, sum exp) per 128-column slice
   float* zlab;            // [M] logit at the label (written by the slice holding it)
 };
 
@@ -73,13 +73,30 @@ __device__ inline void stage_bf16(const Acc& acc, uint8_t* region, int lane) {
       }
 }
 
+// Writes rows [64 * half, 64 * half + 64) of the wave's 128 x 128 fp32
+// accumulator block into its private 32 KiB LDS region as [row][col] fp32
+// with 512-byte rows (accumulator tiles i = 2 * half, 2 * half + 1).
+__device__ inline void stage_f32_half(const Acc& acc, int half, uint8_t* region, int lane) {
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = ii * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int col = j * 32 + (lane & 31);
+        *reinterpret_cast<float*>(region + row * 512 + col * 4) = acc.t[2 * half + ii][j][e];
+      }
+}
+
 template <int kMode>
 __global__ __launch_bounds__(ts_gemm::kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flce_gemm(const GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[ts_gemm::kLdsBytes];
   const int64_t MT = (a.M + BM - 1) / BM;
-  const int64_t mt = blockIdx.x % MT;
-  const int64_t nt = blockIdx.x / MT;
+  const int64_t NT = (a.N + BN - 1) / BN;
+  int64_t mt, nt;
+  ts_plan::gemm_tile_of(blockIdx.x, MT, NT, mt, nt);
   const int64_t m0 = mt * BM;
   const int64_t n0 = nt * BN;
   Acc acc;
@@ -91,42 +108,50 @@ void flce_gemm(const GemmArgs a) {
   const int wn = wid & 1;
   const int64_t mb = m0 + wm * 128;  // first row of this wave's block
   const int64_t nb = n0 + wn * 128;  // first column
+  // Every wave is done with the pipeline's LDS before it is reused. Each wave
+  // then works in its own 32 KiB region; LDS operations of one wave complete
+  // in order, so it reads back its own writes without a barrier.
+  __syncthreads();
+  uint8_t* region = smem + wid * 32768;
 
-  if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32) {
+  if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32 || kMode == kEpiAccBf16) {
+    // fp32 C32 rows of 128 columns = 512 B: 32 lanes x 16 B per row, 2 rows per step
+    const int c4 = lane & 31;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int64_t r = mb + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-          const int64_t c = nb + j * 32 + (lane & 31);
-          if (r < a.M && c < a.N) {
-            float* p = a.C32 + r * a.ldc32 + c;
-            *p = kMode == kEpiAccF32 ? *p + acc.t[i][j][e] : acc.t[i][j][e];
+    for (int half = 0; half < 2; ++half) {
+      stage_f32_half(acc, half, region, lane);
+#pragma unroll 4
+      for (int it = 0; it < 32; ++it) {
+        const int lrow = it * 2 + (lane >> 5);
+        const int64_t gm = mb + half * 64 + lrow;
+        const int64_t gc = nb + c4 * 4;
+        if (gm < a.M && gc < a.N) {  // N % 8 == 0: 4 columns are all in or all out
+          float4 v = *reinterpret_cast<const float4*>(region + lrow * 512 + c4 * 16);
+          float* p = a.C32 + gm * a.ldc32 + gc;
+          if constexpr (kMode != kEpiF32) {
+            const float4 o = *reinterpret_cast<const float4*>(p);
+            v.x += o.x;
+            v.y += o.y;
+            v.z += o.z;
+            v.w += o.w;
+          }
+          if constexpr (kMode == kEpiAccBf16) {
+            bf16x2_t lo = {(__bf16)v.x, (__bf16)v.y};
+            bf16x2_t hi = {(__bf16)v.z, (__bf16)v.w};
+            uint2 pk;
+            pk.x = __builtin_bit_cast(uint32_t, lo);
+            pk.y = __builtin_bit_cast(uint32_t, hi);
+            *reinterpret_cast<uint2*>(a.C + gm * a.ldc + gc) = pk;
+          } else {
+            *reinterpret_cast<float4*>(p) = v;
           }
         }
-    return;
-  } else {
-    if constexpr (kMode == kEpiAccBf16) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int64_t r = mb + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            const int64_t c = nb + j * 32 + (lane & 31);
-            if (r < a.M && c < a.N) acc.t[i][j][e] += a.C32[r * a.ldc32 + c];
-          }
+      }
     }
-    // Every wave is done with the pipeline's LDS before it is reused.
-    __syncthreads();
-    uint8_t* region = smem + wid * (128 * kStagePitch);
+  } else {
     stage_bf16(acc, region, lane);
-    // The wave reads back only its own region: LDS operations of one wave
-    // complete in order, so no barrier is needed here.
     const int c16 = lane & 15;  // 16-byte chunk of the 256-byte row
+    const int64_t nparts = 2 * ((a.N + BN - 1) / BN);
 #pragma unroll 4
     for (int it = 0; it < 32; ++it) {
       const int lrow = it * 4 + (lane >> 4);
@@ -149,7 +174,7 @@ void flce_gemm(const GemmArgs a) {
         }
         const float s = row_sum(ls);
         if (gm < a.M) {
-          if (c16 == 0) a.stats[(nt * 2 + wn) * a.M + gm] = make_float2(m, s);
+          if (c16 == 0) a.stats[gm * nparts + nt * 2 + wn] = make_float2(m, s);
           const int64_t lab = a.labels[gm];
           if (in && lab >= gc && lab < gc + 8) a.zlab[gm] = f[lab - gc];
         }
@@ -168,22 +193,29 @@ __global__ __launch_bounds__(256) void flce_count(const int64_t* __restrict__ la
   if (threadIdx.x == 0) *n_valid = (int)c;
 }
 
-// Per row of a chunk: lse from the slice statistics, loss = lse - z[label].
+// Per row of a chunk (one wave per row): lse from the row's slice statistics
+// (contiguous [nparts] float2), loss = lse - z[label]. Fixed combination order:
+// lane-strided partial (max, sum) pairs, then a DPP/lane-read fold.
 __global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stats, int64_t nparts,
                                                  const float* __restrict__ zlab,
                                                  const int64_t* __restrict__ labels, int64_t M,
                                                  int64_t V, int64_t ignore_index,
                                                  float* __restrict__ lse_out,
                                                  float* __restrict__ loss_rows) {
-  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (r >= M) return;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= M) return;  // wave-uniform
+  const float2* sr = stats + r * nparts;
   float m = -INFINITY;
-  for (int64_t p = 0; p < nparts; ++p) m = fmaxf(m, stats[p * M + r].x);
+  for (int64_t p = lane; p < nparts; p += 64) m = fmaxf(m, sr[p].x);
+  m = wave_max(m);
   float s = 0.f;
-  for (int64_t p = 0; p < nparts; ++p) {
-    const float2 st = stats[p * M + r];
+  for (int64_t p = lane; p < nparts; p += 64) {
+    const float2 st = sr[p];
     s += st.y == 0.f ? 0.f : st.y * fast_exp2((st.x - m) * kLog2e);
   }
+  s = wave_sum(s);
+  if (lane != 0) return;
   const float l = m + logf(s);
   const int64_t lab = labels[r];
   float out;
@@ -469,7 +501,7 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
     g.stats = stats;
     g.zlab = zlab + r0;
     TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_gemm_logits"));
-    hipLaunchKernelGGL(flce_rows, dim3((unsigned)((Mc + 255) / 256)), dim3(256), 0, st, stats,
+    hipLaunchKernelGGL(flce_rows, dim3((unsigned)((Mc + 3) / 4)), dim3(256), 0, st, stats,
                        lay.nparts, zlab + r0, labels + r0, Mc, V, ignore_index, lse_ws + r0,
                        rows_ws + r0);
     TS_TRY(ts_host::check_launch("flce_rows"));

@@ -9,6 +9,12 @@
 
 #include <stdint.h>
 
+#if defined(__HIPCC__)
+#define TS_HOST_DEVICE __host__ __device__
+#else
+#define TS_HOST_DEVICE
+#endif
+
 namespace ts_plan {
 
 constexpr int kWave = 64;
@@ -157,5 +163,24 @@ inline uint32_t magic_div(uint32_t n, uint32_t magic) {
   return magic == 0 ? n : (uint32_t)(((uint64_t)n * magic) >> 32);
 }
 inline bool magic_exact(uint64_t n_max, uint64_t d) { return n_max * d < ((uint64_t)1 << 32); }
+
+// ---------------------------------------------------------------------------
+// GEMM tile order: workgroup `bid` of MT x NT output tiles, in groups of
+// kGemmGroupM M-tiles; inside a group M-tiles vary fastest, then N-tiles. The
+// ~256 workgroups resident at a time then cover about 16 M-tiles x 16
+// N-tiles, so both operands' tiles are shared by many concurrent workgroups
+// whatever the aspect ratio of C (a tall grad-weight output included).
+// ---------------------------------------------------------------------------
+constexpr int64_t kGemmGroupM = 16;
+
+TS_HOST_DEVICE inline void gemm_tile_of(int64_t bid, int64_t MT, int64_t NT, int64_t& mt,
+                                        int64_t& nt) {
+  const int64_t per_group = kGemmGroupM * NT;
+  const int64_t g = bid / per_group;
+  const int64_t w = bid - g * per_group;
+  const int64_t gm = MT - g * kGemmGroupM < kGemmGroupM ? MT - g * kGemmGroupM : kGemmGroupM;
+  mt = g * kGemmGroupM + w % gm;
+  nt = w / gm;
+}
 
 }  // namespace ts_plan
