@@ -191,6 +191,24 @@ ts_status ts_ce_bwd(const void* logits, int64_t ld, ts_dtype dtype,
                     float logit_scale, float softcap, float label_smoothing,
                     ts_stream_t stream);
 
+/*
+ * ts_ce_fwd and ts_ce_bwd in one pass when the upstream gradient is known at
+ * forward time (dloss as for ts_ce_bwd): loss[r], lse[r] and grad as those two
+ * functions define them. Each valid row is read once and every row of grad
+ * written once while a row of up to 1024 * 16 16-byte vectors (V <= 131072
+ * for bf16) fits one workgroup's registers; longer rows run the two calls.
+ * grad must not alias the logits. Replaces the forward + backward pair of
+ * Fast_CrossEntropyLoss (kernels/triton_kernels.py:320-424) and
+ * FusedCrossEntropyFunction (loss/sota_losses.py:437-532) for callers that
+ * reduce the per-row losses with fixed weights (mean, sum, batchmean).
+ */
+ts_status ts_ce_fwd_bwd(const void* logits, int64_t ld, ts_dtype dtype,
+                        const int64_t* labels, int64_t N, int64_t V,
+                        int64_t ignore_index, float logit_scale, float softcap,
+                        float label_smoothing, const float* dloss, int64_t dloss_stride,
+                        float dloss_scale, float* loss, float* lse,
+                        void* grad, int64_t ld_grad, ts_dtype grad_dtype, ts_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused linear cross-entropy                                                */
 /* ------------------------------------------------------------------------ */
@@ -232,12 +250,15 @@ ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight, i
                           void* workspace, size_t workspace_bytes, ts_stream_t stream);
 
 /*
- * x[i] *= *scale for n bf16 values (n a multiple of 8, x 16-byte aligned);
- * scale is a device pointer, and when *scale == 1 nothing is written. Used to
- * apply an upstream gradient other than 1 to ts_flce_fwd_bwd's gradients
- * without a host synchronisation.
+ * x[i] *= *scale for n values of `dtype` (n a multiple of 16 bytes' worth of
+ * elements, x 16-byte aligned); scale is a device pointer, and when
+ * *scale == 1 nothing is written. Applies an upstream gradient other than 1
+ * to gradients formed in a forward pass (ts_ce_fwd_bwd, ts_flce_fwd_bwd)
+ * without a host synchronisation. Has no counterpart in the reference, whose
+ * backward passes receive the upstream gradient directly.
  */
-ts_status ts_scale_bf16(void* x, int64_t n, const float* scale, ts_stream_t stream);
+ts_status ts_scale_inplace(void* x, int64_t n, ts_dtype dtype, const float* scale,
+                           ts_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -169,3 +169,100 @@ def test_out_of_range_label_is_nan(gpu):
     loss, _ = ops.ce_forward(logits, 64, labels)
     l = loss.cpu()
     assert math.isnan(l[1]) and not math.isnan(l[0]) and l[2] == 0.0
+
+
+# ---------------------------------------------------------------------------
+# Schedule B: loss and gradient in one pass (ts_ce_fwd_bwd)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("V", [8, 1000, 4096, 32000, 128256, 140000])
+@pytest.mark.parametrize("dtype", [BF, torch.float16, torch.float32])
+def test_fused_fwd_bwd_matches_oracle(gpu, V, dtype):
+    torch.manual_seed(V + 1)
+    N = 20
+    logits = (2 * torch.randn(N, V, device=gpu)).to(dtype)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::6] = -100
+    dl = torch.tensor([0.25], device=gpu)
+    loss, lse, grad = ops.ce_forward_backward(logits, V, labels, dl)
+    ref, ref_lse = oracle.ce_fwd(logits.cpu(), labels.cpu())
+    torch.testing.assert_close(loss.cpu(), ref, rtol=1e-5, atol=1e-6)
+    ref_g = oracle.ce_bwd(logits.cpu(), labels.cpu(), torch.tensor(0.25))
+    if dtype == torch.float32:
+        torch.testing.assert_close(grad.cpu(), ref_g, rtol=1e-5, atol=1e-9)
+    else:
+        assert_ulp(grad, ref_g, 1, tiny=TINY if dtype == BF else 1e-7)
+    # the two-pass schedule gives the same numbers
+    l2, lse2 = ops.ce_forward(logits, V, labels)
+    g2 = torch.empty_like(logits)
+    ops.ce_backward(logits, V, labels, lse2, dl, g2, V)
+    torch.testing.assert_close(loss, l2, rtol=1e-6, atol=1e-6)
+    if dtype != torch.float32:
+        assert max_ulp_gpu(grad, g2) <= 1
+
+
+def max_ulp_gpu(a, b):
+    from helpers import max_ulp
+    return max_ulp(a.cpu(), b.cpu())
+
+
+@pytest.mark.parametrize("cap,sc,a", [(30.0, 0.0, 0.0), (0.0, 0.5, 0.0), (0.0, 0.0, 0.1),
+                                      (5.0, 0.5, 0.1)])
+def test_fused_transforms(gpu, cap, sc, a):
+    torch.manual_seed(3)
+    N, V = 24, 3000
+    logits = (4 * torch.randn(N, V, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[2] = -100
+    dl = torch.full((N,), 0.5, device=gpu)
+    loss, _, grad = ops.ce_forward_backward(logits, V, labels, dl, 1.0, -100, sc, cap, a,
+                                            grad_dtype=torch.float32)
+    ref, _ = oracle.ce_fwd(logits.cpu(), labels.cpu(), logit_scale=sc, softcap=cap,
+                           label_smoothing=a)
+    torch.testing.assert_close(loss.cpu(), ref, rtol=1e-5, atol=1e-5)
+    ref_g = oracle.ce_bwd(logits.cpu(), labels.cpu(), torch.full((N,), 0.5), logit_scale=sc,
+                          softcap=cap, label_smoothing=a, out_dtype=torch.float32)
+    torch.testing.assert_close(grad.cpu(), ref_g, rtol=1e-4, atol=2e-8)
+
+
+@pytest.mark.parametrize("red", ["mean", "sum", "batchmean"])
+def test_loss_classes_upstream_scale_and_no_grad(gpu, red):
+    torch.manual_seed(4)
+    N, V = 64, 2048
+    logits = (2 * torch.randn(N, V, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[:5] = -100
+    lab = labels.cpu()
+    n_valid = int((lab != -100).sum())
+    rows, _ = oracle.ce_fwd(logits.cpu(), lab)
+    w = {"mean": 1.0 / n_valid, "sum": 1.0, "batchmean": 1.0 / N}[red]
+    for mod in (ChunkedCrossEntropyLoss(reduction=red), FusedCrossEntropyLoss(reduction=red)):
+        x = logits.clone().requires_grad_()
+        out = mod(x, labels)
+        assert abs(out.item() - float(rows.sum()) * w) <= 1e-5 * abs(float(rows.sum()) * w)
+        (-2.5 * out).backward()  # upstream gradient -2.5: scaled in place on the device
+        ref_g = oracle.ce_bwd(logits.cpu(), lab, torch.tensor(-2.5 * w))
+        assert_ulp(x.grad, ref_g, 1, tiny=TINY, what=f"{type(mod).__name__} {red}")
+        with torch.no_grad():
+            out2 = mod(logits, labels)
+        assert abs(out2.item() - out.item()) <= 1e-6 * abs(out.item())
+
+
+def test_c3_full_fused(gpu):
+    wl = workloads.ce_workload(gpu)
+    logits, labels = wl.tensors["logits"], wl.tensors["labels"]
+    N, V = logits.shape
+    n_valid = int((labels != -100).sum())
+    dl = torch.tensor([1.0 / n_valid], device=gpu)
+    loss, lse, grad = ops.ce_forward_backward(logits, V, labels, dl)
+    lab_cpu = labels.cpu()
+    sample = torch.cat([torch.arange(0, 256), torch.arange(N - 128, N)])
+    ref_rows, _ = oracle.ce_fwd(logits[sample].cpu(), lab_cpu[sample])
+    torch.testing.assert_close(loss[sample].cpu(), ref_rows, rtol=1e-5, atol=1e-6)
+    ref_g = oracle.ce_bwd(logits[sample].cpu(), lab_cpu[sample], torch.tensor(1.0 / n_valid))
+    assert_ulp(grad[sample], ref_g, 1, tiny=TINY, what="grad")
+    ign = labels == -100
+    assert torch.count_nonzero(grad[ign]) == 0
+    # agrees with the two-pass schedule on every row's loss
+    l2, _ = ops.ce_forward(logits, V, labels)
+    torch.testing.assert_close(loss, l2, rtol=1e-6, atol=1e-6)

@@ -125,6 +125,29 @@ __device__ inline void st16_stream(T* p, const u32x4& v) {
 }
 
 // ---------------------------------------------------------------------------
+// Raw buffer access: a 128-bit resource (base, byte range) held in SGPRs and
+// a 32-bit per-lane byte offset, so a row's addresses cost one VGPR instead
+// of a 64-bit pointer per access. The hardware range check drops stores and
+// zero-fills loads at offsets >= the range. It looks at the VGPR offset only
+// (the SGPR offset operand is not range-checked), so every offset goes in the
+// VGPR operand and an access that must not happen uses kBufOob. The range
+// must stay below 2^31 bytes for kBufOob to lie outside it.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr int kBufOob = (int)0x80000000u;
+constexpr int kBufNt = 2;  // non-temporal cache policy
+
+__device__ inline Rsrc buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ inline u32x4 buf_ld16_stream(Rsrc r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, kBufNt);
+}
+__device__ inline void buf_st16_stream(const u32x4& v, Rsrc r, int voff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, kBufNt);
+}
+
+// ---------------------------------------------------------------------------
 // Wave64 reductions: DPP inside each 16-lane row (every lane of a row ends
 // with the row's result), then the four row results are read with
 // v_readlane_b32 and combined in a fixed order. Every lane gets the result.

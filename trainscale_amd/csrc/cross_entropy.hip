@@ -321,6 +321,221 @@ __global__ __launch_bounds__(kThreads) void ce_bwd_generic(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Forward + backward in one pass ("schedule B"): one row per 1024-thread
+// workgroup, held in registers (kFusedKv 16-byte vectors per thread, so
+// V <= 1024 * kFusedKv * vector width). Each thread folds its vectors into an
+// online (max, sum of exp) pair as they arrive; one LDS exchange of the 16
+// wave pairs gives the lse (a single barrier). The gradient is then written
+// from the same registers: each valid row is read once and every row written
+// once. Ignored rows are written as zeros without being read.
+//
+// The row is addressed through buffer resources (base and range in SGPRs,
+// one VGPR of offset per lane), which keeps the 64 data VGPRs plus the
+// working set inside the 128-VGPR budget of a 1024-thread workgroup. Without
+// label smoothing or logit transforms an element's gradient is
+// exp2(z*log2e - (lse*log2e - log2|dl|)) with the sign of dl applied to the
+// packed result, one FMA and one exp per element; the label element is
+// corrected by the one lane that holds it.
+// ---------------------------------------------------------------------------
+constexpr int kFusedThreads = 1024;
+constexpr int kFusedWaves = kFusedThreads / kWave;
+constexpr int kFusedKv = 16;
+
+// Byte offset of this thread's k-th vector, kBufOob past the row end.
+__device__ inline int fused_voff(int k, int nvec, int vec_bytes) {
+  const int v = threadIdx.x + k * kFusedThreads;
+  return v < nvec ? v * vec_bytes : kBufOob;
+}
+
+// Row lse (and, with kSmooth, the row sum of z) from every thread's online
+// (max, sum of exp) pair. lds holds 3 * kFusedWaves floats. One barrier: the
+// caller must not write lds again without another barrier in between.
+template <bool kSmooth>
+__device__ inline float fused_lse(float m, float s, float& sz, float* lds) {
+  const float wm = wave_max(m);
+  const float ws = wave_sum(s == 0.f ? 0.f : s * fast_exp2((m - wm) * kLog2e));
+  const int wid = threadIdx.x / kWave;
+  if constexpr (kSmooth) sz = wave_sum(sz);
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    lds[wid] = wm;
+    lds[kFusedWaves + wid] = ws;
+    if constexpr (kSmooth) lds[2 * kFusedWaves + wid] = sz;
+  }
+  __syncthreads();
+  float gm = lds[0];
+#pragma unroll
+  for (int i = 1; i < kFusedWaves; ++i) gm = fmaxf(gm, lds[i]);
+  float gs = 0.f, gz = 0.f;
+#pragma unroll
+  for (int i = 0; i < kFusedWaves; ++i) {
+    const float si = lds[kFusedWaves + i];
+    gs += si == 0.f ? 0.f : si * fast_exp2((lds[i] - gm) * kLog2e);
+    if constexpr (kSmooth) gz += lds[2 * kFusedWaves + i];
+  }
+  if constexpr (kSmooth) sz = gz;
+  return gm + logf(gs);
+}
+
+template <typename G>
+constexpr uint32_t sign_bits() {
+  return sizeof(G) == 4 ? 0x80000000u : 0x80008000u;
+}
+
+template <typename T, typename G, bool kXform, bool kSmooth>
+__global__ __launch_bounds__(kFusedThreads) void ce_fused_vec(
+    const T* __restrict__ logits, int64_t ld, const int64_t* __restrict__ labels, int64_t V,
+    int nvec, int64_t ignore_index, Xform xf, float smoothing, const float* __restrict__ dloss,
+    int64_t dloss_stride, float dloss_scale, float* __restrict__ loss, float* __restrict__ lse_out,
+    G* __restrict__ grad, int64_t ld_grad) {
+  constexpr int VE = Elt<T>::kVec;
+  constexpr int kGradBytes = VE * (int)sizeof(G);  // grad bytes per logits vector
+  __shared__ float lds[3 * kFusedWaves];
+  const int64_t row = blockIdx.x;
+  const int64_t label = labels[row];
+  const Rsrc go = buf_rsrc(grad + row * ld_grad, (uint32_t)nvec * kGradBytes);
+  if (label == ignore_index) {
+    const u32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < kFusedKv; ++k) {
+      const int off = fused_voff(k, nvec, kGradBytes);
+      buf_st16_stream(zero, go, off);
+      if constexpr (kGradBytes == 32) buf_st16_stream(zero, go, off + 16);
+    }
+    if (threadIdx.x == 0) {
+      loss[row] = 0.f;
+      lse_out[row] = 0.f;
+    }
+    return;
+  }
+  const T* xr = logits + row * ld;
+  const Rsrc xi = buf_rsrc(xr, (uint32_t)nvec * 16u);
+  u32x4 buf[kFusedKv];
+#pragma unroll
+  for (int k = 0; k < kFusedKv; ++k) buf[k] = buf_ld16_stream(xi, fused_voff(k, nvec, 16));
+  float m = -INFINITY, s = 0.f, sz = 0.f;
+#pragma unroll
+  for (int k = 0; k < kFusedKv; ++k) {
+    if (threadIdx.x + k * kFusedThreads < nvec) {
+      float z[VE];
+      Elt<T>::unpack(buf[k], z);
+      float cm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < VE; ++i) {
+        z[i] = xform<kXform>(z[i], xf);
+        cm = fmaxf(cm, z[i]);
+        if constexpr (kSmooth) sz += z[i];
+      }
+      const float mn = fmaxf(m, cm), mb = mn * kLog2e;
+      float cs = 0.f;
+#pragma unroll
+      for (int i = 0; i < VE; ++i) cs += fast_exp2(__builtin_fmaf(z[i], kLog2e, -mb));
+      s = (s == 0.f ? 0.f : s * fast_exp2((m - mn) * kLog2e)) + cs;
+      m = mn;
+    }
+  }
+  const float l = fused_lse<kSmooth>(m, s, sz, lds);
+  // The gradient pass re-unpacks the stored vectors; this keeps the compiler
+  // from carrying the first pass's unpacked floats (twice the registers).
+#pragma unroll
+  for (int k = 0; k < kFusedKv; ++k) asm volatile("" : "+v"(buf[k]));
+  if (threadIdx.x == 0) {
+    float out;
+    if (label < 0 || label >= V) {
+      out = __builtin_nanf("");
+    } else {
+      const float zt = xform<kXform>(Elt<T>::load1(xr + label), xf);
+      out = l - zt;
+      if constexpr (kSmooth) out = (1.f - smoothing) * out + smoothing * (l - sz / (float)V);
+    }
+    loss[row] = out;
+    lse_out[row] = l;
+  }
+  const float dl = dloss[row * dloss_stride] * dloss_scale;
+  if constexpr (!kXform && !kSmooth) {
+    const float adl = fabsf(dl);
+    const float l2 = l * kLog2e;
+    const float l2d = l2 - __builtin_amdgcn_logf(adl);  // v_log_f32 is log2
+    const uint32_t sgn = dl < 0.f ? sign_bits<G>() : 0u;
+#pragma unroll
+    for (int k = 0; k < kFusedKv; ++k) {
+      float z[VE], g[VE];
+      Elt<T>::unpack(buf[k], z);
+#pragma unroll
+      for (int i = 0; i < VE; ++i) g[i] = fast_exp2(__builtin_fmaf(z[i], kLog2e, -l2d));
+      const int64_t d = label - (int64_t)(threadIdx.x + k * kFusedThreads) * VE;
+      if (d >= 0 && d < VE) {
+#pragma unroll
+        for (int i = 0; i < VE; ++i)
+          if (d == i) g[i] = adl * (fast_exp2(__builtin_fmaf(z[i], kLog2e, -l2)) - 1.f);
+      }
+      const int off = fused_voff(k, nvec, kGradBytes);
+      if constexpr (kGradBytes == 32) {
+        buf_st16_stream(Elt<float>::pack(g) ^ sgn, go, off);
+        buf_st16_stream(Elt<float>::pack(g + 4) ^ sgn, go, off + 16);
+      } else {
+        buf_st16_stream(Elt<G>::pack(g) ^ sgn, go, off);
+      }
+    }
+  } else {
+    BwdRow r;
+    r.dl = dl;
+    r.lse2 = l * kLog2e;
+    r.label = label;
+    const float inv_v = 1.f / (float)V;
+#pragma unroll
+    for (int k = 0; k < kFusedKv; ++k) {
+      float x[VE], g[VE];
+      Elt<T>::unpack(buf[k], x);
+      const int64_t j0 = (int64_t)(threadIdx.x + k * kFusedThreads) * VE;
+#pragma unroll
+      for (int i = 0; i < VE; ++i)
+        g[i] = ce_grad<kXform, kSmooth>(x[i], j0 + i, r, xf, smoothing, inv_v);
+      const int off = fused_voff(k, nvec, kGradBytes);
+      if constexpr (kGradBytes == 32) {
+        buf_st16_stream(Elt<float>::pack(g), go, off);
+        buf_st16_stream(Elt<float>::pack(g + 4), go, off + 16);
+      } else {
+        buf_st16_stream(Elt<G>::pack(g), go, off);
+      }
+    }
+  }
+}
+
+// Schedule B when the row fits the registers of one workgroup and 16-byte
+// access is possible; returns false (nothing launched) otherwise.
+template <typename T, typename G>
+bool fused_typed(const void* logits, int64_t ld, const int64_t* labels, int64_t N, int64_t V,
+                 int64_t ignore_index, Xform xf, float smoothing, const float* dloss,
+                 int64_t dloss_stride, float dloss_scale, float* loss, float* lse, void* grad,
+                 int64_t ld_grad, hipStream_t st, ts_status* status) {
+  constexpr int VE = sizeof(T) == 4 ? 4 : 8;
+  const bool grad_ok = sizeof(G) == sizeof(T) || (sizeof(G) == 4 && VE == 8);
+  const int64_t nvec = V / VE;
+  if (!(V % VE == 0 && ld % VE == 0 && ld_grad % VE == 0 && ts_host::aligned16(logits) &&
+        ts_host::aligned16(grad) && grad_ok && nvec <= (int64_t)kFusedThreads * kFusedKv &&
+        N <= INT32_MAX))
+    return false;
+  const T* lp = static_cast<const T*>(logits);
+  G* gp = static_cast<G*>(grad);
+  const bool xform_on = xf.scale != 0.f || xf.softcap != 0.f;
+  const bool smooth = smoothing != 0.f;
+#define TS_CE_FUSED(X, S)                                                                        \
+  if (xform_on == X && smooth == S) {                                                            \
+    hipLaunchKernelGGL((ce_fused_vec<T, G, X, S>), dim3((unsigned)N), dim3(kFusedThreads), 0, st, \
+                       lp, ld, labels, V, (int)nvec, ignore_index, xf, smoothing, dloss,        \
+                       dloss_stride, dloss_scale, loss, lse, gp, ld_grad);                      \
+    *status = ts_host::check_launch("ce_fused_vec");                                             \
+    return true;                                                                                 \
+  }
+  TS_CE_FUSED(false, false)
+  TS_CE_FUSED(false, true)
+  TS_CE_FUSED(true, false)
+  TS_CE_FUSED(true, true)
+#undef TS_CE_FUSED
+  return false;
+}
+
 template <typename T>
 ts_status fwd_typed(const void* logits, int64_t ld, const int64_t* labels, int64_t N, int64_t V,
                     int64_t ignore_index, Xform xf, float smoothing, float* loss, float* lse,
@@ -475,4 +690,55 @@ extern "C" ts_status ts_ce_bwd(const void* logits, int64_t ld, ts_dtype dtype,
   }
 #undef TS_CE_BWD_T
   return fail(TS_ERR_UNSUPPORTED_DTYPE, "ce_bwd: bad dtype");
+}
+
+extern "C" ts_status ts_ce_fwd_bwd(const void* logits, int64_t ld, ts_dtype dtype,
+                                   const int64_t* labels, int64_t N, int64_t V,
+                                   int64_t ignore_index, float logit_scale, float softcap,
+                                   float label_smoothing, const float* dloss,
+                                   int64_t dloss_stride, float dloss_scale, float* loss,
+                                   float* lse, void* grad, int64_t ld_grad, ts_dtype grad_dtype,
+                                   ts_stream_t stream) {
+  using ts_host::fail;
+  ts_status s = check_ce(logits, ld, dtype, labels, N, V, logit_scale, softcap, label_smoothing);
+  if (s != TS_OK) return s;
+  if (!ts_host::valid_dtype(grad_dtype))
+    return fail(TS_ERR_UNSUPPORTED_DTYPE, "ce_fwd_bwd: bad grad dtype");
+  if (grad_dtype != dtype && grad_dtype != TS_F32)
+    return fail(TS_ERR_UNSUPPORTED_DTYPE,
+                "ce_fwd_bwd: grad dtype must equal logits dtype or be f32");
+  if (N > 0 && (loss == nullptr || lse == nullptr || dloss == nullptr || grad == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "ce_fwd_bwd: loss, lse, dloss or grad is NULL");
+  if (ld_grad < V) return fail(TS_ERR_SHAPE, "ce_fwd_bwd: grad row stride < V");
+  if (dloss_stride < 0) return fail(TS_ERR_SHAPE, "ce_fwd_bwd: negative dloss stride");
+  if (grad == logits)
+    return fail(TS_ERR_INVALID_ARGUMENT,
+                "ce_fwd_bwd: grad must not alias the logits (use ts_ce_fwd + ts_ce_bwd)");
+  if (N == 0) return TS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Xform xf{logit_scale, softcap};
+  bool done = false;
+#define TS_CE_FB_T(T)                                                                           \
+  done = grad_dtype == TS_F32 && dtype != TS_F32                                                \
+             ? fused_typed<T, float>(logits, ld, labels, N, V, ignore_index, xf,                \
+                                     label_smoothing, dloss, dloss_stride, dloss_scale, loss,   \
+                                     lse, grad, ld_grad, st, &s)                                \
+             : fused_typed<T, T>(logits, ld, labels, N, V, ignore_index, xf, label_smoothing,   \
+                                 dloss, dloss_stride, dloss_scale, loss, lse, grad, ld_grad,    \
+                                 st, &s);
+  switch (dtype) {
+    case TS_BF16: TS_CE_FB_T(__bf16) break;
+    case TS_F16: TS_CE_FB_T(_Float16) break;
+    case TS_F32: TS_CE_FB_T(float) break;
+  }
+#undef TS_CE_FB_T
+  if (done) return s;
+  // Rows too long for one workgroup's registers (or no 16-byte access): the
+  // two-pass schedule, forward then backward.
+  s = ts_ce_fwd(logits, ld, dtype, labels, N, V, ignore_index, logit_scale, softcap,
+                label_smoothing, loss, lse, stream);
+  if (s != TS_OK) return s;
+  return ts_ce_bwd(logits, ld, dtype, labels, lse, dloss, dloss_stride, dloss_scale, grad,
+                   ld_grad, grad_dtype, N, V, ignore_index, logit_scale, softcap,
+                   label_smoothing, stream);
 }

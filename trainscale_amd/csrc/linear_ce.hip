@@ -331,18 +331,21 @@ __global__ __launch_bounds__(256) void fill_zero_u32(uint32_t* __restrict__ p, i
   if (i == 0 && loss != nullptr) *loss = 0.f;
 }
 
-// x[i] *= *scale unless *scale == 1 (then the kernel only reads the scalar).
-__global__ __launch_bounds__(256) void scale_bf16(__bf16* __restrict__ x, int64_t nvec,
-                                                  const float* __restrict__ scale_p) {
+// x[i] *= *scale unless *scale == 1 (then the kernel only reads the scalar);
+// nvec 16-byte vectors of element type T.
+template <typename T>
+__global__ __launch_bounds__(256) void scale_inplace(T* __restrict__ x, int64_t nvec,
+                                                     const float* __restrict__ scale_p) {
+  constexpr int VE = Elt<T>::kVec;
   const float s = *scale_p;
   if (s == 1.f) return;
   for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < nvec;
        v += (int64_t)gridDim.x * 256) {
-    float f[8];
-    Elt<__bf16>::unpack(ld16(x + v * 8), f);
+    float f[VE];
+    Elt<T>::unpack(ld16(x + v * VE), f);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] *= s;
-    st16(x + v * 8, Elt<__bf16>::pack(f));
+    for (int e = 0; e < VE; ++e) f[e] *= s;
+    st16(x + v * VE, Elt<T>::pack(f));
   }
 }
 
@@ -552,16 +555,35 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   return ts_host::check_launch("flce_loss");
 }
 
-extern "C" ts_status ts_scale_bf16(void* x, int64_t n, const float* scale, ts_stream_t stream) {
-  if (n < 0 || n % 8 != 0)
-    return ts_host::fail(TS_ERR_SHAPE, "scale_bf16: n must be a non-negative multiple of 8");
+extern "C" ts_status ts_scale_inplace(void* x, int64_t n, ts_dtype dtype, const float* scale,
+                                      ts_stream_t stream) {
+  if (!ts_host::valid_dtype(dtype))
+    return ts_host::fail(TS_ERR_UNSUPPORTED_DTYPE, "scale_inplace: bad dtype");
+  const int64_t per = dtype == TS_F32 ? 4 : 8;
+  if (n < 0 || n % per != 0)
+    return ts_host::fail(TS_ERR_SHAPE,
+                         "scale_inplace: n must be a non-negative multiple of %lld",
+                         (long long)per);
   if (n > 0 && (x == nullptr || scale == nullptr || !ts_host::aligned16(x)))
-    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "scale_bf16: bad pointer");
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "scale_inplace: bad pointer");
   if (n == 0) return TS_OK;
-  const int64_t nvec = n / 8;
+  const int64_t nvec = n / per;
   int64_t blocks = (nvec + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(scale_bf16, dim3((unsigned)blocks), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<__bf16*>(x), nvec, scale);
-  return ts_host::check_launch("scale_bf16");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TS_BF16:
+      hipLaunchKernelGGL(scale_inplace<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
+                         static_cast<__bf16*>(x), nvec, scale);
+      break;
+    case TS_F16:
+      hipLaunchKernelGGL(scale_inplace<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st,
+                         static_cast<_Float16*>(x), nvec, scale);
+      break;
+    case TS_F32:
+      hipLaunchKernelGGL(scale_inplace<float>, dim3((unsigned)blocks), dim3(256), 0, st,
+                         static_cast<float*>(x), nvec, scale);
+      break;
+  }
+  return ts_host::check_launch("scale_inplace");
 }

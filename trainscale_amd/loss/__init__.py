@@ -50,6 +50,8 @@ class CrossEntropyLoss(nn.Module):
         if logits.dim() == 3:
             logits = logits.reshape(-1, logits.shape[-1])
             labels = labels.reshape(-1)
-        loss = CrossEntropyRowsFunction.apply(logits, labels, self.ignore_index,
-                                              self.label_smoothing)
-        return reduce_rows(loss, labels, self.ignore_index, self.reduction)
+        if self.reduction == "none":
+            return CrossEntropyRowsFunction.apply(logits, labels, self.ignore_index,
+                                                  self.label_smoothing)
+        return FusedCrossEntropyFunction.apply(logits, labels, self.ignore_index,
+                                               self.label_smoothing, self.reduction)

@@ -21,7 +21,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from .. import _lib
+from .. import _lib, ops
 from .._lib import check, ptr
 
 __all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy", "DEFAULT_LOGITS_SCRATCH"]
@@ -86,12 +86,8 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
 
 
 def _scale_(t: Optional[Tensor], scale: Tensor) -> None:
-    if t is None or t.numel() == 0:
-        return
-    lib = _lib.load()
-    with torch.cuda.device(t.device):
-        check(lib.ts_scale_bf16(ptr(t), t.numel(), ptr(scale), _lib.stream_handle(t.device)),
-              "ts_scale_bf16")
+    if t is not None:
+        ops.scale_(t, scale)
 
 
 class LinearCrossEntropyFunction(torch.autograd.Function):

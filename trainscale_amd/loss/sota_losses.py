@@ -12,8 +12,9 @@ All three compute the same quantity: per-row
 loss = (1-a)*(lse - x[label]) + a*(lse - mean(x)), zero on ignore_index rows,
 reduced by mean (over non-ignored rows, at least 1), sum, batchmean (over all
 rows) or none. Here every one runs the gfx950 kernels directly on the logits
-in their own dtype: one read in forward, one read plus one write in backward,
-fp32 arithmetic throughout. The reference's ChunkedCrossEntropyLoss builds an
+in their own dtype with fp32 arithmetic: with a reduction, one pass reads each
+valid row once and writes its gradient (the forward forms it); without one,
+one read in forward, one read plus one write in backward. The reference's ChunkedCrossEntropyLoss builds an
 fp32 copy of the logits and differentiates through torch ops; its eval mode
 accumulates in the logits dtype, where this version stays in fp32.
 """
@@ -87,8 +88,28 @@ def _flatten(logits: Tensor, labels: Tensor) -> Tuple[Tensor, Tensor]:
     return logits, labels
 
 
+def _row_weight(labels: Tensor, ignore_index: int, reduction: str, n: int) -> Tensor:
+    """d(reduced loss)/d(row loss) as a one-element fp32 device tensor (no host sync)."""
+    if reduction == "mean":
+        valid = (labels != ignore_index).sum().clamp(min=1)
+        return valid.to(torch.float32).reciprocal().reshape(1)
+    if reduction == "batchmean":
+        return torch.full((1,), 1.0 / max(n, 1), dtype=torch.float32, device=labels.device)
+    return torch.ones((1,), dtype=torch.float32, device=labels.device)
+
+
 class FusedCrossEntropyFunction(torch.autograd.Function):
-    """Reduced cross-entropy in one autograd node (reference: loss/sota_losses.py:437-532)."""
+    """Reduced cross-entropy in one autograd node (reference: loss/sota_losses.py:437-532).
+
+    For mean, sum and batchmean the gradient is formed in the forward pass in
+    the same read of the logits that yields the loss (ts_ce_fwd_bwd: one read
+    of each valid row, one write of each gradient row), for an upstream
+    gradient of 1; backward scales it in place by the actual upstream gradient,
+    on the device and only when that is not 1. Without a gradient to compute
+    (no_grad, eval) only the forward kernel runs. reduction="none" keeps the
+    two-pass schedule, since per-row upstream gradients are unknown until
+    backward.
+    """
 
     @staticmethod
     def forward(ctx, logits: Tensor, labels: Tensor, ignore_index: int, label_smoothing: float,
@@ -96,27 +117,39 @@ class FusedCrossEntropyFunction(torch.autograd.Function):
         if reduction not in _REDUCTIONS:
             raise ValueError(f"Invalid reduction: {reduction}")
         l2d, ld = ops.as_rows(logits)
-        loss, lse = ops.ce_forward(l2d, ld, labels, ignore_index, 0.0, 0.0, label_smoothing)
-        ctx.save_for_backward(l2d, labels, lse)
-        ctx.ld = ld
+        flat = labels.reshape(-1)
+        ctx.shape = logits.shape
         ctx.cfg = (ignore_index, label_smoothing, reduction)
-        return reduce_rows(loss, labels, ignore_index, reduction)
+        if reduction != "none" and ctx.needs_input_grad[0]:
+            w = _row_weight(flat, ignore_index, reduction, l2d.shape[0])
+            loss, _, grad = ops.ce_forward_backward(l2d, ld, flat, w, 1.0, ignore_index, 0.0, 0.0,
+                                                    label_smoothing)
+            ctx.fused = True
+            ctx.save_for_backward(grad)
+            return reduce_rows(loss, flat, ignore_index, reduction)
+        loss, lse = ops.ce_forward(l2d, ld, flat, ignore_index, 0.0, 0.0, label_smoothing)
+        ctx.fused = False
+        ctx.save_for_backward(l2d, flat, lse)
+        ctx.ld = ld
+        return reduce_rows(loss, flat, ignore_index, reduction)
 
     @staticmethod
     def backward(ctx, grad_output: Tensor):
-        l2d, labels, lse = ctx.saved_tensors
         ignore_index, label_smoothing, reduction = ctx.cfg
+        if ctx.fused:
+            (grad,) = ctx.saved_tensors
+            ops.scale_(grad, grad_output)
+            return grad.view(ctx.shape), None, None, None, None
+        l2d, labels, lse = ctx.saved_tensors
         n = l2d.shape[0]
-        if reduction == "mean":
-            dloss = grad_output.float() / (labels != ignore_index).sum().clamp(min=1)
-        elif reduction == "batchmean":
-            dloss = grad_output.float() / max(n, 1)
+        if reduction == "none":
+            dloss = grad_output.float().reshape(-1)
         else:
-            dloss = grad_output.float()
+            dloss = grad_output.float() * _row_weight(labels, ignore_index, reduction, n)
         grad = torch.empty(l2d.shape, dtype=l2d.dtype, device=l2d.device)
         ops.ce_backward(l2d, ctx.ld, labels, lse, dloss, grad, l2d.shape[1],
                         ignore_index=ignore_index, label_smoothing=label_smoothing)
-        return grad, None, None, None, None
+        return grad.view(ctx.shape), None, None, None, None
 
 
 class FusedCrossEntropyLoss(nn.Module):
@@ -152,7 +185,8 @@ class ChunkedCrossEntropyLoss(nn.Module):
 
     ``chunk_size`` is kept for signature compatibility; the gfx950 kernel walks
     the whole vocabulary row with an online max/sum and never materialises an
-    fp32 copy, so no chunking is needed.
+    fp32 copy, so no chunking is needed. With a reduction, the gradient is
+    formed in the forward pass (see FusedCrossEntropyFunction).
     """
 
     __constants__ = ["ignore_index", "label_smoothing", "reduction", "chunk_size"]
@@ -169,8 +203,8 @@ class ChunkedCrossEntropyLoss(nn.Module):
 
     def forward(self, logits: Tensor, labels: Tensor) -> Tensor:
         logits, labels = _flatten(logits, labels)
-        loss = CrossEntropyRowsFunction.apply(logits, labels, self.ignore_index,
-                                              self.label_smoothing)
-        if self.reduction == "batchmean":
-            return loss.mean()
-        return reduce_rows(loss, labels, self.ignore_index, self.reduction)
+        if self.reduction == "none":
+            return CrossEntropyRowsFunction.apply(logits, labels, self.ignore_index,
+                                                  self.label_smoothing)
+        return FusedCrossEntropyFunction.apply(logits, labels, self.ignore_index,
+                                               self.label_smoothing, self.reduction)

@@ -269,3 +269,61 @@ def ce_backward(logits2d: Tensor, ld: int, labels: Tensor, lse: Tensor, dloss: T
                             int(ignore_index), float(logit_scale), float(softcap),
                             float(label_smoothing), _lib.stream_handle(dev)), "ts_ce_bwd")
     return grad
+
+
+def ce_forward_backward(logits2d: Tensor, ld: int, labels: Tensor, dloss: Tensor,
+                        dloss_scale: float = 1.0, ignore_index: int = -100,
+                        logit_scale: float = 0.0, softcap: float = 0.0,
+                        label_smoothing: float = 0.0,
+                        grad_dtype: Optional[torch.dtype] = None,
+                        grad: Optional[Tensor] = None) -> Tuple[Tensor, Tensor, Tensor]:
+    """Per-row (loss, lse) and dL/dlogits for the upstream gradient `dloss` (fp32,
+    one value per row or a single value for every row) in one pass over the logits.
+    Returns (loss [N] fp32, lse [N] fp32, grad [N, V] in grad_dtype or the logits dtype);
+    `grad`, if given, is a contiguous [N, V] tensor to write into."""
+    dev = _lib.require_gpu("cross_entropy", logits2d, labels, dloss)
+    n, v = logits2d.shape
+    labels = _labels(labels, n)
+    if dloss.dtype != torch.float32:
+        dloss = dloss.float()
+    if dloss.numel() == 1:
+        dloss = dloss.reshape(1)
+        dstride = 0
+    else:
+        dloss = dloss.reshape(-1)
+        if dloss.shape[0] != n:
+            raise ValueError(f"cross_entropy: {dloss.shape[0]} upstream grads for {n} rows")
+        dstride = dloss.stride(0)
+    loss = torch.empty((n,), dtype=torch.float32, device=dev)
+    lse = torch.empty((n,), dtype=torch.float32, device=dev)
+    if grad is None:
+        grad = torch.empty((n, v), dtype=grad_dtype or logits2d.dtype, device=dev)
+    elif grad.shape != (n, v) or not grad.is_contiguous():
+        raise ValueError("cross_entropy: grad must be a contiguous [N, V] tensor")
+    if n == 0:
+        return loss, lse, grad
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_ce_fwd_bwd(ptr(logits2d), ld, _lib.dtype_code(logits2d, "cross_entropy"),
+                                ptr(labels), n, v, int(ignore_index), float(logit_scale),
+                                float(softcap), float(label_smoothing), ptr(dloss), dstride,
+                                float(dloss_scale), ptr(loss), ptr(lse), ptr(grad), v,
+                                _lib.dtype_code(grad, "cross_entropy grad"),
+                                _lib.stream_handle(dev)), "ts_ce_fwd_bwd")
+    return loss, lse, grad
+
+
+def scale_(t: Tensor, scale: Tensor) -> Tensor:
+    """t *= scale in place (scale: a one-element fp32 device tensor); a no-op on the
+    device when scale == 1, without synchronising."""
+    if t.numel() == 0:
+        return t
+    dev = _lib.require_gpu("scale_", t, scale)
+    if not t.is_contiguous():
+        raise ValueError("scale_: tensor must be contiguous")
+    scale = scale.detach().to(torch.float32).reshape(1).contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_scale_inplace(ptr(t), t.numel(), _lib.dtype_code(t, "scale_"), ptr(scale),
+                                   _lib.stream_handle(dev)), "ts_scale_inplace")
+    return t

@@ -159,6 +159,12 @@ def ce_bytes(n: int, n_valid: int, v: int, elt: int = 2) -> Dict[str, int]:
     return dict(fwd=fwd, bwd=bwd)
 
 
+def ce_bytes_fused(n: int, n_valid: int, v: int, elt: int = 2) -> int:
+    """Schedule B (loss and gradient in one pass): read every row with a label once,
+    write every row's gradient once; labels, loss and lse per row."""
+    return n_valid * v * elt + n * v * elt + n * (8 + 4 + 4)
+
+
 def linear_ce_flops(n: int, h: int, v: int) -> int:
     """Three GEMMs of 2*N*V*H: logits, grad_hidden, grad_weight."""
     return 3 * 2 * n * v * h
