@@ -260,6 +260,20 @@ ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight, i
 ts_status ts_scale_inplace(void* x, int64_t n, ts_dtype dtype, const float* scale,
                            ts_stream_t stream);
 
+/*
+ * x[i] *= *now / *used in place (same layout rules as ts_scale_inplace);
+ * nothing is written to x when the ratio is exactly 1. If hint_out is not
+ * NULL it receives *now when that is finite and non-zero, else 1 (it must
+ * not alias now or used). This lets a forward pass form a gradient for a
+ * predicted upstream gradient `used` (the previous step's, for a loss whose
+ * scale is fixed across steps, such as 1 / gradient-accumulation steps),
+ * and the backward pass correct it only when the prediction was wrong. No
+ * counterpart in the reference (its backward passes get the upstream
+ * gradient directly).
+ */
+ts_status ts_rescale_inplace(void* x, int64_t n, ts_dtype dtype, const float* now,
+                             const float* used, float* hint_out, ts_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

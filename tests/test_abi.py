@@ -109,3 +109,16 @@ def test_ce_validation(lib):
     rc = lib.ts_ce_bwd(FAKE, 128, 1, FAKE, FAKE, FAKE, 1, 1.0, FAKE, 128, 2, 4, 128, -100,
                        0.0, 0.0, 0.0, st)
     assert rc == DTYPE
+
+
+def test_scale_and_rescale_validation(lib):
+    st = NULL
+    assert lib.ts_scale_inplace(FAKE, 12, 1, FAKE, st) == SHAPE
+    assert lib.ts_scale_inplace(FAKE, 16, 9, FAKE, st) == DTYPE
+    assert lib.ts_scale_inplace(FAKE, 16, 1, NULL, st) == INVALID
+    assert lib.ts_rescale_inplace(FAKE, 16, 1, FAKE, NULL, NULL, st) == INVALID
+    hint = ctypes.c_void_p(0x2000)
+    assert lib.ts_rescale_inplace(FAKE, 16, 1, hint, FAKE, hint, st) == INVALID
+    assert b"aliases" in lib.ts_last_error()
+    assert lib.ts_rescale_inplace(FAKE, 16, 9, FAKE, FAKE, NULL, st) == DTYPE
+    assert lib.ts_scale_inplace(NULL, 0, 1, FAKE, st) == TS_OK

@@ -266,3 +266,45 @@ def test_c3_full_fused(gpu):
     # agrees with the two-pass schedule on every row's loss
     l2, _ = ops.ce_forward(logits, V, labels)
     torch.testing.assert_close(loss, l2, rtol=1e-6, atol=1e-6)
+
+
+def test_upstream_grad_hint_across_steps(gpu):
+    """A loss scaled the same way every step (1/4, as with 4 accumulation steps): the
+    first backward rescales the gradient formed for 1, later steps form it for 1/4
+    directly (ratio exactly 1, nothing rescaled); each step matches the oracle."""
+    torch.manual_seed(6)
+    N, V = 48, 4096
+    logits = (2 * torch.randn(N, V, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[7] = -100
+    lab = labels.cpu()
+    n_valid = int((lab != -100).sum())
+    mod = ChunkedCrossEntropyLoss()
+    for step, up in enumerate([0.25, 0.25, 0.25, 0.0, 0.5]):
+        x = logits.clone().requires_grad_()
+        (mod(x, labels) * up).backward()
+        ref_g = oracle.ce_bwd(logits.cpu(), lab, torch.tensor(up / n_valid))
+        assert_ulp(x.grad, ref_g, 1, tiny=TINY, what=f"step {step} upstream {up}")
+        hint = float(mod.grad_hint.get(x.device).item())
+        assert hint == (up if up != 0.0 else 1.0), (step, hint)
+    # two forwards before one backward: each node keeps the prediction it used
+    x = logits.clone().requires_grad_()
+    (0.5 * mod(x, labels) + 0.125 * mod(x, labels)).backward()
+    ref_g = oracle.ce_bwd(logits.cpu(), lab, torch.tensor(0.625 / n_valid))
+    assert_ulp(x.grad, ref_g, 2, tiny=TINY, what="two nodes")
+
+
+def test_rescale_inplace_ratio_and_hint(gpu):
+    t = torch.randn(4096, device=gpu).to(BF)
+    orig = t.clone()
+    now = torch.tensor([0.75], device=gpu)
+    used = torch.tensor([0.75], device=gpu)
+    hint = torch.zeros(1, device=gpu)
+    ops.rescale_(t, now, used, hint)
+    assert torch.equal(t, orig) and hint.item() == 0.75
+    used.fill_(1.5)
+    ops.rescale_(t, now, used, hint)
+    torch.testing.assert_close(t.float(), (orig.float() * 0.5).to(BF).float(), rtol=0, atol=0)
+    now.fill_(float("inf"))
+    ops.rescale_(t[:0], now, used, hint)  # empty tensor: only the hint is written
+    assert hint.item() == 1.0

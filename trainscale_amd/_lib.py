@@ -74,6 +74,7 @@ SIGNATURES = {
     "ts_flce_fwd_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, P, P, P, P, P, I64, P, SZ, P],
                         I32),
     "ts_scale_inplace": ([P, I64, I32, P, P], I32),
+    "ts_rescale_inplace": ([P, I64, I32, P, P, P, P], I32),
 }
 
 _lock = threading.Lock()

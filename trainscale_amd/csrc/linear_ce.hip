@@ -331,21 +331,46 @@ __global__ __launch_bounds__(256) void fill_zero_u32(uint32_t* __restrict__ p, i
   if (i == 0 && loss != nullptr) *loss = 0.f;
 }
 
-// x[i] *= *scale unless *scale == 1 (then the kernel only reads the scalar);
-// nvec 16-byte vectors of element type T.
+// x[i] *= *scale unless *scale == 1, over nvec 16-byte vectors of element
+// type T. The grid is capped (kScaleGrid workgroups, each thread four vectors
+// per sweep) so that the common no-op case, an upstream gradient of exactly
+// 1, costs little more than a launch.
+constexpr int kScaleGrid = 2048;
+constexpr int kScaleUnroll = 4;
+// The factor is *num, or *num / *den when den is given. With hint_out, the
+// first thread also stores *num there when it is finite and non-zero (else
+// 1): the prediction a later forward pass uses for the upstream gradient.
 template <typename T>
 __global__ __launch_bounds__(256) void scale_inplace(T* __restrict__ x, int64_t nvec,
-                                                     const float* __restrict__ scale_p) {
+                                                     const float* __restrict__ num,
+                                                     const float* __restrict__ den,
+                                                     float* __restrict__ hint_out) {
   constexpr int VE = Elt<T>::kVec;
-  const float s = *scale_p;
+  const float g = *num;
+  if (hint_out != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+    *hint_out = (__builtin_isfinite(g) && g != 0.f) ? g : 1.f;
+  const float s = den != nullptr ? g / *den : g;
   if (s == 1.f) return;
-  for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < nvec;
-       v += (int64_t)gridDim.x * 256) {
-    float f[VE];
-    Elt<T>::unpack(ld16(x + v * VE), f);
+  const int64_t stride = (int64_t)gridDim.x * 256 * kScaleUnroll;
+  for (int64_t v0 = (int64_t)blockIdx.x * 256 * kScaleUnroll + threadIdx.x; v0 < nvec;
+       v0 += stride) {
+    u32x4 q[kScaleUnroll];
 #pragma unroll
-    for (int e = 0; e < VE; ++e) f[e] *= s;
-    st16(x + v * VE, Elt<T>::pack(f));
+    for (int u = 0; u < kScaleUnroll; ++u) {
+      const int64_t v = v0 + u * 256;
+      if (v < nvec) q[u] = ld16_stream(x + v * VE);
+    }
+#pragma unroll
+    for (int u = 0; u < kScaleUnroll; ++u) {
+      const int64_t v = v0 + u * 256;
+      if (v < nvec) {
+        float f[VE];
+        Elt<T>::unpack(q[u], f);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) f[e] *= s;
+        st16_stream(x + v * VE, Elt<T>::pack(f));
+      }
+    }
   }
 }
 
@@ -555,35 +580,54 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   return ts_host::check_launch("flce_loss");
 }
 
-extern "C" ts_status ts_scale_inplace(void* x, int64_t n, ts_dtype dtype, const float* scale,
-                                      ts_stream_t stream) {
+namespace {
+ts_status scale_launch(const char* what, void* x, int64_t n, ts_dtype dtype, const float* num,
+                       const float* den, float* hint_out, hipStream_t st) {
   if (!ts_host::valid_dtype(dtype))
-    return ts_host::fail(TS_ERR_UNSUPPORTED_DTYPE, "scale_inplace: bad dtype");
+    return ts_host::fail(TS_ERR_UNSUPPORTED_DTYPE, "%s: bad dtype", what);
   const int64_t per = dtype == TS_F32 ? 4 : 8;
   if (n < 0 || n % per != 0)
-    return ts_host::fail(TS_ERR_SHAPE,
-                         "scale_inplace: n must be a non-negative multiple of %lld",
+    return ts_host::fail(TS_ERR_SHAPE, "%s: n must be a non-negative multiple of %lld", what,
                          (long long)per);
-  if (n > 0 && (x == nullptr || scale == nullptr || !ts_host::aligned16(x)))
-    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "scale_inplace: bad pointer");
-  if (n == 0) return TS_OK;
+  if (num == nullptr) return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "%s: NULL factor", what);
+  if (n > 0 && (x == nullptr || !ts_host::aligned16(x)))
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "%s: bad pointer", what);
+  if (hint_out != nullptr && (hint_out == num || hint_out == den))
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "%s: hint_out aliases an input", what);
+  if (n == 0 && hint_out == nullptr) return TS_OK;
   const int64_t nvec = n / per;
-  int64_t blocks = (nvec + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  int64_t blocks = (nvec + 256 * kScaleUnroll - 1) / (256 * kScaleUnroll);
+  if (blocks > kScaleGrid) blocks = kScaleGrid;
+  if (blocks < 1) blocks = 1;
   switch (dtype) {
     case TS_BF16:
       hipLaunchKernelGGL(scale_inplace<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
-                         static_cast<__bf16*>(x), nvec, scale);
+                         static_cast<__bf16*>(x), nvec, num, den, hint_out);
       break;
     case TS_F16:
       hipLaunchKernelGGL(scale_inplace<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st,
-                         static_cast<_Float16*>(x), nvec, scale);
+                         static_cast<_Float16*>(x), nvec, num, den, hint_out);
       break;
     case TS_F32:
       hipLaunchKernelGGL(scale_inplace<float>, dim3((unsigned)blocks), dim3(256), 0, st,
-                         static_cast<float*>(x), nvec, scale);
+                         static_cast<float*>(x), nvec, num, den, hint_out);
       break;
   }
-  return ts_host::check_launch("scale_inplace");
+  return ts_host::check_launch(what);
+}
+}  // namespace
+
+extern "C" ts_status ts_scale_inplace(void* x, int64_t n, ts_dtype dtype, const float* scale,
+                                      ts_stream_t stream) {
+  return scale_launch("scale_inplace", x, n, dtype, scale, nullptr, nullptr,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" ts_status ts_rescale_inplace(void* x, int64_t n, ts_dtype dtype, const float* now,
+                                        const float* used, float* hint_out,
+                                        ts_stream_t stream) {
+  if (used == nullptr)
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rescale_inplace: NULL used factor");
+  return scale_launch("rescale_inplace", x, n, dtype, now, used, hint_out,
+                      static_cast<hipStream_t>(stream));
 }

@@ -16,6 +16,7 @@ from .sota_losses import (
     CrossEntropyRowsFunction,
     FusedCrossEntropyFunction,
     FusedCrossEntropyLoss,
+    UpstreamGradHint,
     reduce_rows,
 )
 
@@ -25,6 +26,7 @@ __all__ = [
     "FusedCrossEntropyLoss",
     "FusedCrossEntropyFunction",
     "CrossEntropyRowsFunction",
+    "UpstreamGradHint",
     "LinearCrossEntropyFunction",
     "fused_linear_cross_entropy",
 ]
@@ -45,6 +47,7 @@ class CrossEntropyLoss(nn.Module):
         self.reduction = reduction
         # Accepted for signature compatibility; every path runs the gfx950 kernels.
         self.use_triton = use_triton
+        self.grad_hint = UpstreamGradHint()
 
     def forward(self, logits: Tensor, labels: Tensor) -> Tensor:
         if logits.dim() == 3:
@@ -54,4 +57,5 @@ class CrossEntropyLoss(nn.Module):
             return CrossEntropyRowsFunction.apply(logits, labels, self.ignore_index,
                                                   self.label_smoothing)
         return FusedCrossEntropyFunction.apply(logits, labels, self.ignore_index,
-                                               self.label_smoothing, self.reduction)
+                                               self.label_smoothing, self.reduction,
+                                               self.grad_hint)

@@ -30,6 +30,7 @@ from .. import ops
 
 __all__ = [
     "CrossEntropyRowsFunction",
+    "UpstreamGradHint",
     "FusedCrossEntropyFunction",
     "FusedCrossEntropyLoss",
     "ChunkedCrossEntropyLoss",
@@ -98,22 +99,44 @@ def _row_weight(labels: Tensor, ignore_index: int, reduction: str, n: int) -> Te
     return torch.ones((1,), dtype=torch.float32, device=labels.device)
 
 
+class UpstreamGradHint:
+    """Prediction of a loss's upstream gradient, one fp32 device scalar per device.
+
+    A trainer scales the loss the same way every step (the reference divides it
+    by gradient_accumulation_steps, trainers/sota_trainer.py:2190, which is 4 in
+    its ROCm configs), so the upstream gradient of step t predicts that of step
+    t+1. The forward pass forms the gradient for the prediction; backward
+    corrects it by now/predicted, which is exactly 1 (nothing written) once the
+    prediction holds, and records the new value. All on the device, no sync.
+    """
+
+    def __init__(self) -> None:
+        self._per_device = {}
+
+    def get(self, device: torch.device) -> Tensor:
+        t = self._per_device.get(device)
+        if t is None:
+            t = torch.ones((1,), dtype=torch.float32, device=device)
+            self._per_device[device] = t
+        return t
+
+
 class FusedCrossEntropyFunction(torch.autograd.Function):
     """Reduced cross-entropy in one autograd node (reference: loss/sota_losses.py:437-532).
 
     For mean, sum and batchmean the gradient is formed in the forward pass in
     the same read of the logits that yields the loss (ts_ce_fwd_bwd: one read
-    of each valid row, one write of each gradient row), for an upstream
-    gradient of 1; backward scales it in place by the actual upstream gradient,
-    on the device and only when that is not 1. Without a gradient to compute
-    (no_grad, eval) only the forward kernel runs. reduction="none" keeps the
-    two-pass schedule, since per-row upstream gradients are unknown until
-    backward.
+    of each valid row, one write of each gradient row), for a predicted
+    upstream gradient (``hint``, an UpstreamGradHint, else 1); backward
+    rescales it in place by actual/predicted, on the device and only when the
+    ratio is not 1. Without a gradient to compute (no_grad, eval) only the
+    forward kernel runs. reduction="none" keeps the two-pass schedule, since
+    per-row upstream gradients are unknown until backward.
     """
 
     @staticmethod
     def forward(ctx, logits: Tensor, labels: Tensor, ignore_index: int, label_smoothing: float,
-                reduction: str) -> Tensor:
+                reduction: str, hint: Optional[UpstreamGradHint] = None) -> Tensor:
         if reduction not in _REDUCTIONS:
             raise ValueError(f"Invalid reduction: {reduction}")
         l2d, ld = ops.as_rows(logits)
@@ -122,10 +145,17 @@ class FusedCrossEntropyFunction(torch.autograd.Function):
         ctx.cfg = (ignore_index, label_smoothing, reduction)
         if reduction != "none" and ctx.needs_input_grad[0]:
             w = _row_weight(flat, ignore_index, reduction, l2d.shape[0])
+            if hint is not None:
+                ctx.hint = hint.get(l2d.device)
+                used = ctx.hint.clone()
+                w = w * used
+            else:
+                ctx.hint = None
+                used = None
             loss, _, grad = ops.ce_forward_backward(l2d, ld, flat, w, 1.0, ignore_index, 0.0, 0.0,
                                                     label_smoothing)
             ctx.fused = True
-            ctx.save_for_backward(grad)
+            ctx.save_for_backward(grad, used)
             return reduce_rows(loss, flat, ignore_index, reduction)
         loss, lse = ops.ce_forward(l2d, ld, flat, ignore_index, 0.0, 0.0, label_smoothing)
         ctx.fused = False
@@ -137,9 +167,12 @@ class FusedCrossEntropyFunction(torch.autograd.Function):
     def backward(ctx, grad_output: Tensor):
         ignore_index, label_smoothing, reduction = ctx.cfg
         if ctx.fused:
-            (grad,) = ctx.saved_tensors
-            ops.scale_(grad, grad_output)
-            return grad.view(ctx.shape), None, None, None, None
+            grad, used = ctx.saved_tensors
+            if used is None:
+                ops.scale_(grad, grad_output)
+            else:
+                ops.rescale_(grad, grad_output, used, ctx.hint)
+            return grad.view(ctx.shape), None, None, None, None, None
         l2d, labels, lse = ctx.saved_tensors
         n = l2d.shape[0]
         if reduction == "none":
@@ -149,7 +182,7 @@ class FusedCrossEntropyFunction(torch.autograd.Function):
         grad = torch.empty(l2d.shape, dtype=l2d.dtype, device=l2d.device)
         ops.ce_backward(l2d, ctx.ld, labels, lse, dloss, grad, l2d.shape[1],
                         ignore_index=ignore_index, label_smoothing=label_smoothing)
-        return grad.view(ctx.shape), None, None, None, None
+        return grad.view(ctx.shape), None, None, None, None, None
 
 
 class FusedCrossEntropyLoss(nn.Module):
@@ -169,11 +202,13 @@ class FusedCrossEntropyLoss(nn.Module):
         self.ignore_index = ignore_index
         self.label_smoothing = label_smoothing
         self.reduction = reduction
+        self.grad_hint = UpstreamGradHint()
 
     def forward(self, logits: Tensor, labels: Tensor) -> Tensor:
         logits, labels = _flatten(logits, labels)
         return FusedCrossEntropyFunction.apply(logits, labels, self.ignore_index,
-                                               self.label_smoothing, self.reduction)
+                                               self.label_smoothing, self.reduction,
+                                               self.grad_hint)
 
     def extra_repr(self) -> str:
         return (f"ignore_index={self.ignore_index}, label_smoothing={self.label_smoothing}, "
@@ -200,6 +235,7 @@ class ChunkedCrossEntropyLoss(nn.Module):
         self.label_smoothing = label_smoothing
         self.reduction = reduction
         self.chunk_size = chunk_size
+        self.grad_hint = UpstreamGradHint()
 
     def forward(self, logits: Tensor, labels: Tensor) -> Tensor:
         logits, labels = _flatten(logits, labels)
@@ -207,4 +243,5 @@ class ChunkedCrossEntropyLoss(nn.Module):
             return CrossEntropyRowsFunction.apply(logits, labels, self.ignore_index,
                                                   self.label_smoothing)
         return FusedCrossEntropyFunction.apply(logits, labels, self.ignore_index,
-                                               self.label_smoothing, self.reduction)
+                                               self.label_smoothing, self.reduction,
+                                               self.grad_hint)

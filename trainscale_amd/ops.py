@@ -327,3 +327,23 @@ def scale_(t: Tensor, scale: Tensor) -> Tensor:
         check(lib.ts_scale_inplace(ptr(t), t.numel(), _lib.dtype_code(t, "scale_"), ptr(scale),
                                    _lib.stream_handle(dev)), "ts_scale_inplace")
     return t
+
+
+def rescale_(t: Tensor, now: Tensor, used: Tensor, hint_out: Optional[Tensor] = None) -> Tensor:
+    """t *= now / used in place (one-element fp32 device tensors); a no-op on the device
+    when the ratio is exactly 1. hint_out (one-element fp32, distinct from now and used)
+    receives now when finite and non-zero, else 1."""
+    dev = _lib.require_gpu("rescale_", t, now, used)
+    if not t.is_contiguous():
+        raise ValueError("rescale_: tensor must be contiguous")
+    now = now.detach().to(torch.float32).reshape(1).contiguous()
+    used = used.detach().to(torch.float32).reshape(1).contiguous()
+    if hint_out is not None and (hint_out.dtype != torch.float32 or hint_out.numel() != 1
+                                 or hint_out.device != t.device):
+        raise ValueError("rescale_: hint_out must be a one-element fp32 tensor on the device")
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_rescale_inplace(ptr(t), t.numel(), _lib.dtype_code(t, "rescale_"),
+                                     ptr(now), ptr(used), ptr(hint_out),
+                                     _lib.stream_handle(dev)), "ts_rescale_inplace")
+    return t
