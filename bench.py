@@ -175,6 +175,36 @@ def time_ms(fn, steps: int, warmup: int) -> float:
     return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
 
 
+def device_reference(dev):
+    """Measured reference points of this GPU, next to the published peaks: a plain
+    device-to-device copy of 1 GiB (read + write, the HIP runtime's copy kernel) and a
+    large bf16 GEMM from hipBLASLt (torch.matmul, 8192^3)."""
+    import torch
+
+    nbytes = 1 << 30
+    bufs = [(torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1),
+             torch.empty(nbytes, dtype=torch.uint8, device=dev)) for _ in range(2)]
+    it = iter(range(1 << 30))
+
+    def copy():
+        a, b = bufs[next(it) % 2]
+        b.copy_(a)
+
+    copy_ms = time_ms(copy, 10, 2)
+    del bufs
+    g = torch.Generator(device=dev).manual_seed(7)
+    m = 8192
+    a = torch.randn(m, m, device=dev, generator=g).to(torch.bfloat16)
+    b = torch.randn(m, m, device=dev, generator=g).to(torch.bfloat16)
+    gemm_ms = time_ms(lambda: torch.matmul(a, b), 10, 2)
+    del a, b
+    torch.cuda.empty_cache()
+    return {"d2d_copy_GB_s": round(2 * nbytes / (copy_ms * 1e-3) / 1e9, 1),
+            "d2d_copy_bytes": nbytes,
+            "hipblaslt_bf16_gemm_TFLOP_s": round(2 * m ** 3 / (gemm_ms * 1e-3) / 1e12, 1),
+            "gemm_shape": [m, m, m]}
+
+
 def bench_packed(dev, steps: int, warmup: int):
     """C4: packed varlen RMSNorm [32768, 8192] and RoPE (64q + 8k heads) with position_ids."""
     import torch
@@ -419,6 +449,7 @@ def main():
     del c1, c2, c3, x, w, dy, x2d, dy2d, q, k, dq, dk, q_out, k_out, dq_out, dk_out
     del logits, labels, grad, state, upstream
     torch.cuda.empty_cache()
+    out["device_reference"] = device_reference(dev)
     if not args.no_extra:
         out["c4_packed"] = bench_packed(dev, args.steps, args.warmup)
         out["c5_linear_ce"] = bench_linear_ce(dev, args.steps, args.warmup,
