@@ -14,7 +14,8 @@
 // three k-blocks of loads in flight while the MFMAs consume one (a fifth
 // stage, the whole 160 KiB of a CU, measured slower on MI355X); one barrier
 // per k-block, and the MFMA operand fragments are double-buffered in registers
-// so every LDS read overlaps MFMAs (see mainloop). Buffer resources make
+// with the LDS reads and global loads interleaved between MFMAs (see
+// mainloop). Buffer resources make
 // out-of-range rows (and the k tail) read as zeros, so partial tiles need no
 // branches.
 //
@@ -173,15 +174,60 @@ __device__ inline void mma_frags(const Frags& f, Acc& acc) {
       acc.t[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.t[i][j], 0, 0, 0);
 }
 
+// Instruction interleaving. A wave issues MFMAs one at a time and waits for
+// the matrix core to accept each; other instructions placed between two MFMAs
+// issue in the shadow of the first for free. These scheduling groups ask the
+// compiler for such an order (the grouped instructions are independent of
+// the MFMAs they sit between).
+//
+// 16 MFMAs, the first 8 each followed by one LDS read.
+__device__ inline void sched_mfma_lds() {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+}
+// 16 - kPreBarrier MFMAs: 8 each followed by a global->LDS load, then the rest
+// each followed by an LDS read.
+constexpr int kPreBarrier = 2;  // MFMAs issued before the barrier (see mainloop)
+__device__ inline void sched_mfma_vmem_lds() {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (to LDS)
+  }
+#pragma unroll
+  for (int i = 0; i < 8 - kPreBarrier; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+}
+
+// MFMA q (0..15) of a k-step: tile (q / 4, q % 4).
+__device__ inline void mma_one(const Frags& f, Acc& acc, int q) {
+  acc.t[q / 4][q % 4] =
+      __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[q / 4], f.b[q % 4], acc.t[q / 4][q % 4], 0, 0, 0);
+}
+
 // Main loop for the tile at (m0, n0). `smem` holds kLdsBytes (16-byte aligned).
 //
-// Per k-block kt (two 16-deep k-steps):
-//   read fragments (kt, 1)            | MFMAs (kt, 0)
-//   wait for stage kt+1, barrier, issue global loads of stage kt+3 into the
-//   buffer of stage kt-1 (consumed by every wave before the barrier)
-//   read fragments (kt+1, 0)          | MFMAs (kt, 1)
-// so LDS reads always overlap MFMAs of the other fragment set, and global
-// loads run two to three k-blocks ahead.
+// Steady state, per k-block kt (two 16-deep k-steps, 16 MFMAs each):
+//   MFMAs (kt, 0), interleaved with the LDS reads of fragments (kt, 1)
+//   kPreBarrier MFMAs of (kt, 1), so the matrix core stays busy while the
+//   wave waits for stage kt+1 and the workgroup barrier
+//   the other MFMAs of (kt, 1), interleaved with the global->LDS loads of
+//   stage kt+3 (into the buffer of stage kt-1, which every wave finished
+//   reading before the barrier) and the LDS reads of fragments (kt+1, 0)
+// Global loads run two to three k-blocks ahead. The last kStages-1 k-blocks
+// issue no loads and run a plain drain loop, so the steady-state body has no
+// branches (a branch there splits the interleaved block and makes the
+// register allocator shuffle the accumulators).
+//
+// Measured at 8192 x 128256 x 4096 (main loop only, on MI355X): 1446
+// TFLOP/s, against 1219 TFLOP/s with the LDS reads and loads issued in
+// blocks between the MFMA groups.
 __device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64_t M,
                                 const __bf16* __restrict__ B, int64_t ldb, int64_t N, int64_t K,
                                 int64_t m0, int64_t n0, uint8_t* smem, Acc& acc) {
@@ -212,22 +258,41 @@ __device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64
   Frags f0, f1;
   read_frags(smem, smem + kTileBytes, wm, wn, lane, 0, f0);
 
-  for (int64_t kt = 0; kt < KT; ++kt) {
+  int64_t kt = 0;
+  for (; kt + kStages - 1 < KT; ++kt) {
+    const uint8_t* As = smem + (kt % kStages) * kStageBytes;
+    read_frags(As, As + kTileBytes, wm, wn, lane, 1, f1);
+    mma_frags(f0, acc);
+    sched_mfma_lds();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < kPreBarrier; ++q) mma_one(f1, acc, q);
+    __builtin_amdgcn_sched_barrier(0);
+    // stage kt+1 landed: stages kt+2 .. kt+kStages-2 may remain in flight
+    wait_stage(kStages - 3);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const int s = (int)((kt + kStages - 1) % kStages);
+    issue_loads(la, (kt + kStages - 1) * BK, K, smem + s * kStageBytes);
+    issue_loads(lb, (kt + kStages - 1) * BK, K, smem + s * kStageBytes + kTileBytes);
+    const uint8_t* An = smem + ((kt + 1) % kStages) * kStageBytes;
+    read_frags(An, An + kTileBytes, wm, wn, lane, 0, f0);
+#pragma unroll
+    for (int q = kPreBarrier; q < 16; ++q) mma_one(f1, acc, q);
+    sched_mfma_vmem_lds();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // drain: the last k-blocks, no loads left to issue
+  for (; kt < KT; ++kt) {
     const uint8_t* As = smem + (kt % kStages) * kStageBytes;
     read_frags(As, As + kTileBytes, wm, wn, lane, 1, f1);
     __builtin_amdgcn_sched_barrier(0);
     mma_frags(f0, acc);
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < KT) {
-      // stage kt+1 landed: stages kt+2 .. kt+kStages-2 may remain in flight
       const int64_t later = KT - 2 - kt;
       wait_stage(later < kStages - 3 ? later : kStages - 3);
       __builtin_amdgcn_s_barrier();
-      if (kt + kStages - 1 < KT) {
-        const int s = (int)((kt + kStages - 1) % kStages);
-        issue_loads(la, (kt + kStages - 1) * BK, K, smem + s * kStageBytes);
-        issue_loads(lb, (kt + kStages - 1) * BK, K, smem + s * kStageBytes + kTileBytes);
-      }
       const uint8_t* An = smem + ((kt + 1) % kStages) * kStageBytes;
       read_frags(An, An + kTileBytes, wm, wn, lane, 0, f0);
     }

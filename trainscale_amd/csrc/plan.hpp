@@ -165,19 +165,27 @@ inline uint32_t magic_div(uint32_t n, uint32_t magic) {
 inline bool magic_exact(uint64_t n_max, uint64_t d) { return n_max * d < ((uint64_t)1 << 32); }
 
 // ---------------------------------------------------------------------------
-// GEMM tile order: workgroup `bid` of MT x NT output tiles, in groups of
-// kGemmGroupM M-tiles; inside a group M-tiles vary fastest, then N-tiles. The
-// ~256 workgroups resident at a time then cover about 16 M-tiles x 16
-// N-tiles, so both operands' tiles are shared by many concurrent workgroups
-// whatever the aspect ratio of C (a tall grad-weight output included).
+// GEMM tile order. The dispatcher sends workgroup `bid` to XCD bid % 8, and
+// each XCD has its own L2. Workgroups are first renumbered so that each XCD
+// gets one contiguous range of logical tiles (XCD x takes the x-th eighth),
+// and logical tiles run in groups of kGemmGroupM M-tiles with M-tiles
+// varying fastest, then N-tiles. The 32 workgroups an XCD holds at a time
+// then cover about 4 M-tiles x 8 N-tiles, whose operand panels its L2
+// shares. Measured on MI355X at the fused linear-CE shapes (random bf16
+// data): 4-11% faster than the same grouping without the XCD renumbering
+// and 16 M-tiles per group.
 // ---------------------------------------------------------------------------
-constexpr int64_t kGemmGroupM = 16;
+constexpr int64_t kGemmGroupM = 4;
+constexpr int64_t kXcds = 8;
 
 TS_HOST_DEVICE inline void gemm_tile_of(int64_t bid, int64_t MT, int64_t NT, int64_t& mt,
                                         int64_t& nt) {
+  const int64_t T = MT * NT;
+  const int64_t x = bid % kXcds, i = bid / kXcds, q = T / kXcds, r = T % kXcds;
+  const int64_t t = x * q + (x < r ? x : r) + i;  // logical tile
   const int64_t per_group = kGemmGroupM * NT;
-  const int64_t g = bid / per_group;
-  const int64_t w = bid - g * per_group;
+  const int64_t g = t / per_group;
+  const int64_t w = t - g * per_group;
   const int64_t gm = MT - g * kGemmGroupM < kGemmGroupM ? MT - g * kGemmGroupM : kGemmGroupM;
   mt = g * kGemmGroupM + w % gm;
   nt = w / gm;

@@ -26,8 +26,11 @@ from .._lib import check, ptr
 
 __all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy", "DEFAULT_LOGITS_SCRATCH"]
 
-# Upper bound on the bf16 logits scratch of one token chunk.
-DEFAULT_LOGITS_SCRATCH = 1 << 30
+# Upper bound on the bf16 logits scratch of one token chunk. 4 GiB keeps a
+# batch of up to 16384 tokens at V = 128256 in one chunk (one grad-weight GEMM
+# with a bf16 epilogue instead of an fp32 accumulator read and written per
+# chunk); against 288 GB of HBM the scratch is small.
+DEFAULT_LOGITS_SCRATCH = 4 << 30
 
 _REDUCTIONS = {"mean": 0, "sum": 1}
 
