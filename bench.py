@@ -256,6 +256,45 @@ def bench_packed(dev, steps: int, warmup: int):
             "kernels": res}
 
 
+def bench_next_rows(dev, steps: int, warmup: int):
+    """Rows beyond the hot path's five configs: fused residual add + RMSNorm forward at
+    the C1 and C4 shapes, and SwiGLU forward + backward at the Llama-3-8B MLP shape
+    [8, 2048, 14336]. Synthetic seeded inputs, each op timed alone."""
+    import torch
+
+    from trainscale_amd import ops
+    from trainscale_amd import workloads as W
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    res = {}
+    for name, rows, cols in (("add_rmsnorm_fwd_c1", 16384, 4096),
+                             ("add_rmsnorm_fwd_c4", 32768, 8192)):
+        x = torch.randn(rows, cols, device=dev, generator=g).to(torch.bfloat16)
+        r = torch.randn(rows, cols, device=dev, generator=g).to(torch.bfloat16)
+        w = (1 + 0.02 * torch.randn(cols, device=dev, generator=g)).to(torch.bfloat16)
+        ms = time_ms(lambda: ops.add_rmsnorm_forward(x, cols, r, cols, w, 1e-6), steps, warmup)
+        b = W.add_rmsnorm_bytes(rows, cols)
+        res[name] = {"shape": [rows, cols], "ms": round(ms, 4), "bytes": b,
+                     "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del x, r, w
+    shape = (8, 2048, 14336)
+    gate = (3 * torch.randn(shape, device=dev, generator=g)).to(torch.bfloat16)
+    up = torch.randn(shape, device=dev, generator=g).to(torch.bfloat16)
+    dout = torch.randn(shape, device=dev, generator=g).to(torch.bfloat16)
+    n = gate.numel()
+    sb = W.swiglu_bytes(n)
+    for name, fn, b in (("swiglu_fwd", lambda: ops.swiglu_forward(gate, up), sb["fwd"]),
+                        ("swiglu_bwd", lambda: ops.swiglu_backward(dout, gate, up), sb["bwd"])):
+        ms = time_ms(fn, steps, warmup)
+        res[name] = {"shape": list(shape), "ms": round(ms, 4), "bytes": b,
+                     "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del gate, up, dout
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_linear_ce(dev, steps: int, warmup: int, cpu: bool, cpu_seconds: float):
     """C5: fused linear CE fwd+bwd (loss, grad_hidden, grad_weight) in one call."""
     import torch
@@ -455,6 +494,7 @@ def main():
         out["c5_linear_ce"] = bench_linear_ce(dev, args.steps, args.warmup,
                                               cpu=not args.no_cpu_baseline,
                                               cpu_seconds=args.cpu_seconds)
+        out["next_rows"] = bench_next_rows(dev, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -79,6 +79,27 @@ ts_status ts_rmsnorm_fwd(const void* x, int64_t ldx, ts_dtype x_dtype,
                          int64_t rows, int64_t cols, float eps,
                          int32_t round_mode, ts_stream_t stream);
 
+/*
+ * Fused residual add + RMSNorm:
+ *   h = x + residual (fp32),  rstd[r] = 1 / sqrt(mean(h[r, :]^2) + eps),
+ *   y = h * rstd * w with round_mode as in ts_rmsnorm_fwd,
+ *   h_out = h rounded to x_dtype when h_out is not NULL.
+ * x, residual, y, h_out: [rows, cols] of x_dtype with row strides ldx, ldr,
+ * ldy, ldh. rstd comes from the unrounded h; the backward pass is
+ * ts_rmsnorm_bwd with x = h_out (the rounded h, as the reference saves it).
+ * Replaces _fused_add_rms_layernorm_kernel, kernels/layernorm_kernels.py:495-552,
+ * launched by FusedAddRMSLayerNormFunction.forward, layernorm_kernels.py:957-1009
+ * (which uses round-twice numerics: y = h_norm.to(w.dtype) * w).
+ */
+ts_status ts_add_rmsnorm_fwd(const void* x, int64_t ldx,
+                             const void* residual, int64_t ldr, ts_dtype x_dtype,
+                             const void* w, ts_dtype w_dtype,
+                             void* y, int64_t ldy,
+                             void* h_out, int64_t ldh,
+                             float* rstd,
+                             int64_t rows, int64_t cols, float eps,
+                             int32_t round_mode, ts_stream_t stream);
+
 /* Bytes of workspace ts_rmsnorm_bwd needs for these sizes (dW partial sums). */
 size_t ts_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols);
 
@@ -101,6 +122,30 @@ ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy,
                          void* dw,
                          void* workspace, size_t workspace_bytes,
                          int64_t rows, int64_t cols, ts_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* SwiGLU                                                                    */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * out = round(round(silu(gate)) * up),  silu(g) = g * sigmoid(g), fp32 math,
+ * over n contiguous elements of dtype (silu is rounded to the data type
+ * before the product, as the reference does).
+ * Replaces _swiglu_forward_kernel, kernels/triton_kernels.py:1042-1067,
+ * launched by Fast_SwiGLU.forward, triton_kernels.py:1108-1127.
+ */
+ts_status ts_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n,
+                        ts_dtype dtype, ts_stream_t stream);
+
+/*
+ * dgate = dout * up * sigmoid(g) * (1 + g * (1 - sigmoid(g))),
+ * dup = dout * silu(g), fp32 math, over n contiguous elements.
+ * Replaces _swiglu_backward_kernel, kernels/triton_kernels.py:1069-1101,
+ * launched by Fast_SwiGLU.backward, triton_kernels.py:1129-1143.
+ */
+ts_status ts_swiglu_bwd(const void* dout, const void* gate, const void* up,
+                        void* dgate, void* dup, int64_t n, ts_dtype dtype,
+                        ts_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Rotary position embedding                                                 */

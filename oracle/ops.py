@@ -15,6 +15,7 @@ from torch import Tensor
 
 __all__ = [
     "rms_norm_fwd",
+    "add_rms_norm_fwd",
     "rms_norm_bwd",
     "rope_inv_freq",
     "rope_tables",
@@ -23,6 +24,8 @@ __all__ = [
     "ce_fwd",
     "ce_bwd",
     "linear_ce",
+    "swiglu_fwd",
+    "swiglu_bwd",
 ]
 
 
@@ -58,6 +61,32 @@ def rms_norm_fwd(x: Tensor, w: Optional[Tensor], eps: float = 1e-6,
     else:
         y = xn
     return y.to(x.dtype).reshape(x.shape), rstd
+
+
+def add_rms_norm_fwd(x: Tensor, r: Tensor, w: Optional[Tensor], eps: float = 1e-6,
+                     round_twice: bool = True) -> Tuple[Tensor, Tensor, Tensor]:
+    """Residual add + RMSNorm: h = x + r in fp32, rstd from the unrounded h,
+    y = h * rstd * w (round_twice: y = round(round(h*rstd) * w) for a 16-bit w of
+    x's dtype), and h rounded once to x.dtype.
+
+    Restates _fused_add_rms_layernorm_kernel (kernels/layernorm_kernels.py:528-552)
+    as FusedAddRMSLayerNormFunction.forward launches it (:957-1009). Returns
+    (y, h, rstd fp32 [rows]); the backward is rms_norm_bwd on the rounded h
+    (:1011-1045).
+    """
+    x, r, w = _cpu(x), _cpu(r), _cpu(w)
+    c = x.shape[-1]
+    h32 = x.reshape(-1, c).float() + r.reshape(-1, c).float()
+    rstd = 1.0 / torch.sqrt((h32 * h32).sum(-1) / c + eps)
+    hn = h32 * rstd[:, None]
+    if w is not None:
+        if round_twice and w.dtype == x.dtype and x.dtype != torch.float32:
+            y = hn.to(x.dtype).float() * w.float()
+        else:
+            y = hn * w.float()
+    else:
+        y = hn
+    return y.to(x.dtype).reshape(x.shape), h32.to(x.dtype).reshape(x.shape), rstd
 
 
 def rms_norm_bwd(dy: Tensor, x: Tensor, w: Optional[Tensor],
@@ -243,3 +272,29 @@ def linear_ce(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int 
     if return_rows:
         return loss, grad_h, grad_w, loss_rows, lse
     return loss, grad_h, grad_w
+
+
+def swiglu_fwd(gate: Tensor, up: Tensor) -> Tensor:
+    """out = (silu(g) rounded to up.dtype) * up, silu(g) = g * sigmoid(g) in fp32.
+
+    Restates _swiglu_forward_kernel (kernels/triton_kernels.py:1058-1066):
+    silu.to(up.dtype) * up, the product of two values of up's dtype formed in
+    fp32 and rounded once more.
+    """
+    gate, up = _cpu(gate), _cpu(up)
+    g = gate.float()
+    silu = g * torch.sigmoid(g)
+    return (silu.to(up.dtype).float() * up.float()).to(up.dtype)
+
+
+def swiglu_bwd(dout: Tensor, gate: Tensor, up: Tensor) -> Tuple[Tensor, Tensor]:
+    """dgate = dout*up*s*(1 + g*(1 - s)), dup = dout*g*s, s = sigmoid(g), fp32, rounded once.
+
+    Restates _swiglu_backward_kernel (kernels/triton_kernels.py:1089-1101).
+    """
+    dout, gate, up = _cpu(dout), _cpu(gate), _cpu(up)
+    d, g, u = dout.float(), gate.float(), up.float()
+    s = torch.sigmoid(g)
+    dg = d * u * (s * (1.0 + g * (1.0 - s)))
+    du = d * (g * s)
+    return dg.to(gate.dtype), du.to(up.dtype)

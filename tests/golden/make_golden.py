@@ -13,6 +13,11 @@ oracle/ (no torch ops, no shared code):
   softmax - onehot; label smoothing as the cross-entropy against the smoothed
   target distribution (1-a)*onehot + a/V.
 * Linear cross-entropy: float64 matmul followed by the above.
+* SwiGLU: silu(g) = g / (1 + exp(-g)) and its derivative
+  1/(1+e^-g) + g e^-g / (1+e^-g)^2 (the quotient rule, not the reference's
+  factored form).
+* Residual add + RMSNorm: h = x + r in float64, then the RMSNorm forward above
+  on the unrounded h (h * rstd stored separately for the round-twice form).
 
 Inputs are rounded to bfloat16 values (stored as float32) so every kernel
 dtype sees them exactly. Run: python tests/golden/make_golden.py
@@ -61,6 +66,18 @@ def rmsnorm_case(seed, rows, cols, eps, zero_row=False):
     return dict(x=x, w=w, dy=dy, eps=np.float64(eps), y=y, rstd=rstd, dx=dx, dw=dw)
 
 
+def add_rmsnorm_case(seed, rows, cols, eps):
+    r = rng(seed)
+    x = bf16_round(r.standard_normal((rows, cols)).astype(np.float32))
+    res = bf16_round(r.standard_normal((rows, cols)).astype(np.float32))
+    w = bf16_round((1.0 + 0.02 * r.standard_normal(cols)).astype(np.float32))
+    H = x.astype(np.float64) + res.astype(np.float64)
+    rstd = 1.0 / np.sqrt((H * H).mean(axis=1) + eps)
+    hn = H * rstd[:, None]
+    return dict(x=x, r=res, w=w, eps=np.float64(eps), h=H, rstd=rstd, hn=hn,
+                y=hn * w.astype(np.float64)[None, :])
+
+
 # ---------------------------------------------------------------------------
 def rope_case(seed, B, S, H, D, theta, positions, interleaved):
     r = rng(seed)
@@ -89,6 +106,20 @@ def rope_case(seed, B, S, H, D, theta, positions, interleaved):
 
     return dict(x=x, g=g, positions=positions.astype(np.int64), theta=np.float64(theta),
                 interleaved=np.int64(interleaved), fwd=unz(fx), bwd=unz(bg))
+
+
+# ---------------------------------------------------------------------------
+def swiglu_case(seed, n, std):
+    r = rng(seed)
+    g = bf16_round((std * r.standard_normal(n)).astype(np.float32))
+    g[:6] = np.array([0.0, -1.0, 1.0, -30.0, 30.0, -100.0], dtype=np.float32)
+    u = bf16_round(r.standard_normal(n).astype(np.float32))
+    d = bf16_round(r.standard_normal(n).astype(np.float32))
+    G, U, D = g.astype(np.float64), u.astype(np.float64), d.astype(np.float64)
+    e = np.exp(-G)
+    silu = G / (1.0 + e)
+    dsilu = 1.0 / (1.0 + e) + G * e / (1.0 + e) ** 2
+    return dict(gate=g, up=u, dout=d, silu=silu, dgate=D * U * dsilu, dup=D * silu)
 
 
 # ---------------------------------------------------------------------------
@@ -153,6 +184,8 @@ def main():
     cases["rmsnorm_64"] = rmsnorm_case(10, 4, 64, 1e-6, zero_row=True)
     cases["rmsnorm_4096"] = rmsnorm_case(11, 3, 4096, 1e-6)
     cases["rmsnorm_100"] = rmsnorm_case(12, 5, 100, 1e-5)  # not a multiple of 8
+    cases["add_rmsnorm_4096"] = add_rmsnorm_case(13, 3, 4096, 1e-6)
+    cases["add_rmsnorm_72"] = add_rmsnorm_case(14, 4, 72, 1e-5)
     pos_seq = np.tile(np.arange(7), (2, 1))
     pos_packed = np.array([[0, 1, 2, 0, 1, 0, 1, 2, 3, 4, 5, 6, 0]])
     cases["rope_neox_seq"] = rope_case(20, 2, 7, 3, 16, 10000.0, pos_seq, False)
@@ -165,6 +198,7 @@ def main():
     cases["ce_smooth"] = ce_case(32, 4, 128, ignore=[1], smoothing=0.1)
     cases["ce_softcap_scale"] = ce_case(33, 4, 96, ignore=[], scale=0.5, softcap=3.0, std=4.0)
     cases["linear_ce"] = linear_ce_case(40, 6, 32, 50, ignore=[3])
+    cases["swiglu"] = swiglu_case(50, 4096, 3.0)
     for name, arrays in cases.items():
         np.savez(OUT / f"{name}.npz", **arrays)
     print(f"wrote {len(cases)} golden cases to {OUT}")

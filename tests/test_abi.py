@@ -122,3 +122,27 @@ def test_scale_and_rescale_validation(lib):
     assert b"aliases" in lib.ts_last_error()
     assert lib.ts_rescale_inplace(FAKE, 16, 9, FAKE, FAKE, NULL, st) == DTYPE
     assert lib.ts_scale_inplace(NULL, 0, 1, FAKE, st) == TS_OK
+
+
+def test_add_rmsnorm_fwd_validation(lib):
+    st = NULL
+    args = lambda **kw: [kw.get("x", FAKE), kw.get("ldx", 64), kw.get("r", FAKE), kw.get("ldr", 64),
+                         kw.get("dt", 1), FAKE, 1, FAKE, 64, kw.get("h", FAKE), kw.get("ldh", 64),
+                         FAKE, kw.get("rows", 4), 64, 1e-6, kw.get("mode", 1), st]
+    assert lib.ts_add_rmsnorm_fwd(*args(r=NULL)) == INVALID
+    assert lib.ts_add_rmsnorm_fwd(*args(ldr=32)) == SHAPE
+    assert lib.ts_add_rmsnorm_fwd(*args(ldh=32)) == SHAPE
+    assert lib.ts_add_rmsnorm_fwd(*args(dt=5)) == DTYPE
+    assert lib.ts_add_rmsnorm_fwd(*args(mode=3)) == INVALID
+    # h_out may be NULL (its stride is then ignored); an empty batch is a no-op
+    assert lib.ts_add_rmsnorm_fwd(*args(h=NULL, ldh=0, rows=0)) == TS_OK
+
+
+def test_swiglu_validation(lib):
+    st = NULL
+    assert lib.ts_swiglu_fwd(FAKE, FAKE, FAKE, -1, 1, st) == SHAPE
+    assert lib.ts_swiglu_fwd(FAKE, FAKE, FAKE, 16, 7, st) == DTYPE
+    assert lib.ts_swiglu_fwd(FAKE, NULL, FAKE, 16, 1, st) == INVALID
+    assert lib.ts_swiglu_bwd(FAKE, FAKE, FAKE, FAKE, NULL, 16, 1, st) == INVALID
+    assert lib.ts_swiglu_fwd(NULL, NULL, NULL, 0, 1, st) == TS_OK
+    assert lib.ts_swiglu_bwd(NULL, NULL, NULL, NULL, NULL, 0, 1, st) == TS_OK

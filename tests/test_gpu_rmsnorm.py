@@ -154,3 +154,93 @@ def test_empty_batch(gpu):
     y, dx, dw = run_fwd_bwd(Fast_RMS_LayerNorm.apply, x, w, torch.empty_like(x), 1e-6)
     assert y.shape == (0, 4096) and dx.shape == (0, 4096)
     assert torch.count_nonzero(dw) == 0
+
+
+# ---------------------------------------------------------------------------
+# Fused residual add + RMSNorm
+# ---------------------------------------------------------------------------
+from trainscale_amd.kernels import (FusedAddRMSLayerNormFunction, FusedRMSNorm,  # noqa: E402
+                                    fused_add_rms_layernorm)
+
+
+@pytest.mark.parametrize("case", ["add_rmsnorm_4096", "add_rmsnorm_72"])
+def test_add_golden(gpu, case):
+    g = golden(case)
+    x = torch.from_numpy(g["x"]).to(BF).to(gpu)
+    r = torch.from_numpy(g["r"]).to(BF).to(gpu)
+    w = torch.from_numpy(g["w"]).to(BF).to(gpu)
+    y, h = fused_add_rms_layernorm(x, r, w, float(g["eps"]), return_residual=True)
+    assert torch.equal(h.cpu(), round_to(g["h"], BF))
+    expect = (round_to(g["hn"], BF).double() * w.cpu().double()).numpy()
+    assert_ulp(y, round_to(expect, BF), 1, what="y")
+    x2d, ld = ops.as_rows(x)
+    _, _, rstd = ops.add_rmsnorm_forward(x2d, ld, r, r.shape[1], w, float(g["eps"]))
+    np.testing.assert_allclose(rstd.double().cpu().numpy(), g["rstd"], rtol=1e-6)
+
+
+def check_add(x, r, w, dy, eps, store=True):
+    xg = x.detach().clone().requires_grad_()
+    rg = r.detach().clone().requires_grad_()
+    wg = w.detach().clone().requires_grad_()
+    out = FusedAddRMSLayerNormFunction.apply(xg, rg, wg, eps, store)
+    y, h = out
+    y.backward(dy)
+    y_ref, h_ref, rstd_ref = oracle.add_rms_norm_fwd(x, r, w, eps)
+    assert_ulp(y, y_ref, 1 if x.dtype != torch.float32 else 8, what="y")
+    if store:
+        assert torch.equal(h.cpu(), h_ref)
+    else:
+        assert h is None
+    dx_ref, _ = oracle.rms_norm_bwd(dy, h_ref, w, rstd_ref)
+    tiny = 1e-6 if x.dtype == torch.float32 else 1e-4
+    assert_ulp(xg.grad, dx_ref, 1 if x.dtype != torch.float32 else 64, tiny=tiny, what="dx")
+    assert torch.equal(xg.grad, rg.grad)
+    assert wg.grad is None  # as the reference: no weight gradient
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (33, 8192), (17, 72), (5, 100), (8, 64)])
+def test_add_shapes(gpu, rows, cols):
+    torch.manual_seed(rows * 7 + cols)
+    x = torch.randn(rows, cols, device=gpu).to(BF)
+    r = torch.randn(rows, cols, device=gpu).to(BF)
+    w = (1 + 0.02 * torch.randn(cols, device=gpu)).to(BF)
+    dy = torch.randn(rows, cols, device=gpu).to(BF)
+    check_add(x, r, w, dy, 1e-6)
+
+
+@pytest.mark.parametrize("dtype,wdtype", [(BF, torch.float32), (torch.float16, torch.float16),
+                                          (torch.float32, torch.float32)])
+def test_add_dtypes(gpu, dtype, wdtype):
+    torch.manual_seed(11)
+    x = torch.randn(40, 512, device=gpu).to(dtype)
+    r = torch.randn(40, 512, device=gpu).to(dtype)
+    w = (1 + 0.1 * torch.randn(512, device=gpu)).to(wdtype)
+    dy = torch.randn(40, 512, device=gpu).to(dtype)
+    check_add(x, r, w, dy, 1e-5)
+
+
+def test_add_no_store_and_strided(gpu):
+    torch.manual_seed(12)
+    base = torch.randn(32, 2 * 1024, device=gpu).to(BF)
+    x = base[:, :1024]  # row stride 2048
+    r = torch.randn(32, 1024, device=gpu).to(BF)
+    w = (1 + 0.02 * torch.randn(1024, device=gpu)).to(BF)
+    dy = torch.randn(32, 1024, device=gpu).to(BF)
+    check_add(x, r, w, dy, 1e-6, store=False)
+    mod = FusedRMSNorm(1024, eps=1e-6, device=gpu, dtype=BF)
+    y1 = mod(x, r)
+    y2, h2 = mod(x, r, return_residual=True)
+    assert torch.equal(y1, y2) and torch.equal(h2, (x.float() + r.float()).to(BF))
+
+
+def test_add_c1_full(gpu):
+    wl = workloads.rmsnorm_workload(gpu)
+    x, w, dy = wl.tensors["x"], wl.tensors["w"], wl.tensors["dy"]
+    r = torch.flip(x, dims=[0]).contiguous()
+    y, h = fused_add_rms_layernorm(x, r, w, 1e-6, return_residual=True)
+    sample = torch.cat([torch.arange(0, 512), torch.arange(x.shape[0] * x.shape[1] - 512,
+                                                            x.shape[0] * x.shape[1])])
+    x2, r2 = x.reshape(-1, x.shape[-1]), r.reshape(-1, r.shape[-1])
+    y_ref, h_ref, _ = oracle.add_rms_norm_fwd(x2[sample], r2[sample], w, 1e-6)
+    assert_ulp(y.reshape(-1, y.shape[-1])[sample], y_ref, 1, what="y")
+    assert torch.equal(h.reshape(-1, h.shape[-1])[sample].cpu(), h_ref)

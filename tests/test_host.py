@@ -95,3 +95,28 @@ def test_patch_boundary_keeps_cpu_modules_on_their_own_forward():
     assert patcher.patched_layers == [("1", "LlamaRMSNorm")]
     assert torch.equal(model(x), before)  # CPU tensors: the module's original forward
     assert "LlamaRMSNorm" in registry.LAYER_PATCHES
+
+
+class LlamaMLP(nn.Module):
+    def __init__(self, h, i):
+        super().__init__()
+        self.gate_proj = nn.Linear(h, i, bias=False)
+        self.up_proj = nn.Linear(h, i, bias=False)
+        self.down_proj = nn.Linear(i, h, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(torch.nn.functional.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+def test_patch_boundary_mlp_and_flags():
+    model = nn.Sequential(LlamaMLP(8, 16), LlamaRMSNorm(8))
+    x = torch.randn(3, 8)
+    before = model(x)
+    patcher = registry.KernelPatcher(patch_layernorm=False)
+    patcher.patch(model)
+    assert patcher.patched_layers == [("0", "LlamaMLP")]
+    assert torch.equal(model(x), before)  # CPU tensors keep the original forward
+    p2 = registry.KernelPatcher()
+    p2.patch(model)  # idempotent for the MLP, patches the norm now
+    assert p2.patched_layers == [("1", "LlamaRMSNorm")]
+    assert "LlamaMLP" in registry.LAYER_PATCHES and "Qwen2MLP" in registry.LAYER_PATCHES

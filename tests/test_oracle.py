@@ -99,6 +99,39 @@ def test_rmsnorm_invariants():
     assert torch.count_nonzero(yz.float()) == 0
 
 
+@pytest.mark.parametrize("case", ["add_rmsnorm_4096", "add_rmsnorm_72"])
+def test_add_rmsnorm_matches_golden(case):
+    g = golden(case)
+    x, r, w = t32(g["x"]).to(BF), t32(g["r"]).to(BF), t32(g["w"]).to(BF)
+    eps = float(g["eps"])
+    y1, h, rstd = oracle.add_rms_norm_fwd(x, r, w, eps, round_twice=False)
+    assert_ulp(y1, round_to(g["y"], BF), 1, what=case + " y once")
+    assert torch.equal(h, round_to(g["h"], BF)), case + " h"
+    np.testing.assert_allclose(rstd.double().numpy(), g["rstd"], rtol=2e-6)
+    y2, _, _ = oracle.add_rms_norm_fwd(x, r, w, eps, round_twice=True)
+    expect = (round_to(g["hn"], BF).double() * w.double()).numpy()
+    assert_ulp(y2, round_to(expect, BF), 1, what=case + " y twice")
+    # a plausible mistake, rstd taken from the rounded h, fails the rstd check
+    hb = h.float()
+    bad = 1.0 / torch.sqrt((hb * hb).sum(-1) / hb.shape[-1] + eps)
+    assert not np.allclose(bad.double().numpy(), g["rstd"], rtol=2e-6, atol=0)
+
+
+def test_add_rmsnorm_invariants():
+    torch.manual_seed(5)
+    x = torch.randn(6, 256).to(BF)
+    r = torch.randn(6, 256).to(BF)
+    w = (1 + 0.1 * torch.randn(256)).to(BF)
+    # zero residual: plain RMSNorm with the same rounding, h == x
+    y0, h0, rs0 = oracle.add_rms_norm_fwd(x, torch.zeros_like(x), w, 1e-6)
+    yr, rsr = oracle.rms_norm_fwd(x, w, 1e-6, round_twice=True)
+    assert torch.equal(y0, yr) and torch.equal(h0, x) and torch.equal(rs0, rsr)
+    # x + r == r + x in fp32
+    ya, ha, ra = oracle.add_rms_norm_fwd(x, r, w, 1e-6)
+    yb, hb, rb = oracle.add_rms_norm_fwd(r, x, w, 1e-6)
+    assert torch.equal(ya, yb) and torch.equal(ha, hb) and torch.equal(ra, rb)
+
+
 def test_rmsnorm_round_twice_is_double_rounding():
     torch.manual_seed(3)
     x = torch.randn(64, 256).to(BF)
@@ -313,3 +346,46 @@ def test_linear_ce_bf16_logits_mode():
     s = oracle.linear_ce(he, we, labels, reduction="sum", bf16_logits=True)
     n_valid = int((labels != -100).sum())
     assert abs(float(s[0]) - n_valid * float(a[0])) <= 1e-4 * abs(float(s[0]))
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU
+# ---------------------------------------------------------------------------
+def test_swiglu_matches_golden():
+    g = golden("swiglu")
+    gate, up, dout = t32(g["gate"]).to(BF), t32(g["up"]).to(BF), t32(g["dout"]).to(BF)
+    # silu alone (up = 1): one rounding of the fp64 value, within 1 ulp
+    silu = oracle.swiglu_fwd(gate, torch.ones_like(up))
+    assert_ulp(silu, round_to(g["silu"], BF), 1, what="silu")
+    # out = round(round(silu) * up): a silu rounding flip moves out by at most 2 ulps
+    out = oracle.swiglu_fwd(gate, up)
+    expect = round_to(g["silu"], BF).double() * up.double()
+    assert_ulp(out, expect.to(BF), 2, what="out")
+    dg, du = oracle.swiglu_bwd(dout, gate, up)
+    # dsilu crosses zero near g = -1.28, where fp32 loses relative accuracy
+    assert_ulp(dg, round_to(g["dgate"], BF), 1, tiny=1e-5, what="dgate")
+    assert_ulp(du, round_to(g["dup"], BF), 1, what="dup")
+    # a plausible mistake, sigmoid' in place of silu', fails the same check
+    s = torch.sigmoid(gate.float())
+    bad = (dout.float() * up.float() * s * (1 - s)).to(BF)
+    with pytest.raises(AssertionError):
+        assert_ulp(bad, round_to(g["dgate"], BF), 1, tiny=1e-5, what="mutated")
+
+
+def test_swiglu_bwd_matches_autograd_float64():
+    torch.manual_seed(9)
+    gate = (3 * torch.randn(300, dtype=torch.float64)).requires_grad_()
+    up = torch.randn(300, dtype=torch.float64).requires_grad_()
+    dout = torch.randn(300, dtype=torch.float64)
+    (F.silu(gate) * up).backward(dout)
+    dg, du = oracle.swiglu_bwd(dout.float(), gate.detach().float(), up.detach().float())
+    torch.testing.assert_close(dg.double(), gate.grad, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(du.double(), up.grad, rtol=1e-5, atol=1e-6)
+
+
+def test_swiglu_invariants():
+    g = torch.tensor([0.0, 40.0, -40.0, 2.0], dtype=BF)
+    u = torch.tensor([5.0, 1.0, 1.0, 0.0], dtype=BF)
+    out = oracle.swiglu_fwd(g, u)
+    assert out[0].item() == 0.0 and out[3].item() == 0.0   # silu(0) = 0; up = 0
+    assert out[1].item() == 40.0 and abs(out[2].item()) < 1e-15  # saturation

@@ -54,6 +54,8 @@ SIGNATURES = {
     "ts_last_error": ([], ctypes.c_char_p),
     "ts_version": ([], ctypes.c_char_p),
     "ts_rmsnorm_fwd": ([P, I64, I32, P, I32, P, I64, P, I64, I64, F32, I32, P], I32),
+    "ts_add_rmsnorm_fwd": ([P, I64, P, I64, I32, P, I32, P, I64, P, I64, P, I64, I64, F32, I32, P],
+                           I32),
     "ts_rmsnorm_bwd_workspace_size": ([I64, I64], SZ),
     "ts_rmsnorm_bwd": ([P, I64, P, I64, I32, P, I32, P, P, I64, P, P, SZ, I64, I64, P], I32),
     "ts_rope_apply": (
@@ -74,6 +76,8 @@ SIGNATURES = {
     "ts_flce_fwd_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, P, P, P, P, P, I64, P, SZ, P],
                         I32),
     "ts_scale_inplace": ([P, I64, I32, P, P], I32),
+    "ts_swiglu_fwd": ([P, P, P, I64, I32, P], I32),
+    "ts_swiglu_bwd": ([P, P, P, P, P, I64, I32, P], I32),
     "ts_rescale_inplace": ([P, I64, I32, P, P, P, P], I32),
 }
 

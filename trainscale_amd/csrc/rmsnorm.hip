@@ -58,17 +58,41 @@ __device__ inline float row_reduce(float v, float* red) {
   }
 }
 
+// Residual input of the fused add + RMSNorm (kAdd kernels): the normalised
+// row is h = x + r in fp32; h rounded to the data type is stored to `h` when
+// it is not null (the reference's residual_out).
+template <typename T>
+struct AddArgs {
+  const T* r;
+  int64_t ldr;
+  T* h;
+  int64_t ldh;
+};
+
+// x (+ r) of one 16-byte vector, in fp32.
+template <typename T, bool kAdd>
+__device__ inline void row_values(const u32x4& xq, const u32x4& rq, float* f) {
+  Elt<T>::unpack(xq, f);
+  if constexpr (kAdd) {
+    float g[Elt<T>::kVec];
+    Elt<T>::unpack(rq, g);
+#pragma unroll
+    for (int i = 0; i < Elt<T>::kVec; ++i) f[i] += g[i];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Forward, register path.
 // ---------------------------------------------------------------------------
-template <typename T, typename W, int TPR, int KV>
+template <typename T, typename W, int TPR, int KV, bool kAdd>
 __global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
     const T* __restrict__ x, int64_t ldx, const W* __restrict__ w, T* __restrict__ y,
     int64_t ldy, float* __restrict__ rstd_out, int64_t rows, int nvec, float fcols, float eps,
-    int twice) {
+    int twice, AddArgs<T> add) {
   constexpr int V = Elt<T>::kVec;
   constexpr int kBlock = TPR > 256 ? TPR : 256;
   constexpr int kRpb = kBlock / TPR;
+  constexpr int KR = kAdd ? KV : 1;
   __shared__ float red[kBlock / kWave];
   const int sub = threadIdx.x / TPR;
   const int t = threadIdx.x % TPR;
@@ -76,19 +100,34 @@ __global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
   const bool valid = row < rows;
 
   const T* xr = x + row * ldx;
-  u32x4 xv[KV];
+  u32x4 xv[KV], rv[KR];
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
     const int v = t + k * TPR;
     xv[k] = valid && v < nvec ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
   }
+  if constexpr (kAdd) {
+    const T* rr = add.r + row * add.ldr;
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      const int v = t + k * TPR;
+      rv[k] = valid && v < nvec ? ld16_stream(rr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+    }
+  } else {
+    rv[0] = u32x4{0, 0, 0, 0};
+  }
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
     float f[V];
-    Elt<T>::unpack(xv[k], f);
+    row_values<T, kAdd>(xv[k], rv[kAdd ? k : 0], f);
 #pragma unroll
     for (int i = 0; i < V; ++i) ss = __builtin_fmaf(f[i], f[i], ss);
+    if constexpr (kAdd) {
+      const int v = t + k * TPR;
+      if (add.h != nullptr && valid && v < nvec)
+        st16_stream(add.h + row * add.ldh + (int64_t)v * V, Elt<T>::pack(f));
+    }
   }
   ss = row_reduce<TPR, kBlock>(ss, red);
   // mean(x^2) = sum / n (a division, as the reference divides by n_cols), then
@@ -103,7 +142,7 @@ __global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
     const int v = t + k * TPR;
     if (v < nvec) {
       float f[V];
-      Elt<T>::unpack(xv[k], f);
+      row_values<T, kAdd>(xv[k], rv[kAdd ? k : 0], f);
       if (w != nullptr) {
         float wf[V];
         load_w<W, V>(w, (int64_t)v * V, wf);
@@ -293,18 +332,24 @@ __global__ __launch_bounds__(256) void rms_dw_reduce1(const float* __restrict__ 
 // ---------------------------------------------------------------------------
 // Generic path: one 256-thread workgroup per row, element-wise.
 // ---------------------------------------------------------------------------
-template <typename T, typename W>
+template <typename T, typename W, bool kAdd>
 __global__ __launch_bounds__(256) void rms_fwd_generic(const T* __restrict__ x, int64_t ldx,
                                                        const W* __restrict__ w,
                                                        T* __restrict__ y, int64_t ldy,
                                                        float* __restrict__ rstd_out,
-                                                       int64_t cols, float eps, int twice) {
+                                                       int64_t cols, float eps, int twice,
+                                                       AddArgs<T> add) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * ldx;
+  const T* rr = kAdd ? add.r + row * add.ldr : nullptr;
   float ss = 0.f;
   for (int64_t c = threadIdx.x; c < cols; c += 256) {
-    const float f = Elt<T>::load1(xr + c);
+    float f = Elt<T>::load1(xr + c);
+    if constexpr (kAdd) {
+      f += Elt<T>::load1(rr + c);
+      if (add.h != nullptr) Elt<T>::store1(add.h + row * add.ldh + c, f);
+    }
     ss = __builtin_fmaf(f, f, ss);
   }
   ss = block_sum<4>(ss, red);
@@ -312,7 +357,8 @@ __global__ __launch_bounds__(256) void rms_fwd_generic(const T* __restrict__ x, 
   if (threadIdx.x == 0) rstd_out[row] = rstd;
   T* yr = y + row * ldy;
   for (int64_t c = threadIdx.x; c < cols; c += 256) {
-    const float f = Elt<T>::load1(xr + c);
+    float f = Elt<T>::load1(xr + c);
+    if constexpr (kAdd) f += Elt<T>::load1(rr + c);
     float o;
     if (w != nullptr) {
       const float wf = Elt<W>::load1(w + c);
@@ -378,24 +424,27 @@ bool vec_ok(const void* a, int64_t lda, int64_t cols, const void* w) {
          (w == nullptr || ts_host::aligned16(w));
 }
 
-template <typename T, typename W>
+template <typename T, typename W, bool kAdd = false>
 ts_status fwd_typed(const void* x, int64_t ldx, const void* w, void* y, int64_t ldy,
                     float* rstd, int64_t rows, int64_t cols, float eps, int twice,
-                    hipStream_t st) {
+                    hipStream_t st, AddArgs<T> add = AddArgs<T>{nullptr, 0, nullptr, 0}) {
   constexpr int V = sizeof(T) == 4 ? 4 : 8;
   const T* xp = static_cast<const T*>(x);
   const W* wp = static_cast<const W*>(w);
   T* yp = static_cast<T*>(y);
   const int64_t nvec = cols / V;
   const ts_plan::RmsRowPlan plan = ts_plan::rms_fwd_plan(nvec);
-  if (vec_ok<T, W>(x, ldx, cols, w) && vec_ok<T, W>(y, ldy, cols, nullptr) && plan.reg) {
+  const bool add_ok = !kAdd || (vec_ok<T, W>(add.r, add.ldr, cols, nullptr) &&
+                                (add.h == nullptr || vec_ok<T, W>(add.h, add.ldh, cols, nullptr)));
+  if (vec_ok<T, W>(x, ldx, cols, w) && vec_ok<T, W>(y, ldy, cols, nullptr) && add_ok &&
+      plan.reg) {
     const dim3 grid((unsigned)((rows + plan.rpb - 1) / plan.rpb));
     const dim3 block(plan.block);
     bool launched = false;
 #define TS_LAUNCH_FWD(TPR, KV)                                                                 \
   if (plan.tpr == TPR && plan.kv == KV) {                                                      \
-    hipLaunchKernelGGL((rms_fwd_reg<T, W, TPR, KV>), grid, block, 0, st, xp, ldx, wp, yp, ldy, \
-                       rstd, rows, (int)nvec, (float)cols, eps, twice);                        \
+    hipLaunchKernelGGL((rms_fwd_reg<T, W, TPR, KV, kAdd>), grid, block, 0, st, xp, ldx, wp,    \
+                       yp, ldy, rstd, rows, (int)nvec, (float)cols, eps, twice, add);          \
     launched = true;                                                                           \
   }
     TS_LAUNCH_FWD(64, 1)
@@ -410,8 +459,8 @@ ts_status fwd_typed(const void* x, int64_t ldx, const void* w, void* y, int64_t 
                            plan.tpr, plan.kv);
     return ts_host::check_launch("rms_fwd_reg");
   }
-  hipLaunchKernelGGL((rms_fwd_generic<T, W>), dim3((unsigned)rows), dim3(256), 0, st, xp, ldx,
-                     wp, yp, ldy, rstd, cols, eps, twice);
+  hipLaunchKernelGGL((rms_fwd_generic<T, W, kAdd>), dim3((unsigned)rows), dim3(256), 0, st, xp,
+                     ldx, wp, yp, ldy, rstd, cols, eps, twice, add);
   return ts_host::check_launch("rms_fwd_generic");
 }
 
@@ -536,6 +585,48 @@ extern "C" ts_status ts_rmsnorm_fwd(const void* x, int64_t ldx, ts_dtype x_dtype
       return fwd_typed<float, float>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st);
   }
   return fail(TS_ERR_UNSUPPORTED_DTYPE, "rmsnorm_fwd: unsupported dtype");
+}
+
+extern "C" ts_status ts_add_rmsnorm_fwd(const void* x, int64_t ldx, const void* residual,
+                                        int64_t ldr, ts_dtype x_dtype, const void* w,
+                                        ts_dtype w_dtype, void* y, int64_t ldy, void* h_out,
+                                        int64_t ldh, float* rstd, int64_t rows, int64_t cols,
+                                        float eps, int32_t round_mode, ts_stream_t stream) {
+  using ts_host::fail;
+  ts_status s = check_common(x, ldx, x_dtype, w, w_dtype, rows, cols);
+  if (s != TS_OK) return s;
+  if (rows > 0 && (residual == nullptr || y == nullptr || rstd == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "add_rmsnorm_fwd: residual, y or rstd is NULL");
+  if (ldr < cols || ldy < cols || (h_out != nullptr && ldh < cols))
+    return fail(TS_ERR_SHAPE, "add_rmsnorm_fwd: row stride < cols");
+  if (!(eps >= 0.f)) return fail(TS_ERR_INVALID_ARGUMENT, "add_rmsnorm_fwd: eps must be >= 0");
+  if (round_mode != TS_RMS_ROUND_ONCE && round_mode != TS_RMS_ROUND_TWICE)
+    return fail(TS_ERR_INVALID_ARGUMENT, "add_rmsnorm_fwd: bad round_mode %d", (int)round_mode);
+  if (rows == 0) return TS_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int twice = round_mode == TS_RMS_ROUND_TWICE && w != nullptr && w_dtype == x_dtype &&
+                    x_dtype != TS_F32;
+#define TS_ADD_FWD(T)                                                                          \
+  {                                                                                            \
+    const AddArgs<T> add{static_cast<const T*>(residual), ldr, static_cast<T*>(h_out), ldh};   \
+    return w_dtype == TS_F32 && w != nullptr                                                   \
+               ? fwd_typed<T, float, true>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st, \
+                                           add)                                                \
+               : fwd_typed<T, T, true>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st,    \
+                                       add);                                                   \
+  }
+  switch (x_dtype) {
+    case TS_BF16: TS_ADD_FWD(__bf16)
+    case TS_F16: TS_ADD_FWD(_Float16)
+    case TS_F32: {
+      const AddArgs<float> add{static_cast<const float*>(residual), ldr,
+                               static_cast<float*>(h_out), ldh};
+      return fwd_typed<float, float, true>(x, ldx, w, y, ldy, rstd, rows, cols, eps, twice, st,
+                                           add);
+    }
+  }
+#undef TS_ADD_FWD
+  return fail(TS_ERR_UNSUPPORTED_DTYPE, "add_rmsnorm_fwd: unsupported dtype");
 }
 
 extern "C" size_t ts_rmsnorm_bwd_workspace_size(int64_t rows, int64_t cols) {

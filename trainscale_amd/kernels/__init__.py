@@ -8,11 +8,21 @@ from .fused_kernels import (
     Fast_CrossEntropyLoss,
     Fast_RMS_LayerNorm,
     Fast_RoPE,
+    Fast_SwiGLU,
     HipRMSNorm,
     TritonRMSNorm,
     fast_cross_entropy_loss,
+    swiglu_forward,
 )
-from .layernorm_kernels import RMSLayerNormFunction, RMSNorm, fast_rms_layernorm, rms_layernorm
+from .layernorm_kernels import (
+    FusedAddRMSLayerNormFunction,
+    FusedRMSNorm,
+    RMSLayerNormFunction,
+    RMSNorm,
+    fast_rms_layernorm,
+    fused_add_rms_layernorm,
+    rms_layernorm,
+)
 from .rope_kernels import (
     Fast_RoPE_Embedding,
     FusedRoPEQKFunction,
@@ -32,6 +42,8 @@ from .rope_kernels import (
 __all__ = [
     "Fast_CrossEntropyLoss",
     "fast_cross_entropy_loss",
+    "Fast_SwiGLU",
+    "swiglu_forward",
     "Fast_RMS_LayerNorm",
     "HipRMSNorm",
     "TritonRMSNorm",
@@ -39,6 +51,9 @@ __all__ = [
     "RMSNorm",
     "rms_layernorm",
     "fast_rms_layernorm",
+    "FusedAddRMSLayerNormFunction",
+    "fused_add_rms_layernorm",
+    "FusedRMSNorm",
     "Fast_RoPE",
     "Fast_RoPE_Embedding",
     "FusedRoPEQKFunction",

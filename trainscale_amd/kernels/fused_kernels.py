@@ -13,6 +13,9 @@ reference (paths relative to ``data_pipeline/trainer/``):
   (kernels/triton_kernels.py:309-467): per-row losses with optional logit
   scaling and softcapping; the backward writes the gradient into the saved
   logits buffer and returns it, as the reference does.
+* ``Fast_SwiGLU`` / ``swiglu_forward`` (kernels/triton_kernels.py:1105-1148):
+  out = silu(gate).to(up.dtype) * up; backward returns (dgate, dup) in fp32
+  arithmetic rounded once.
 
 Every op runs the gfx950 kernels of ``libtrainscale_amd.so``. Unlike the
 reference there is no eager fallback: CPU tensors raise.
@@ -37,6 +40,8 @@ __all__ = [
     "precompute_freqs_cis",
     "Fast_CrossEntropyLoss",
     "fast_cross_entropy_loss",
+    "Fast_SwiGLU",
+    "swiglu_forward",
 ]
 
 
@@ -197,3 +202,23 @@ def fast_cross_entropy_loss(logits: Tensor, labels: Tensor, logit_softcapping: f
     if n_items is None:
         n_items = (labels != -100).sum()
     return loss.sum() / n_items
+
+
+class Fast_SwiGLU(torch.autograd.Function):
+    """SwiGLU (reference: kernels/triton_kernels.py:1105-1143): forward(gate, up) -> out."""
+
+    @staticmethod
+    def forward(ctx, gate: Tensor, up: Tensor) -> Tensor:
+        out = ops.swiglu_forward(gate, up)
+        ctx.save_for_backward(gate.contiguous(), up.contiguous())
+        return out
+
+    @staticmethod
+    def backward(ctx, dout: Tensor) -> Tuple[Tensor, Tensor]:
+        gate, up = ctx.saved_tensors
+        return ops.swiglu_backward(dout, gate, up)
+
+
+def swiglu_forward(gate: Tensor, up: Tensor) -> Tensor:
+    """silu(gate) * up (reference: kernels/triton_kernels.py:1146-1148)."""
+    return Fast_SwiGLU.apply(gate, up)

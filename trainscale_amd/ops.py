@@ -66,6 +66,36 @@ def rmsnorm_forward(x2d: Tensor, ldx: int, weight: Optional[Tensor], eps: float,
     return y, rstd
 
 
+def add_rmsnorm_forward(x2d: Tensor, ldx: int, r2d: Tensor, ldr: int, weight: Optional[Tensor],
+                        eps: float, round_mode: int = ROUND_TWICE, store_h: bool = True
+                        ) -> Tuple[Tensor, Optional[Tensor], Tensor]:
+    """h = x + r, y = h * rstd * w over the rows; returns (y, h rounded to the data dtype
+    or None, rstd fp32), y and h contiguous [rows, cols]."""
+    dev = _lib.require_gpu("add_rmsnorm_forward", x2d, r2d, weight)
+    rows, cols = x2d.shape
+    if r2d.shape != x2d.shape:
+        raise ValueError(f"add_rmsnorm: residual {tuple(r2d.shape)} != x {tuple(x2d.shape)}")
+    if r2d.dtype != x2d.dtype:
+        raise TypeError(f"add_rmsnorm: residual dtype {r2d.dtype} != x dtype {x2d.dtype}")
+    y = torch.empty((rows, cols), dtype=x2d.dtype, device=dev)
+    h = torch.empty((rows, cols), dtype=x2d.dtype, device=dev) if store_h else None
+    rstd = torch.empty((rows,), dtype=torch.float32, device=dev)
+    if rows == 0:
+        return y, h, rstd
+    if weight is not None:
+        if weight.dim() != 1 or weight.shape[0] != cols:
+            raise ValueError(f"add_rmsnorm: weight shape {tuple(weight.shape)} != ({cols},)")
+        weight = weight.contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_add_rmsnorm_fwd(
+            ptr(x2d), ldx, ptr(r2d), ldr, _lib.dtype_code(x2d, "add_rmsnorm"),
+            ptr(weight), _lib.dtype_code(weight, "add_rmsnorm weight") if weight is not None else 0,
+            ptr(y), cols, ptr(h), cols, ptr(rstd), rows, cols, float(eps), round_mode,
+            _lib.stream_handle(dev)), "ts_add_rmsnorm_fwd")
+    return y, h, rstd
+
+
 def rmsnorm_backward(dy2d: Tensor, lddy: int, x2d: Tensor, ldx: int, weight: Optional[Tensor],
                      rstd: Tensor, need_dw: bool) -> Tuple[Tensor, Optional[Tensor]]:
     """Returns (dx [rows, cols] contiguous, dw in the weight dtype or None)."""
@@ -347,3 +377,41 @@ def rescale_(t: Tensor, now: Tensor, used: Tensor, hint_out: Optional[Tensor] = 
                                      ptr(now), ptr(used), ptr(hint_out),
                                      _lib.stream_handle(dev)), "ts_rescale_inplace")
     return t
+
+
+def _flat(t: Tensor, name: str) -> Tensor:
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: tensor must be contiguous")
+    return t
+
+
+def swiglu_forward(gate: Tensor, up: Tensor) -> Tensor:
+    """out = round(round(silu(gate)) * up) elementwise; a new tensor shaped like gate."""
+    dev = _lib.require_gpu("swiglu_forward", gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError(f"swiglu: gate {tuple(gate.shape)} {gate.dtype} and up "
+                         f"{tuple(up.shape)} {up.dtype} must match")
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(gate)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_swiglu_fwd(ptr(gate), ptr(up), ptr(out), gate.numel(),
+                                _lib.dtype_code(gate, "swiglu"), _lib.stream_handle(dev)),
+              "ts_swiglu_fwd")
+    return out
+
+
+def swiglu_backward(dout: Tensor, gate: Tensor, up: Tensor) -> Tuple[Tensor, Tensor]:
+    """(dgate, dup) of out = silu(gate) * up for the upstream gradient dout."""
+    dev = _lib.require_gpu("swiglu_backward", dout, gate, up)
+    gate, up = _flat(gate, "swiglu"), _flat(up, "swiglu")
+    dout = dout.to(gate.dtype).contiguous()
+    if dout.shape != gate.shape:
+        raise ValueError(f"swiglu: dout {tuple(dout.shape)} != gate {tuple(gate.shape)}")
+    dgate, dup = torch.empty_like(gate), torch.empty_like(up)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_swiglu_bwd(ptr(dout), ptr(gate), ptr(up), ptr(dgate), ptr(dup),
+                                gate.numel(), _lib.dtype_code(gate, "swiglu"),
+                                _lib.stream_handle(dev)), "ts_swiglu_bwd")
+    return dgate, dup

@@ -1,12 +1,14 @@
-"""RMSNorm patch boundary with TrainScale's registry API.
+"""RMSNorm and SwiGLU-MLP patch boundary with TrainScale's registry API.
 
-Mirrors ``register_layer_patch``, ``LAYER_PATCHES``, ``auto_patch_layernorm``
-and the RMSNorm part of ``KernelPatcher`` (data_pipeline/trainer/registry/
-__init__.py:997-1077, :1331-1418): every module whose class name is registered
-gets its ``forward`` replaced by ``fast_rms_layernorm`` on the gfx950 kernels.
-As in the reference, the patched forward keeps calling the module's original
-forward for tensors that are not on a GPU (the module's own code, not a copy
-of the kernel math).
+Mirrors ``register_layer_patch``, ``LAYER_PATCHES``, ``auto_patch_layernorm``,
+``auto_patch_mlp`` and the RMSNorm/MLP part of ``KernelPatcher``
+(data_pipeline/trainer/registry/__init__.py:997-1091, :1194-1200, :1331-1418):
+every module whose class name is registered gets its ``forward`` replaced, an
+RMSNorm by ``fast_rms_layernorm`` and a gate/up/down MLP by
+``down_proj(swiglu_forward(gate_proj(x), up_proj(x)))``, both on the gfx950
+kernels. The patched forward keeps calling the module's original forward for
+tensors that are not on a GPU (the module's own code, not a copy of the kernel
+math).
 """
 from __future__ import annotations
 
@@ -15,10 +17,10 @@ from typing import Callable, Dict, List, Tuple
 import torch
 import torch.nn as nn
 
-from .kernels.fused_kernels import fast_rms_layernorm
+from .kernels.fused_kernels import fast_rms_layernorm, swiglu_forward
 
-__all__ = ["LAYER_PATCHES", "register_layer_patch", "auto_patch_layernorm", "KernelPatcher",
-           "patch_model"]
+__all__ = ["LAYER_PATCHES", "register_layer_patch", "auto_patch_layernorm", "auto_patch_mlp",
+           "KernelPatcher", "patch_model"]
 
 LAYER_PATCHES: Dict[str, Callable[[nn.Module], None]] = {}
 
@@ -53,22 +55,60 @@ for _name in ("LlamaRMSNorm", "Qwen2RMSNorm", "Qwen3RMSNorm", "GemmaRMSNorm", "G
     register_layer_patch(_name, auto_patch_layernorm)
 
 
-class KernelPatcher:
-    """Applies the registered layer patches to a model (registry/__init__.py:1331-1418)."""
+def auto_patch_mlp(module: nn.Module) -> None:
+    """Routes a gate/up/down MLP through the gfx950 SwiGLU kernel (registry/__init__.py:1080-1091)."""
+    if not (hasattr(module, "gate_proj") and hasattr(module, "up_proj")
+            and hasattr(module, "down_proj")):
+        return
+    original_forward = module.forward
 
-    def __init__(self, patch_layernorm: bool = True, verbose: bool = False):
+    def patched_forward(x):
+        if not isinstance(x, torch.Tensor) or not x.is_cuda:
+            return original_forward(x)
+        return module.down_proj(swiglu_forward(module.gate_proj(x), module.up_proj(x)))
+
+    module.forward = patched_forward
+    module._trainscale_amd_patched = True
+
+
+for _name in ("LlamaMLP", "Qwen2MLP", "Qwen3MLP", "MistralMLP", "MixtralBlockSparseTop2MLP",
+              "Phi3MLP", "Phi4MLP"):
+    register_layer_patch(_name, auto_patch_mlp)
+
+
+class KernelPatcher:
+    """Applies the registered layer patches to a model (registry/__init__.py:1331-1418).
+
+    ``patch_attention``, ``patch_rope`` and ``patch_fp8`` are accepted for
+    signature compatibility; this layer registers no attention, rotary-module
+    or FP8 patches, so they select nothing.
+    """
+
+    def __init__(self, patch_layernorm: bool = True, patch_mlp: bool = True,
+                 patch_attention: bool = True, patch_rope: bool = True, patch_fp8: bool = False,
+                 verbose: bool = False):
         self.patch_layernorm = patch_layernorm
+        self.patch_mlp = patch_mlp
+        self.patch_attention = patch_attention
+        self.patch_rope = patch_rope
+        self.patch_fp8 = patch_fp8
         self.verbose = verbose
         self.patched_layers: List[Tuple[str, str]] = []
 
     def patch(self, model: nn.Module) -> nn.Module:
-        if not self.patch_layernorm:
-            return model
         for name, module in model.named_modules():
             cls = module.__class__.__name__
             fn = LAYER_PATCHES.get(cls)
-            if fn is not None and not getattr(module, "_trainscale_amd_patched", False):
-                fn(module)
+            if fn is None or getattr(module, "_trainscale_amd_patched", False):
+                continue
+            if cls.endswith(("RMSNorm", "LayerNorm")):
+                if not self.patch_layernorm:
+                    continue
+            elif cls.endswith("MLP"):
+                if not self.patch_mlp:
+                    continue
+            fn(module)
+            if getattr(module, "_trainscale_amd_patched", False):
                 self.patched_layers.append((name, cls))
         if self.verbose and self.patched_layers:
             print(f"patched {len(self.patched_layers)} layers")

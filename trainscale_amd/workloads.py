@@ -144,6 +144,16 @@ def rmsnorm_bytes(rows: int, cols: int, elt: int = 2, w_elt: int = 2) -> Dict[st
     return dict(fwd=fwd, bwd=bwd)
 
 
+def add_rmsnorm_bytes(rows: int, cols: int, elt: int = 2, w_elt: int = 2) -> int:
+    """Fused residual add + RMSNorm forward: read x, residual, w; write y, h, rstd."""
+    return 4 * rows * cols * elt + cols * w_elt + rows * 4
+
+
+def swiglu_bytes(n: int, elt: int = 2) -> Dict[str, int]:
+    """fwd: read gate, up; write out. bwd: read dout, gate, up; write dgate, dup."""
+    return dict(fwd=3 * n * elt, bwd=5 * n * elt)
+
+
 def rope_bytes(tokens: int, heads: int, D: int, elt: int = 2, pos_bytes: int = 0) -> Dict[str, int]:
     """fwd and bwd each read and write every Q/K element once (+ position_ids)."""
     t = tokens * heads * D * elt
