@@ -193,3 +193,106 @@ def test_out_of_range_positions_give_nan(gpu):
     y = apply_rope(x, cos.to(gpu), sin.to(gpu), position_ids=pos, inplace=False).float()
     assert torch.isnan(y[0, 2]).all()
     assert not torch.isnan(y[0, [0, 1, 3]]).any()
+
+
+# ---------------------------------------------------------------------------
+# transformers' apply_rotary_pos_emb routed to the kernel; packed rows from cu_seqlens
+# ---------------------------------------------------------------------------
+from trainscale_amd.kernels.rope_kernels import (hf_apply_rotary_pos_emb,  # noqa: E402
+                                                 position_ids_from_cu_seqlens)
+
+
+def _hf_tables(B, S, D, theta, device):
+    pos = torch.stack([torch.arange(S), torch.arange(7, 7 + S)])[:B]
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    freqs = pos[:, :, None].float() * inv[None, None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().to(BF).to(device), emb.sin().to(BF).to(device)
+
+
+def _rotate64(x, cos, sin, transpose=False):
+    """q*cos + rotate_half(q)*sin (or the transpose) in float64; x [B, H, S, D]."""
+    x, c, s = x.double().cpu(), cos.double().cpu()[:, None], sin.double().cpu()[:, None]
+    h = x.shape[-1] // 2
+    rot = torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+    if transpose:
+        rot = torch.cat([x[..., h:], -x[..., :h]], dim=-1)
+    return x * c + rot * s
+
+
+def test_hf_apply_rotary_pos_emb(gpu):
+    torch.manual_seed(21)
+    B, S, Hq, Hk, D = 2, 33, 8, 2, 128
+    q = torch.randn(B, S, Hq, D, device=gpu).to(BF).transpose(1, 2)  # HF layout views
+    k = torch.randn(B, S, Hk, D, device=gpu).to(BF).transpose(1, 2)
+    cos, sin = _hf_tables(B, S, D, 500000.0, gpu)
+    qg, kg = q.detach().clone().requires_grad_(), k.detach().clone().requires_grad_()
+    qe, ke = hf_apply_rotary_pos_emb(qg, kg, cos, sin)
+    assert qe.shape == q.shape and ke.shape == k.shape
+    assert_ulp(qe, _rotate64(q, cos, sin).to(BF), 1, tiny=1e-5, what="q")
+    assert_ulp(ke, _rotate64(k, cos, sin).to(BF), 1, tiny=1e-5, what="k")
+    gq = torch.randn_like(qe)
+    gk = torch.randn_like(ke)
+    torch.autograd.backward([qe, ke], [gq, gk])
+    assert_ulp(qg.grad, _rotate64(gq, cos, sin, transpose=True).to(BF), 1, tiny=1e-5, what="dq")
+    assert_ulp(kg.grad, _rotate64(gk, cos, sin, transpose=True).to(BF), 1, tiny=1e-5, what="dk")
+    # [B, S, H, D] layout (unsqueeze_dim=2) gives the same rotation
+    q2, k2 = hf_apply_rotary_pos_emb(q.transpose(1, 2), k.transpose(1, 2), cos, sin, 2)
+    assert torch.equal(q2.transpose(1, 2), qe.detach()) and torch.equal(k2.transpose(1, 2),
+                                                                        ke.detach())
+
+
+def test_hf_llama_routed_through_registry(gpu):
+    transformers = pytest.importorskip("transformers")
+    from transformers.models.llama import modeling_llama as ml
+    from trainscale_amd import registry
+    original = ml.apply_rotary_pos_emb
+    cfg = transformers.LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2,
+                                   vocab_size=1000, max_position_embeddings=256)
+    torch.manual_seed(1)
+    model = transformers.LlamaModel(cfg).to(gpu).to(BF).eval()
+    ids = torch.randint(0, 1000, (2, 64), device=gpu)
+    calls = []
+    try:
+        with torch.no_grad():
+            ref = model(ids).last_hidden_state.float()
+        registry.KernelPatcher(patch_layernorm=False, patch_mlp=False).patch(model)
+        routed = ml.apply_rotary_pos_emb
+
+        def counting(*a, **kw):
+            calls.append(1)
+            return routed(*a, **kw)
+
+        ml.apply_rotary_pos_emb = counting
+        with torch.no_grad():
+            out = model(ids).last_hidden_state.float()
+    finally:
+        ml.apply_rotary_pos_emb = original
+    assert len(calls) == cfg.num_hidden_layers
+    # transformers rounds each product and the sum to bf16; the kernel rounds once
+    rel = (out - ref).abs().mean() / ref.abs().mean()
+    assert rel < 1e-2, float(rel)
+
+
+def test_packed_rows_from_cu_seqlens(gpu):
+    theta, D, H, L = 500000.0, 128, 4, 512
+    rows_lens = [workloads.packed_doc_lengths(L - 37, 8, 160, 3),
+                 workloads.packed_doc_lengths(L, 8, 160, 4)]
+    cus = [torch.tensor([0] + list(torch.tensor(l).cumsum(0)), dtype=torch.int32, device=gpu)
+           for l in rows_lens]
+    pos = position_ids_from_cu_seqlens(cus, total=L)
+    torch.manual_seed(5)
+    q = torch.randn(2, L, H, D, device=gpu).to(BF)
+    cos, sin = oracle.rope_tables(D, L, theta)
+    y = apply_rope(q, cos.to(gpu), sin.to(gpu), position_ids=pos, inplace=False)
+    yt = apply_rope_theta(q, theta, position_ids=pos, inplace=False)
+    for r, lens in enumerate(rows_lens):
+        start = 0
+        for n in lens:
+            doc = q[r:r + 1, start:start + n].contiguous()
+            assert torch.equal(y[r:r + 1, start:start + n],
+                               apply_rope(doc, cos.to(gpu), sin.to(gpu), inplace=False))
+            assert torch.equal(yt[r:r + 1, start:start + n],
+                               apply_rope_theta(doc, theta, inplace=False))
+            start += n

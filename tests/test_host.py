@@ -120,3 +120,44 @@ def test_patch_boundary_mlp_and_flags():
     p2.patch(model)  # idempotent for the MLP, patches the norm now
     assert p2.patched_layers == [("1", "LlamaRMSNorm")]
     assert "LlamaMLP" in registry.LAYER_PATCHES and "Qwen2MLP" in registry.LAYER_PATCHES
+
+
+def test_position_ids_from_cu_seqlens_matches_pack_sequences_format():
+    from trainscale_amd.kernels.rope_kernels import position_ids_from_cu_seqlens
+    rows, cus = [], []
+    for seed, total in ((1, 700), (2, 1024)):
+        lens = W.packed_doc_lengths(total, 5, 200, seed)
+        pos = W.packed_position_ids(lens)[0]
+        pad = torch.zeros(1024 - pos.numel(), dtype=torch.int64)
+        rows.append(torch.cat([pos, pad]))  # pack_sequences pads positions with 0
+        cus.append(torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32))
+    expect = torch.stack(rows)
+    got = position_ids_from_cu_seqlens(cus, total=1024)
+    assert torch.equal(got, expect)
+    assert torch.equal(position_ids_from_cu_seqlens(cus[1]), expect[1:])
+
+
+def test_rope_patch_routes_hf_apply_and_keeps_cpu_path():
+    transformers = pytest.importorskip("transformers")
+    from transformers.models.llama import modeling_llama as ml
+    original = ml.apply_rotary_pos_emb
+    cfg = transformers.LlamaConfig(hidden_size=64, intermediate_size=128, num_hidden_layers=1,
+                                   num_attention_heads=4, num_key_value_heads=2,
+                                   vocab_size=100, max_position_embeddings=64)
+    torch.manual_seed(0)
+    model = transformers.LlamaModel(cfg).eval()
+    ids = torch.randint(0, 100, (2, 9))
+    with torch.no_grad():
+        before = model(ids).last_hidden_state
+    try:
+        patcher = registry.KernelPatcher(patch_layernorm=False, patch_mlp=False)
+        patcher.patch(model)
+        assert ("rotary_emb", "LlamaRotaryEmbedding") in patcher.patched_layers
+        assert ml.apply_rotary_pos_emb is not original
+        assert ml.apply_rotary_pos_emb._trainscale_amd_original is original
+        assert model.rotary_emb._rope_config.dim in (16, 64)
+        with torch.no_grad():
+            after = model(ids).last_hidden_state  # CPU tensors: the original function
+        assert torch.equal(before, after)
+    finally:
+        ml.apply_rotary_pos_emb = original

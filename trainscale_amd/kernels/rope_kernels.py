@@ -52,6 +52,8 @@ __all__ = [
     "inplace_rope_embedding",
     "apply_rope_theta",
     "RotaryEmbedding",
+    "hf_apply_rotary_pos_emb",
+    "position_ids_from_cu_seqlens",
     "ROPE_GROUP_SIZE",
 ]
 
@@ -356,6 +358,74 @@ def apply_rope_theta(x: Tensor, theta: float = 10000.0, position_ids: Optional[T
         inv_freq = _base_inv_freq(theta, x.shape[-1], "cpu")
     return _RoPEThetaFunction.apply(x, inv_freq, float(scaling_factor), position_ids,
                                     position_offset, interleaved, inplace)
+
+
+class _HFTableRoPEFunction(torch.autograd.Function):
+    """Rotation of HF-layout Q and K with HF's per-token cos/sin.
+
+    q, k: [B, S, H, D] views (any strides, unit last stride); cos, sin: [B or 1, S, D]
+    with duplicated halves (cat(freqs, freqs), the NeoX layout). Token (b, s)
+    uses row b * S + s of the flattened tables (row s when they are shared over
+    the batch), reading its first D / 2 columns. Returns new [B, S, H, D] tensors.
+    """
+
+    @staticmethod
+    def forward(ctx, q: Tensor, k: Tensor, cos: Tensor, sin: Tensor):
+        B, S = q.shape[0], q.shape[1]
+        if cos.shape[0] == 1:
+            pos = torch.arange(S, device=q.device, dtype=torch.int64)
+        else:
+            pos = torch.arange(B * S, device=q.device, dtype=torch.int64).view(B, S)
+        cos2 = cos.reshape(-1, cos.shape[-1])
+        sin2 = sin.reshape(-1, sin.shape[-1])
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+        ops.rope_apply(q, q_out, k, k_out, cos=cos2, sin=sin2, position_ids=pos)
+        ctx.save_for_backward(cos2, sin2, pos)
+        return q_out, k_out
+
+    @staticmethod
+    def backward(ctx, dq: Tensor, dk: Tensor):
+        cos2, sin2, pos = ctx.saved_tensors
+        dq_in, dk_in = torch.empty_like(dq), torch.empty_like(dk)
+        ops.rope_apply(dq, dq_in, dk, dk_in, cos=cos2, sin=sin2, position_ids=pos, backward=True)
+        return dq_in, dk_in, None, None
+
+
+def hf_apply_rotary_pos_emb(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor,
+                            unsqueeze_dim: int = 1) -> Tuple[Tensor, Tensor]:
+    """Drop-in for transformers' ``apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim)``:
+    q, k are [B, H, S, D] (unsqueeze_dim=1) or [B, S, H, D] (unsqueeze_dim=2), cos/sin
+    [B, S, D] with duplicated halves. Computes q*cos + rotate_half(q)*sin in fp32 with
+    one rounding (transformers' eager form rounds each product and the sum)."""
+    if unsqueeze_dim == 1:
+        qo, ko = _HFTableRoPEFunction.apply(q.transpose(1, 2), k.transpose(1, 2), cos, sin)
+        return qo.transpose(1, 2), ko.transpose(1, 2)
+    return _HFTableRoPEFunction.apply(q, k, cos, sin)
+
+
+def position_ids_from_cu_seqlens(cu_seqlens, total: Optional[int] = None) -> Tensor:
+    """Per-token positions of packed rows from their document boundaries.
+
+    cu_seqlens: one int32/int64 tensor [n_docs + 1] (0 = cu[0] < ... < cu[-1] = real
+    tokens of the row) or a list of them, one per packed row: the format
+    ``pack_sequences`` emits (data_pipeline/trainer/packing.py:98-194). Returns int64
+    [rows, total] (total defaults to the longest row's cu[-1]) with positions 0..len-1
+    inside each document and 0 on padding: the position_ids ``pack_sequences``
+    builds, for ``apply_rope(..., position_ids=...)``. Runs on the tensors' device.
+    """
+    rows = list(cu_seqlens) if isinstance(cu_seqlens, (list, tuple)) else [cu_seqlens]
+    rows = [c.to(torch.int64) for c in rows]
+    n = int(max(int(c[-1].item()) for c in rows)) if total is None else int(total)
+    out = torch.zeros((len(rows), n), dtype=torch.int64, device=rows[0].device)
+    for i, cu in enumerate(rows):
+        lens = cu[1:] - cu[:-1]
+        starts = torch.repeat_interleave(cu[:-1], lens)
+        real = starts.numel()
+        if real > n:
+            raise ValueError(f"position_ids_from_cu_seqlens: row {i} has {real} tokens > {n}")
+        out[i, :real] = torch.arange(real, device=cu.device, dtype=torch.int64) - starts
+    return out
 
 
 class RotaryEmbedding(nn.Module):

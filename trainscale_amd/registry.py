@@ -1,4 +1,4 @@
-"""RMSNorm and SwiGLU-MLP patch boundary with TrainScale's registry API.
+"""RMSNorm, SwiGLU-MLP and rotary patch boundary with TrainScale's registry API.
 
 Mirrors ``register_layer_patch``, ``LAYER_PATCHES``, ``auto_patch_layernorm``,
 ``auto_patch_mlp`` and the RMSNorm/MLP part of ``KernelPatcher``
@@ -9,6 +9,13 @@ RMSNorm by ``fast_rms_layernorm`` and a gate/up/down MLP by
 kernels. The patched forward keeps calling the module's original forward for
 tensors that are not on a GPU (the module's own code, not a copy of the kernel
 math).
+
+Rotary modules (``auto_patch_rope``, registry/__init__.py:1209-1282): the
+reference only records a RoPEConfig on the module. Here the patch also routes
+the rotation itself: the ``apply_rotary_pos_emb`` function of the module's
+transformers model file is replaced by ``hf_apply_rotary_pos_emb`` (the gfx950
+kernel reading the model's own cos/sin per token), with the original kept for
+CPU tensors and for layouts it does not cover.
 """
 from __future__ import annotations
 
@@ -17,10 +24,13 @@ from typing import Callable, Dict, List, Tuple
 import torch
 import torch.nn as nn
 
+import sys
+
 from .kernels.fused_kernels import fast_rms_layernorm, swiglu_forward
+from .kernels.rope_kernels import RoPEConfig, RoPEScalingType, hf_apply_rotary_pos_emb
 
 __all__ = ["LAYER_PATCHES", "register_layer_patch", "auto_patch_layernorm", "auto_patch_mlp",
-           "KernelPatcher", "patch_model"]
+           "auto_patch_rope", "KernelPatcher", "patch_model"]
 
 LAYER_PATCHES: Dict[str, Callable[[nn.Module], None]] = {}
 
@@ -76,12 +86,66 @@ for _name in ("LlamaMLP", "Qwen2MLP", "Qwen3MLP", "MistralMLP", "MixtralBlockSpa
     register_layer_patch(_name, auto_patch_mlp)
 
 
+_ROPE_TYPES = {"linear": RoPEScalingType.LINEAR, "ntk": RoPEScalingType.NTK,
+               "yarn": RoPEScalingType.YARN, "dynamic": RoPEScalingType.DYNAMIC_NTK,
+               "longrope": RoPEScalingType.LONGROPE}
+
+
+def _routed_apply(original):
+    """apply_rotary_pos_emb that runs the gfx950 kernel where it covers the call."""
+
+    def apply_rotary_pos_emb(q, k, cos, sin, *args, **kwargs):
+        unsqueeze_dim = kwargs.get("unsqueeze_dim", args[0] if args else 1)
+        ok = (set(kwargs) <= {"unsqueeze_dim"} and len(args) <= 1
+              and isinstance(unsqueeze_dim, int) and unsqueeze_dim in (1, 2)
+              and isinstance(q, torch.Tensor) and q.is_cuda and k.is_cuda and cos.is_cuda
+              and q.dim() == 4 and k.dim() == 4 and cos.dim() == 3
+              and q.shape[-1] == cos.shape[-1] == k.shape[-1] and q.shape[-1] % 2 == 0
+              and q.dtype == k.dtype and sin.shape == cos.shape)
+        if not ok:
+            return original(q, k, cos, sin, *args, **kwargs)
+        return hf_apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim)
+
+    apply_rotary_pos_emb._trainscale_amd_original = original
+    return apply_rotary_pos_emb
+
+
+def auto_patch_rope(module: nn.Module) -> None:
+    """Records the module's RoPEConfig (registry/__init__.py:1209-1265) and routes its model
+    file's apply_rotary_pos_emb to the gfx950 kernel."""
+    dim = getattr(module, "dim", getattr(module, "head_dim", 64))
+    base = getattr(module, "base", getattr(module, "rope_theta", 10000.0))
+    max_seq = getattr(module, "max_position_embeddings", getattr(module, "max_seq_len_cached", 8192))
+    scaling_type, factor = RoPEScalingType.NONE, 1.0
+    rope_scaling = getattr(module, "rope_scaling", None)
+    if isinstance(rope_scaling, dict):
+        scaling_type = _ROPE_TYPES.get(str(rope_scaling.get("type", "none")).lower(),
+                                       RoPEScalingType.NONE)
+        factor = rope_scaling.get("factor", 1.0)
+    module._rope_config = RoPEConfig(dim=dim, max_seq_len=max_seq, base=base,
+                                     scaling_type=scaling_type, scaling_factor=factor)
+    module._uses_triton_rope = True
+    model_file = sys.modules.get(module.__class__.__module__)
+    fn = getattr(model_file, "apply_rotary_pos_emb", None) if model_file is not None else None
+    if callable(fn) and not hasattr(fn, "_trainscale_amd_original"):
+        setattr(model_file, "apply_rotary_pos_emb", _routed_apply(fn))
+    module._trainscale_amd_patched = True
+
+
+for _name in ("LlamaRotaryEmbedding", "LlamaLinearScalingRotaryEmbedding",
+              "LlamaDynamicNTKScalingRotaryEmbedding", "Qwen2RotaryEmbedding",
+              "Qwen3RotaryEmbedding", "MistralRotaryEmbedding", "GemmaRotaryEmbedding",
+              "Gemma2RotaryEmbedding", "Phi3RotaryEmbedding", "Phi4RotaryEmbedding",
+              "FalconRotaryEmbedding", "YiRotaryEmbedding"):
+    register_layer_patch(_name, auto_patch_rope)
+
+
 class KernelPatcher:
     """Applies the registered layer patches to a model (registry/__init__.py:1331-1418).
 
-    ``patch_attention``, ``patch_rope`` and ``patch_fp8`` are accepted for
-    signature compatibility; this layer registers no attention, rotary-module
-    or FP8 patches, so they select nothing.
+    ``patch_attention`` and ``patch_fp8`` are accepted for signature
+    compatibility; this layer registers no attention or FP8 patches, so they
+    select nothing.
     """
 
     def __init__(self, patch_layernorm: bool = True, patch_mlp: bool = True,
@@ -106,6 +170,9 @@ class KernelPatcher:
                     continue
             elif cls.endswith("MLP"):
                 if not self.patch_mlp:
+                    continue
+            elif "Rotary" in cls:
+                if not self.patch_rope:
                     continue
             fn(module)
             if getattr(module, "_trainscale_amd_patched", False):
