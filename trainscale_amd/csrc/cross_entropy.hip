@@ -414,25 +414,31 @@ __global__ __launch_bounds__(kFusedThreads) void ce_fused_vec(
 #pragma unroll
   for (int k = 0; k < kFusedKv; ++k) buf[k] = buf_ld16_stream(xi, fused_voff(k, nvec, 16));
   float m = -INFINITY, s = 0.f, sz = 0.f;
+  // Folds one vector into (m, s): one rescale of the running sum per vector.
+  auto fold = [&](const u32x4& q) {
+    float z[VE];
+    Elt<T>::unpack(q, z);
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      z[i] = xform<kXform>(z[i], xf);
+      if constexpr (kSmooth) sz += z[i];
+    }
+    float cm = z[0];
+#pragma unroll
+    for (int i = 1; i < VE; ++i) cm = __builtin_fmaxf(cm, z[i]);
+    const float mn = __builtin_fmaxf(m, cm), mb = mn * kLog2e;
+    float cs = fast_exp2(__builtin_fmaf(z[0], kLog2e, -mb));
+#pragma unroll
+    for (int i = 1; i < VE; ++i) cs += fast_exp2(__builtin_fmaf(z[i], kLog2e, -mb));
+    s = (s == 0.f ? 0.f : s * fast_exp2((m - mn) * kLog2e)) + cs;
+    m = mn;
+  };
 #pragma unroll
   for (int k = 0; k < kFusedKv; ++k) {
-    if (threadIdx.x + k * kFusedThreads < nvec) {
-      float z[VE];
-      Elt<T>::unpack(buf[k], z);
-      float cm = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < VE; ++i) {
-        z[i] = xform<kXform>(z[i], xf);
-        cm = fmaxf(cm, z[i]);
-        if constexpr (kSmooth) sz += z[i];
-      }
-      const float mn = fmaxf(m, cm), mb = mn * kLog2e;
-      float cs = 0.f;
-#pragma unroll
-      for (int i = 0; i < VE; ++i) cs += fast_exp2(__builtin_fmaf(z[i], kLog2e, -mb));
-      s = (s == 0.f ? 0.f : s * fast_exp2((m - mn) * kLog2e)) + cs;
-      m = mn;
-    }
+    // Vectors every thread holds take a uniform branch; only the row's last
+    // partial sweep tests each lane.
+    if ((k + 1) * kFusedThreads <= nvec) fold(buf[k]);
+    else if (threadIdx.x + k * kFusedThreads < nvec) fold(buf[k]);
   }
   const float l = fused_lse<kSmooth>(m, s, sz, lds);
   // The gradient pass re-unpacks the stored vectors; this keeps the compiler
@@ -456,25 +462,38 @@ __global__ __launch_bounds__(kFusedThreads) void ce_fused_vec(
     const float adl = fabsf(dl);
     const float l2 = l * kLog2e;
     const float l2d = l2 - __builtin_amdgcn_logf(adl);  // v_log_f32 is log2
-    const uint32_t sgn = dl < 0.f ? sign_bits<G>() : 0u;
+    // The sign of dl and the position of the label are uniform over the
+    // workgroup: both corrections are uniform branches, and only the lane
+    // holding the label runs its correction.
+    const bool neg = (__builtin_bit_cast(uint32_t, dl) >> 31) != 0;
+    const int64_t lv = label >= 0 && label < V ? label / VE : -1;  // vector holding the label
+    const int klab = lv < 0 ? -1 : (int)(lv / kFusedThreads);
+    const int tlab = lv < 0 ? -1 : (int)(lv % kFusedThreads);
+    const int elab = lv < 0 ? 0 : (int)(label % VE);
 #pragma unroll
     for (int k = 0; k < kFusedKv; ++k) {
       float z[VE], g[VE];
       Elt<T>::unpack(buf[k], z);
 #pragma unroll
       for (int i = 0; i < VE; ++i) g[i] = fast_exp2(__builtin_fmaf(z[i], kLog2e, -l2d));
-      const int64_t d = label - (int64_t)(threadIdx.x + k * kFusedThreads) * VE;
-      if (d >= 0 && d < VE) {
+      if (k == klab && (int)threadIdx.x == tlab) {
 #pragma unroll
         for (int i = 0; i < VE; ++i)
-          if (d == i) g[i] = adl * (fast_exp2(__builtin_fmaf(z[i], kLog2e, -l2)) - 1.f);
+          if (i == elab) g[i] = adl * (fast_exp2(__builtin_fmaf(z[i], kLog2e, -l2)) - 1.f);
       }
       const int off = fused_voff(k, nvec, kGradBytes);
       if constexpr (kGradBytes == 32) {
-        buf_st16_stream(Elt<float>::pack(g) ^ sgn, go, off);
-        buf_st16_stream(Elt<float>::pack(g + 4) ^ sgn, go, off + 16);
+        u32x4 p0 = Elt<float>::pack(g), p1 = Elt<float>::pack(g + 4);
+        if (neg) {
+          p0 ^= sign_bits<G>();
+          p1 ^= sign_bits<G>();
+        }
+        buf_st16_stream(p0, go, off);
+        buf_st16_stream(p1, go, off + 16);
       } else {
-        buf_st16_stream(Elt<G>::pack(g) ^ sgn, go, off);
+        u32x4 p = Elt<G>::pack(g);
+        if (neg) p ^= sign_bits<G>();
+        buf_st16_stream(p, go, off);
       }
     }
   } else {

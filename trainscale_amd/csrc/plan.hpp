@@ -30,12 +30,15 @@ constexpr int kWave = 64;
 // not (measured on MI355X: one 16-byte load per thread copies at ~6.4 TB/s,
 // eight per thread at ~4.2 TB/s).
 //
-// Backward: each workgroup walks `steps` consecutive row groups and keeps the
-// dW contributions of its threads' columns in registers; it writes rpb fp32
-// partial rows at the end, which a second kernel sums in a fixed order.
+// Backward: each workgroup walks up to `steps` row groups spaced `grid` apart
+// (grid * steps >= the number of row groups) and keeps the dW contributions
+// of its threads' columns in registers; it writes rpb fp32 partial rows at
+// the end, which a second kernel sums in a fixed order.
 // ---------------------------------------------------------------------------
 constexpr int kMaxKv = 4;                 // vectors per thread on the register path
-constexpr int64_t kBwdGridTarget = 512;   // backward workgroups (2 per CU on 256 CUs)
+// Backward workgroups, 2 per CU on 256 CUs (measured on MI355X at
+// [16384, 4096]: 256, 1024 and 2048 workgroups were all slower).
+constexpr int64_t kBwdGridTarget = 512;
 constexpr int64_t kGenericRowsPerGroup = 64;
 
 // Elements per 16-byte vector.

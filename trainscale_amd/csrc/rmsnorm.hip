@@ -164,8 +164,20 @@ __global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
 
 // ---------------------------------------------------------------------------
 // Backward, register path: dx plus one fp32 dW partial row per row slot.
-// Workgroup b handles row groups [b*steps, (b+1)*steps), each of kRpb rows.
+// Workgroup b handles row groups b, b + G, b + 2G, ... (G = gridDim.x, at
+// most `steps` of them), each of kRpb rows. At any moment the running
+// workgroups then work on about G consecutive row groups, a compact window of
+// HBM, rather than on G groups spread over the whole matrix: measured on
+// MI355X at [16384, 4096] (G = 512), 73 us against 82 us for contiguous
+// blocks of row groups per workgroup; 265 us against 300 us at [32768, 8192].
 // ---------------------------------------------------------------------------
+template <typename T, int KV>
+struct BwdSlot {
+  u32x4 xv[KV], dv[KV];  // raw loads; lanes outside the matrix hold other data
+  float rstd;            // raw load
+  bool valid;            // row inside this workgroup's range and the matrix
+};
+
 template <typename T, typename W, int TPR, int KV>
 __global__ __launch_bounds__(512) void rms_bwd_reg(
     const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x, int64_t ldx,
@@ -192,28 +204,54 @@ __global__ __launch_bounds__(512) void rms_bwd_reg(
     if (w != nullptr && v < nvec) load_w<W, V>(w, (int64_t)v * V, wf[k]);
   }
 
-  // `steps` is uniform over the workgroup (barriers inside when TPR > 64).
-  for (int64_t st = 0; st < steps; ++st) {
-    const int64_t row = ((int64_t)blockIdx.x * steps + st) * kRpb + sub;
-    const bool valid = row < rows;
-    const T* xr = x + row * ldx;
-    const T* dyr = dy + row * lddy;
-    u32x4 xv[KV], dv[KV];
+  // Loads of row group st into `sl` (zeros past the end of this workgroup's
+  // range or of the matrix).
+  // This thread's first row and its element t * V there; row group st adds
+  // st * kRpb rows (a uniform offset).
+  const int64_t row0 = (int64_t)blockIdx.x * kRpb + sub;
+  const int64_t rstep = (int64_t)gridDim.x * kRpb;
+  const T* xb = x + row0 * ldx + (int64_t)t * V;
+  const T* dyb = dy + row0 * lddy + (int64_t)t * V;
+  //
+  //
+  // The loads are unconditional (an address outside the matrix is replaced by
+  // the thread's first element, which exists whenever the kernel runs) and
+  // the data of such lanes is zeroed where it is used, which keeps the loads
+  // free of branches.
+  auto issue = [&](BwdSlot<T, KV>& sl, int64_t st) {
+    const int64_t row = row0 + st * rstep;
+    const bool valid = st < steps && row < rows;
+    const int64_t sx = valid ? st * (rstep * ldx) : 0;
+    const int64_t sdy = valid ? st * (rstep * lddy) : 0;
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
-      const int v = t + k * TPR;
-      const bool ok = valid && v < nvec;
-      xv[k] = ok ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
-      dv[k] = ok ? ld16_stream(dyr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+      const bool ok = valid && t + k * TPR < nvec;
+      sl.xv[k] = ld16_stream(xb + (ok ? sx + k * TPR * V : 0));
+      sl.dv[k] = ld16_stream(dyb + (ok ? sdy + k * TPR * V : 0));
     }
-    const float rstd = valid ? rstd_in[row] : 0.f;
+    sl.rstd = rstd_in[valid ? row : row0];
+    sl.valid = valid;
+  };
+
+  // dx of row group st from its loaded slot; dW contributions into acc.
+  auto body = [&](BwdSlot<T, KV>& sl, int64_t st) {
+    const int64_t row = row0 + st * rstep;
+    const bool valid = sl.valid;
+    const float rstd = valid ? sl.rstd : 0.f;
+    const u32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      const bool ok = valid && t + k * TPR < nvec;
+      sl.xv[k] = ok ? sl.xv[k] : zero;
+      sl.dv[k] = ok ? sl.dv[k] : zero;
+    }
     // c1 = mean(dy * w * xhat); rows that are not valid hold zeros.
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
       float xf[V], df[V];
-      Elt<T>::unpack(xv[k], xf);
-      Elt<T>::unpack(dv[k], df);
+      Elt<T>::unpack(sl.xv[k], xf);
+      Elt<T>::unpack(sl.dv[k], df);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         const float xh = xf[i] * rstd;
@@ -222,6 +260,10 @@ __global__ __launch_bounds__(512) void rms_bwd_reg(
       }
     }
     const float c1 = row_reduce<TPR, kBlock>(s, red[st & 1]) / fcols;
+    // dx unpacks the slot again: carrying the unpacked floats across the
+    // reduction would double the slot's registers.
+#pragma unroll
+    for (int k = 0; k < KV; ++k) asm volatile("" : "+v"(sl.xv[k]), "+v"(sl.dv[k]));
     if (valid) {
       T* dxr = dx + row * lddx;
 #pragma unroll
@@ -229,14 +271,22 @@ __global__ __launch_bounds__(512) void rms_bwd_reg(
         const int v = t + k * TPR;
         if (v < nvec) {
           float xf[V], df[V], o[V];
-          Elt<T>::unpack(xv[k], xf);
-          Elt<T>::unpack(dv[k], df);
+          Elt<T>::unpack(sl.xv[k], xf);
+          Elt<T>::unpack(sl.dv[k], df);
 #pragma unroll
           for (int i = 0; i < V; ++i) o[i] = rstd * (df[i] * wf[k][i] - (xf[i] * rstd) * c1);
           st16_stream(dxr + (int64_t)v * V, Elt<T>::pack(o));
         }
       }
     }
+  };
+
+  // `steps` is uniform over the workgroup (barriers inside row_reduce when
+  // TPR > 64).
+  for (int64_t st = 0; st < steps; ++st) {
+    BwdSlot<T, KV> sl;
+    issue(sl, st);
+    body(sl, st);
   }
 
   if (partial == nullptr) return;  // dW not requested
