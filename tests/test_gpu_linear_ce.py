@@ -5,7 +5,11 @@ absolute in bf16. Since 2e-2 is loose next to these gradients' size, they are
 also held to a relative Frobenius error of 1e-2 against the oracle, which
 follows the reference's bf16 numerics (bf16 logits, bf16 dlogits, fp32
 accumulation). With logits that are exact in bf16, GEMM results must agree to
-fp32 rounding, which pins the MFMA tiling and index math.
+fp32 rounding, which pins the MFMA tiling and index math. Per-row losses and lse
+are held to 1e-5 on at least 98% of rows and, on every row, to that plus the
+change one bf16 rounding flip per logit can cause (a logit within an fp32
+rounding error of a bf16 midpoint rounds either way under another summation
+order).
 """
 import math
 
@@ -26,6 +30,38 @@ def rel_fro(a, b):
     return float((a - b).norm() / b.norm().clamp(min=1e-30))
 
 
+def bf16_ulp(x):
+    """Spacing of bf16 values at |x| (8 significant bits)."""
+    e = torch.frexp(x.abs().clamp(min=2.0 ** -126))[1]
+    return torch.ldexp(torch.ones_like(x), e - 8)
+
+
+def flip_bound(h, w, labels):
+    """Per-row bound on the change of lse and of the row loss when bf16 logits round
+    one ulp the other way (the GEMM's fp32 sums are ordered differently from the CPU
+    oracle's, so a logit within a rounding error of a bf16 midpoint may flip):
+    sum_j p_j ulp(z_j) (+ ulp(z_label) for the loss)."""
+    z = (h.float().cpu() @ w.float().cpu().t()).to(BF).float()
+    p = torch.softmax(z, dim=1)
+    u = bf16_ulp(z)
+    lse_b = (p * u).sum(1)
+    lab = labels.cpu().reshape(-1)
+    valid = lab != -100
+    lab_u = torch.zeros_like(lse_b)
+    lab_u[valid] = u[valid.nonzero().squeeze(1), lab[valid]]
+    return lse_b, lse_b + lab_u
+
+
+def assert_rows_close(got, ref, bound, what):
+    """Within 1e-5 (relative and absolute) of the oracle on at least 98% of rows, and
+    within one bf16 rounding flip of the logits (bound) on every row."""
+    got, ref = got.cpu().float(), ref.float()
+    d = (got - ref).abs()
+    tight = d <= 1e-5 + 1e-5 * ref.abs()
+    assert int((~tight).sum()) <= max(1, len(ref) // 50), (what, int((~tight).sum()))
+    assert bool((d <= 1e-5 + 1e-5 * ref.abs() + bound).all()), (what, float(d.max()))
+
+
 def check_against_oracle(h, w, labels, reduction="mean", chunk=None):
     loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels, reduction=reduction,
                                                          chunk_tokens=chunk)
@@ -33,11 +69,10 @@ def check_against_oracle(h, w, labels, reduction="mean", chunk=None):
         h, w, labels, reduction=reduction, bf16_logits=True, return_rows=True)
     assert abs(loss.item() - float(ref_loss)) <= 1e-5 * abs(float(ref_loss)), (loss.item(),
                                                                               float(ref_loss))
-    torch.testing.assert_close(rows.cpu(), ref_rows, rtol=1e-5, atol=1e-5)
+    lse_bound, row_bound = flip_bound(h, w, labels)
+    assert_rows_close(rows, ref_rows, row_bound, "loss rows")
     valid = labels.cpu() != -100
-    # logits on a bf16 rounding boundary may round either way under another fp32
-    # summation order, so lse gets the loss's 1e-5 bar
-    torch.testing.assert_close(lse.cpu()[valid], ref_lse[valid], rtol=1e-5, atol=1e-5)
+    assert_rows_close(lse[valid.to(lse.device)], ref_lse[valid], lse_bound[valid], "lse")
     for name, g, r in (("grad_hidden", gh, ref_gh), ("grad_weight", gw, ref_gw)):
         assert (g.float().cpu() - r.float()).abs().max().item() <= 2e-2, name
         assert rel_fro(g, r) <= 1e-2, (name, rel_fro(g, r))
@@ -45,7 +80,7 @@ def check_against_oracle(h, w, labels, reduction="mean", chunk=None):
 
 
 @pytest.mark.parametrize("N,H,V", [(512, 256, 1000), (520, 64, 256), (256, 512, 4096),
-                                   (8, 32, 8)])
+                                   (8, 32, 8), (264, 40, 520), (1032, 296, 776)])
 def test_small_shapes(gpu, N, H, V):
     torch.manual_seed(N + H + V)
     h = torch.randn(N, H, device=gpu).to(BF)

@@ -10,11 +10,14 @@
 //      exp, and the logit at the row's label.
 //   2. row statistics -> lse, per-row loss (0 on ignore_index rows).
 //   3. dlogits = (softmax - onehot) * scale in bf16, written over the logits
-//      scratch and transposed into a [V, Nc] scratch (scale = 1/n_valid for
-//      the mean, 1 for the sum).
-//   4. grad_hidden[chunk] = dlogits @ weight   (MFMA, B = weight^T [H, V])
-//   5. grad_weight      += dlogits^T @ hidden  (MFMA, B = hidden^T [H, N]);
-//      with several chunks the sum is carried in fp32 and rounded once.
+//      scratch (scale = 1/n_valid for the mean, 1 for the sum).
+//   4. grad_hidden[chunk] = dlogits @ weight   (MFMA; the weight is read in
+//      place as the MN-major [H, V] operand)
+//   5. grad_weight      += dlogits^T @ hidden  (MFMA; dlogits and hidden are
+//      read in place as MN-major operands); with several chunks the sum is
+//      carried in fp32 and rounded once.
+//   No operand is transposed in memory: gemm.hpp reads MN-major tiles with
+//   transposing LDS loads.
 // Every reduction has a fixed order, so results are bit-reproducible.
 //
 // Scratch lives in a caller workspace (ts_flce_workspace_size): with one chunk
@@ -42,6 +45,9 @@ enum EpiMode : int {
   kEpiAccBf16 = 4     // bf16 C = C32 + acc
 };
 
+// A [M, K] and B [N, K] of C = A B^T; lda / ldb are the strides between
+// consecutive rows of a K-major operand, or between consecutive k of an
+// MN-major one (flce_gemm's kMA / kMB).
 struct GemmArgs {
   const __bf16* A;
   int64_t lda;
@@ -89,7 +95,7 @@ __device__ inline void stage_f32_half(const Acc& acc, int half, uint8_t* region,
       }
 }
 
-template <int kMode>
+template <int kMode, int kMA, int kMB>
 __global__ __launch_bounds__(ts_gemm::kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void flce_gemm(const GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[ts_gemm::kLdsBytes];
@@ -100,7 +106,7 @@ void flce_gemm(const GemmArgs a) {
   const int64_t m0 = mt * BM;
   const int64_t n0 = nt * BN;
   Acc acc;
-  ts_gemm::mainloop(a.A, a.lda, a.M, a.B, a.ldb, a.N, a.K, m0, n0, smem, acc);
+  ts_gemm::mainloop<kMA, kMB>(a.A, a.lda, a.M, a.B, a.ldb, a.N, a.K, m0, n0, smem, acc);
 
   const int wid = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -243,84 +249,52 @@ __global__ __launch_bounds__(256) void flce_loss(const float* __restrict__ loss_
   }
 }
 
-// dlogits of a chunk, 64 x 64 tiles: D = (exp(z - lse) - onehot) * scale in
-// bf16, written over the logits [M, V] and transposed into Dt [V, M].
+// dlogits of a chunk in place: D = (exp(z - lse) - onehot) * scale in bf16
+// over the logits [M, V] (0 on ignored rows, which are not read). One-shot
+// grid: a thread owns kDlKv 16-byte vectors of a row, spaced one workgroup
+// apart; blockIdx.x = row * chunks + chunk.
+constexpr int kDlKv = 2;
 __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int64_t ldl,
-                                                    __bf16* __restrict__ Dt, int64_t lddt,
                                                     const float* __restrict__ lse,
                                                     const int64_t* __restrict__ labels,
-                                                    int64_t M, int64_t V, int64_t ignore_index,
+                                                    int64_t V, int64_t chunks,
+                                                    int64_t ignore_index,
                                                     const float* __restrict__ scale_p) {
-  __shared__ __bf16 tile[64][64 + 8];  // [v][m]
-  const int64_t v0 = (int64_t)blockIdx.x * 64;
-  const int64_t r0 = (int64_t)blockIdx.y * 64;
+  const int64_t r = (int64_t)blockIdx.x / chunks;
+  const int64_t c0 = ((int64_t)blockIdx.x % chunks) * (256 * kDlKv) + threadIdx.x;
+  const int64_t nvec = V / 8;
+  const int64_t lab = labels[r];
+  __bf16* row = L + r * ldl;
+  if (lab == ignore_index) {
+    const u32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < kDlKv; ++u) {
+      const int64_t v = c0 + u * 256;
+      if (v < nvec) st16_stream(row + v * 8, zero);
+    }
+    return;
+  }
+  u32x4 q[kDlKv];
+#pragma unroll
+  for (int u = 0; u < kDlKv; ++u) {
+    const int64_t v = c0 + u * 256;
+    if (v < nvec) q[u] = ld16_stream(row + v * 8);
+  }
   const float scale = *scale_p;
+  const float l2 = lse[r] * kLog2e;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = threadIdx.x + 256 * h;  // 512 chunks of 8
-    const int lr = q >> 3;
-    const int lc = (q & 7) * 8;
-    const int64_t r = r0 + lr;
-    const int64_t c = v0 + lc;
-    float g[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (r < M && c < V) {
-      const int64_t lab = labels[r];
-      __bf16* p = L + r * ldl + c;
-      if (lab != ignore_index) {
-        float z[8];
-        Elt<__bf16>::unpack(ld16(p), z);
-        const float l2 = lse[r] * kLog2e;
+  for (int u = 0; u < kDlKv; ++u) {
+    const int64_t v = c0 + u * 256;
+    if (v < nvec) {
+      float z[8], g[8];
+      Elt<__bf16>::unpack(q[u], z);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pr = fast_exp2(__builtin_fmaf(z[e], kLog2e, -l2));
-          g[e] = scale * (c + e == lab ? pr - 1.f : pr);
-        }
+      for (int e = 0; e < 8; ++e) {
+        const float pr = fast_exp2(__builtin_fmaf(z[e], kLog2e, -l2));
+        g[e] = scale * (v * 8 + e == lab ? pr - 1.f : pr);
       }
-      st16(p, Elt<__bf16>::pack(g));
+      st16_stream(row + v * 8, Elt<__bf16>::pack(g));
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) tile[lc + e][lr] = (__bf16)g[e];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = threadIdx.x + 256 * h;
-    const int lv = q >> 3;
-    const int lm = (q & 7) * 8;
-    const int64_t vv = v0 + lv;
-    const int64_t mm = r0 + lm;
-    if (vv < V && mm < M) {
-      // M % 8 == 0: the 8 rows of a chunk are all in range together
-      st16(Dt + vv * lddt + mm, *reinterpret_cast<const u32x4*>(&tile[lv][lm]));
-    }
-  }
-}
-
-// out[c][r] = in[r][c] for a bf16 [R, C] matrix, 64 x 64 tiles; R, C multiples of 8.
-__global__ __launch_bounds__(256) void transpose_bf16(const __bf16* __restrict__ in, int64_t ldi,
-                                                      __bf16* __restrict__ out, int64_t ldo,
-                                                      int64_t R, int64_t C) {
-  __shared__ __bf16 tile[64][64 + 8];  // [c][r]
-  const int64_t c0 = (int64_t)blockIdx.x * 64;
-  const int64_t r0 = (int64_t)blockIdx.y * 64;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = threadIdx.x + 256 * h;
-    const int lr = q >> 3;
-    const int lc = (q & 7) * 8;
-    float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (r0 + lr < R && c0 + lc < C) Elt<__bf16>::unpack(ld16(in + (r0 + lr) * ldi + c0 + lc), f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) tile[lc + e][lr] = (__bf16)f[e];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int q = threadIdx.x + 256 * h;
-    const int lc = q >> 3;
-    const int lr = (q & 7) * 8;
-    if (c0 + lc < C && r0 + lr < R)
-      st16(out + (c0 + lc) * ldo + r0 + lr, *reinterpret_cast<const u32x4*>(&tile[lc][lr]));
   }
 }
 
@@ -381,8 +355,7 @@ inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct Layout {
   int64_t chunk, nchunks, nparts;
-  size_t off_logits, off_dt, off_wt, off_ht, off_stats, off_zlab, off_lse, off_rows, off_misc,
-      off_acc, total;
+  size_t off_logits, off_stats, off_zlab, off_lse, off_rows, off_misc, off_acc, total;
 };
 
 Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
@@ -398,9 +371,6 @@ Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
     return o;
   };
   l.off_logits = take((size_t)l.chunk * V * 2);
-  l.off_dt = grads ? take((size_t)V * l.chunk * 2) : 0;
-  l.off_wt = grads ? take((size_t)H * V * 2) : 0;
-  l.off_ht = grads ? take((size_t)H * N * 2) : 0;
   l.off_stats = take((size_t)l.nparts * l.chunk * sizeof(float2));
   l.off_zlab = take((size_t)N * 4);
   l.off_lse = take((size_t)N * 4);
@@ -411,20 +381,14 @@ Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
   return l;
 }
 
-template <int kMode>
+template <int kMode, int kMA = ts_gemm::kKMajor, int kMB = ts_gemm::kKMajor>
 ts_status launch_gemm(const GemmArgs& a, hipStream_t st, const char* name) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return TS_OK;
   if (tiles > 0x7fffffffLL) return ts_host::fail(TS_ERR_SHAPE, "%s: too many tiles", name);
-  hipLaunchKernelGGL((flce_gemm<kMode>), dim3((unsigned)tiles), dim3(ts_gemm::kThreads), 0, st, a);
+  hipLaunchKernelGGL((flce_gemm<kMode, kMA, kMB>), dim3((unsigned)tiles),
+                     dim3(ts_gemm::kThreads), 0, st, a);
   return ts_host::check_launch(name);
-}
-
-ts_status launch_transpose(const __bf16* in, int64_t ldi, __bf16* out, int64_t ldo, int64_t R,
-                           int64_t C, hipStream_t st) {
-  const dim3 grid((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64));
-  hipLaunchKernelGGL(transpose_bf16, grid, dim3(256), 0, st, in, ldi, out, ldo, R, C);
-  return ts_host::check_launch("transpose_bf16");
 }
 
 }  // namespace
@@ -485,9 +449,6 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
                 lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   __bf16* Lc = reinterpret_cast<__bf16*>(ws + lay.off_logits);
-  __bf16* Dt = reinterpret_cast<__bf16*>(ws + lay.off_dt);
-  __bf16* Wt = reinterpret_cast<__bf16*>(ws + lay.off_wt);
-  __bf16* Ht = reinterpret_cast<__bf16*>(ws + lay.off_ht);
   float2* stats = reinterpret_cast<float2*>(ws + lay.off_stats);
   float* zlab = reinterpret_cast<float*>(ws + lay.off_zlab);
   float* lse_ws = lse != nullptr ? lse : reinterpret_cast<float*>(ws + lay.off_lse);
@@ -500,10 +461,6 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
 
   hipLaunchKernelGGL(flce_count, dim3(1), dim3(256), 0, st, labels, N, ignore_index, n_valid);
   TS_TRY(ts_host::check_launch("flce_count"));
-  if (grads) {
-    TS_TRY(launch_transpose(Wd, ldw, Wt, V, V, H, st));  // Wt [H, V]
-    TS_TRY(launch_transpose(Hd, ldh, Ht, N, N, H, st));  // Ht [H, N]
-  }
   // Pass 1 over chunks: logits, statistics, per-row loss (and lse).
   // With gradients the dlogits of a chunk are consumed right away, so the
   // loss scale (which needs every row's label) is computed up front.
@@ -534,29 +491,31 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
                        rows_ws + r0);
     TS_TRY(ts_host::check_launch("flce_rows"));
     if (!grads) continue;
-    const dim3 dgrid((unsigned)((V + 63) / 64), (unsigned)((Mc + 63) / 64));
-    hipLaunchKernelGGL(flce_dlogits, dgrid, dim3(256), 0, st, Lc, V, Dt, Mc, lse_ws + r0,
-                       labels + r0, Mc, V, ignore_index, scale);
+    const int64_t dchunks = (V / 8 + 256 * kDlKv - 1) / (256 * kDlKv);
+    hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(Mc * dchunks)), dim3(256), 0, st, Lc, V,
+                       lse_ws + r0, labels + r0, V, dchunks, ignore_index, scale);
     TS_TRY(ts_host::check_launch("flce_dlogits"));
+    using ts_gemm::kKMajor;
+    using ts_gemm::kMNMajor;
     if (grad_hidden != nullptr) {
       GemmArgs d{};
-      d.A = Lc;  // dlogits [Mc, V]
+      d.A = Lc;  // dlogits [Mc, V], K-major
       d.lda = V;
-      d.B = Wt;  // weight^T [H, V]
-      d.ldb = V;
+      d.B = Wd;  // weight [V, H] as the [H, V] operand: MN-major, k = v
+      d.ldb = ldw;
       d.M = Mc;
       d.N = H;
       d.K = V;
       d.C = static_cast<__bf16*>(grad_hidden) + r0 * H;
       d.ldc = H;
-      TS_TRY(launch_gemm<kEpiBf16>(d, st, "flce_gemm_dhidden"));
+      TS_TRY((launch_gemm<kEpiBf16, kKMajor, kMNMajor>(d, st, "flce_gemm_dhidden")));
     }
     if (grad_weight != nullptr) {
       GemmArgs d{};
-      d.A = Dt;       // dlogits^T [V, Mc]
-      d.lda = Mc;
-      d.B = Ht + r0;  // hidden^T [H, N], columns r0 .. r0 + Mc
-      d.ldb = N;
+      d.A = Lc;             // dlogits [Mc, V] as the [V, Mc] operand: MN-major, k = token
+      d.lda = V;
+      d.B = Hd + r0 * ldh;  // hidden rows r0 .. r0 + Mc as the [H, Mc] operand: MN-major
+      d.ldb = ldh;
       d.M = V;
       d.N = H;
       d.K = Mc;
@@ -565,13 +524,13 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
       d.C32 = acc32;
       d.ldc32 = H;
       if (lay.nchunks == 1) {
-        TS_TRY(launch_gemm<kEpiBf16>(d, st, "flce_gemm_dweight"));
+        TS_TRY((launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
       } else if (c == 0) {
-        TS_TRY(launch_gemm<kEpiF32>(d, st, "flce_gemm_dweight"));
+        TS_TRY((launch_gemm<kEpiF32, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
       } else if (c + 1 < lay.nchunks) {
-        TS_TRY(launch_gemm<kEpiAccF32>(d, st, "flce_gemm_dweight"));
+        TS_TRY((launch_gemm<kEpiAccF32, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
       } else {
-        TS_TRY(launch_gemm<kEpiAccBf16>(d, st, "flce_gemm_dweight"));
+        TS_TRY((launch_gemm<kEpiAccBf16, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
       }
     }
   }
