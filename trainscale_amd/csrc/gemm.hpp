@@ -165,7 +165,11 @@ __device__ inline void issue_loads(const TileLoader& t, int64_t k0, int64_t K, u
 
 // MN-major tile loads: rows [r0, r0 + 256) of the operand, k-block [k0,
 // k0 + 32). LDS byte (kr, p) of the tile (kr < 32, p < 512) holds logical byte
-// p ^ ((kr & 3) << 5) of k-row kr: the 16-byte chunk at p is 8 consecutive r.
+// p ^ ((kr & 3) << 6) of k-row kr: the 16-byte chunk at p is 8 consecutive r.
+// A half-wave of ds_read_b64_tr_b16 (see read_op_t) reads 64 bytes from each
+// of 4 consecutive k-rows; the swizzle puts them in the 4 distinct 64-byte
+// quarters of a 256-byte bank window (XOR in 32-byte units instead measured
+// 8% of the kernel's cycles as bank conflicts per operand).
 // Wave load u covers LDS chunks [(4u + wid) * 64, +64): k-rows 2 (4u + wid)
 // and 2 (4u + wid) + 1.
 struct TileLoaderT {
@@ -175,7 +179,7 @@ struct TileLoaderT {
   int kr[kLoadsPerWave];        // k-row (0..31) of this lane's chunk
 };
 
-__device__ inline int swz_t(int kr) { return (kr & 3) << 5; }
+__device__ inline int swz_t(int kr) { return (kr & 3) << 6; }
 
 __device__ inline TileLoaderT make_loader_t(const __bf16* g, int64_t ld, int64_t nrows,
                                             int64_t r0) {
