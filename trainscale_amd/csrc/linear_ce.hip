@@ -7,8 +7,9 @@
 //      to bf16 (the logits the reference's bf16 matmul produces,
 //      rl_training.py:177), stores them to an [Nc, V] scratch, and from the
 //      same bf16 values writes per (row, 128-column slice) max and sum of
-//      exp, and the logit at the row's label.
-//   2. row statistics -> lse, per-row loss (0 on ignore_index rows).
+//      exp.
+//   2. row statistics -> lse; per-row loss = lse - the stored logit at the
+//      label (0 on ignore_index rows).
 //   3. dlogits = (softmax - onehot) * scale in bf16, written over the logits
 //      scratch (scale = 1/n_valid for the mean, 1 for the sum).
 //   4. grad_hidden[chunk] = dlogits @ weight   (MFMA; the weight is read in
@@ -38,7 +39,7 @@ using ts_gemm::BN;
 constexpr int kStagePitch = 256;  // bytes per staged epilogue row (128 bf16)
 
 enum EpiMode : int {
-  kEpiLogits = 0,     // bf16 C + row statistics + label logit
+  kEpiLogits = 0,     // bf16 C + row statistics
   kEpiBf16 = 1,       // bf16 C
   kEpiF32 = 2,        // fp32 C32 = acc
   kEpiAccF32 = 3,     // fp32 C32 += acc
@@ -59,9 +60,7 @@ struct GemmArgs {
   float* C32;     // fp32 accumulator (modes 2, 3, 4)
   int64_t ldc32;
   // logits epilogue
-  const int64_t* labels;  // labels of rows [0, M) of this chunk
   float2* stats;          // [M][2 * NT] (max, sum exp) per 128-column slice
-  float* zlab;            // [M] logit at the label (written by the slice holding it)
 };
 
 // Writes the wave's 128 x 128 accumulator block, rounded to bf16, into its
@@ -179,11 +178,7 @@ void flce_gemm(const GemmArgs a) {
           for (int q = 0; q < 8; ++q) ls += fast_exp2((f[q] - m) * kLog2e);
         }
         const float s = row_sum(ls);
-        if (gm < a.M) {
-          if (c16 == 0) a.stats[gm * nparts + nt * 2 + wn] = make_float2(m, s);
-          const int64_t lab = a.labels[gm];
-          if (in && lab >= gc && lab < gc + 8) a.zlab[gm] = f[lab - gc];
-        }
+        if (gm < a.M && c16 == 0) a.stats[gm * nparts + nt * 2 + wn] = make_float2(m, s);
       }
     }
   }
@@ -200,10 +195,11 @@ __global__ __launch_bounds__(256) void flce_count(const int64_t* __restrict__ la
 }
 
 // Per row of a chunk (one wave per row): lse from the row's slice statistics
-// (contiguous [nparts] float2), loss = lse - z[label]. Fixed combination order:
-// lane-strided partial (max, sum) pairs, then a DPP/lane-read fold.
+// (contiguous [nparts] float2), loss = lse - z[label] with z[label] read from
+// the chunk's bf16 logits. Fixed combination order: lane-strided partial
+// (max, sum) pairs, then a DPP/lane-read fold.
 __global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stats, int64_t nparts,
-                                                 const float* __restrict__ zlab,
+                                                 const __bf16* __restrict__ logits, int64_t ldl,
                                                  const int64_t* __restrict__ labels, int64_t M,
                                                  int64_t V, int64_t ignore_index,
                                                  float* __restrict__ lse_out,
@@ -227,7 +223,7 @@ __global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stat
   float out;
   if (lab == ignore_index) out = 0.f;
   else if (lab < 0 || lab >= V) out = __builtin_nanf("");
-  else out = l - zlab[r];
+  else out = l - Elt<__bf16>::load1(logits + r * ldl + lab);
   lse_out[r] = l;
   loss_rows[r] = out;
 }
@@ -355,7 +351,7 @@ inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct Layout {
   int64_t chunk, nchunks, nparts;
-  size_t off_logits, off_stats, off_zlab, off_lse, off_rows, off_misc, off_acc, total;
+  size_t off_logits, off_stats, off_lse, off_rows, off_misc, off_acc, total;
 };
 
 Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
@@ -372,7 +368,6 @@ Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
   };
   l.off_logits = take((size_t)l.chunk * V * 2);
   l.off_stats = take((size_t)l.nparts * l.chunk * sizeof(float2));
-  l.off_zlab = take((size_t)N * 4);
   l.off_lse = take((size_t)N * 4);
   l.off_rows = take((size_t)N * 4);
   l.off_misc = take(64);
@@ -450,7 +445,6 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   __bf16* Lc = reinterpret_cast<__bf16*>(ws + lay.off_logits);
   float2* stats = reinterpret_cast<float2*>(ws + lay.off_stats);
-  float* zlab = reinterpret_cast<float*>(ws + lay.off_zlab);
   float* lse_ws = lse != nullptr ? lse : reinterpret_cast<float*>(ws + lay.off_lse);
   float* rows_ws = loss_rows != nullptr ? loss_rows : reinterpret_cast<float*>(ws + lay.off_rows);
   int* n_valid = reinterpret_cast<int*>(ws + lay.off_misc);
@@ -482,12 +476,10 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
     g.K = H;
     g.C = Lc;
     g.ldc = V;
-    g.labels = labels + r0;
     g.stats = stats;
-    g.zlab = zlab + r0;
     TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_gemm_logits"));
     hipLaunchKernelGGL(flce_rows, dim3((unsigned)((Mc + 3) / 4)), dim3(256), 0, st, stats,
-                       lay.nparts, zlab + r0, labels + r0, Mc, V, ignore_index, lse_ws + r0,
+                       lay.nparts, Lc, V, labels + r0, Mc, V, ignore_index, lse_ws + r0,
                        rows_ws + r0);
     TS_TRY(ts_host::check_launch("flce_rows"));
     if (!grads) continue;
