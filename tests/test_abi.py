@@ -146,3 +146,26 @@ def test_swiglu_validation(lib):
     assert lib.ts_swiglu_bwd(FAKE, FAKE, FAKE, FAKE, NULL, 16, 1, st) == INVALID
     assert lib.ts_swiglu_fwd(NULL, NULL, NULL, 0, 1, st) == TS_OK
     assert lib.ts_swiglu_bwd(NULL, NULL, NULL, NULL, NULL, 0, 1, st) == TS_OK
+
+
+def test_flce_validation(lib):
+    st = NULL
+    N, H, V = 64, 64, 128
+    ws = lib.ts_flce_workspace_size(N, H, V, 0, 1)
+    assert ws > 0 and lib.ts_flce_workspace_size(0, H, V, 0, 1) == 0
+
+    def call(ldh=H, ldw=H, n=N, h=H, v=V, reduction=0, loss=FAKE, wsb=ws, hidden=FAKE):
+        return lib.ts_flce_fwd_bwd(hidden, ldh, FAKE, ldw, FAKE, n, h, v, -100, reduction, loss,
+                                   NULL, NULL, FAKE, FAKE, 0, FAKE, wsb, st)
+
+    assert call(h=60, ldh=64, ldw=64) == SHAPE          # H not a multiple of 8
+    assert call(ldh=32) == SHAPE                        # row stride below H
+    assert call(ldh=72 + 4) == SHAPE                    # row stride not a multiple of 8
+    assert call(ldh=(1 << 22) + 8) == SHAPE             # offsets would leave 32 bits
+    assert b"row strides" in lib.ts_last_error()
+    assert call(ldw=(1 << 22) + 8) == SHAPE
+    assert call(v=(1 << 22) + 8) == SHAPE
+    assert call(reduction=2) == INVALID
+    assert call(loss=NULL) == INVALID
+    assert call(hidden=NULL) == INVALID
+    assert call(wsb=ws - 256) == WORKSPACE

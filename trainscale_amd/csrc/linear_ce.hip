@@ -416,9 +416,14 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
                 (long long)N, (long long)H, (long long)V);
   if (ldh < H || ldw < H || ldh % 8 != 0 || ldw % 8 != 0)
     return fail(TS_ERR_SHAPE, "flce: row strides must be >= H and multiples of 8");
-  // 32-bit buffer offsets per 256-row tile, and 64-row tile grids within 65535 in y
+  // Buffer offsets are 32-bit and must stay below 2^31: within a 256-row K-major tile
+  // (row * ld * 2 bytes, ld = ldh, ldw or V) and within a 32-row k-block of an MN-major
+  // operand (k * ld * 2, ld = ldh, ldw or V).
   if (V > ((int64_t)1 << 22) || H > ((int64_t)1 << 20) || N > ((int64_t)1 << 22))
     return fail(TS_ERR_SHAPE, "flce: shape beyond the kernel's index range");
+  if (ldh > ((int64_t)1 << 22) || ldw > ((int64_t)1 << 22))
+    return fail(TS_ERR_SHAPE, "flce: row strides beyond the kernel's index range (%lld, %lld)",
+                (long long)ldh, (long long)ldw);
   if (reduction != 0 && reduction != 1)
     return fail(TS_ERR_INVALID_ARGUMENT, "flce: reduction must be 0 (mean) or 1 (sum)");
   if (loss == nullptr) return fail(TS_ERR_INVALID_ARGUMENT, "flce: loss is NULL");
