@@ -4,9 +4,13 @@
 // and of the LM head [V, H]), 16-byte aligned, row strides and K multiples of
 // 8 elements.
 //
-// Workgroup tile 256 x 256, k-block 32, 256 threads = 4 waves in a 2 x 2 grid;
-// each wave owns a 128 x 128 block of C as 4 x 4 tiles of
-// v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane).
+// Workgroup tile 256 x 256, k-block 32. Two wave layouts (template kW):
+//   kW = 4: 256 threads in a 2 x 2 grid, each wave a 128 x 128 block of C as
+//           4 x 4 tiles of v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per
+//           lane), one wave per SIMD;
+//   kW = 8: 512 threads in a 4 x 2 grid, each wave a 64 x 128 block (2 x 4
+//           tiles, 128 accumulators), two waves per SIMD, so one wave's MFMAs
+//           can run while the other waits at the barrier or for LDS data.
 //
 // Operands go from HBM straight into LDS with buffer_load_dwordx4 ... lds
 // (no staging registers): a wave's load instruction fills 1 KiB of LDS, lane i
@@ -56,6 +60,7 @@ typedef __attribute__((address_space(3))) bf16x4* lds_bf16x4_t;
 // Storage of a GEMM operand: K-major (element (r, k) at r * ld + k) or
 // MN-major (element (r, k) at k * ld + r).
 enum Major : int { kKMajor = 0, kMNMajor = 1 };
+
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) uint32_t* lds_ptr_t;
@@ -68,16 +73,28 @@ constexpr int BK = 32;
 #endif
 constexpr int kStages = TS_GEMM_STAGES;  // LDS stages of 32 KiB
 static_assert(kStages >= 3 && kStages <= 5, "pipeline depth");
-constexpr int kThreads = 256;
 constexpr int kRowBytes = BK * 2;                       // 64
 constexpr int kTileBytes = BM * kRowBytes;              // 16 KiB per operand per stage
 constexpr int kStageBytes = 2 * kTileBytes;             // A + B
 constexpr size_t kLdsBytes = (size_t)kStages * kStageBytes;
-constexpr int kLoadsPerWave = BM * kRowBytes / 1024 / 4;      // 1 KiB loads per wave per operand
 constexpr uint32_t kOob = 0x80000000u;  // voffset beyond every resource's range -> reads 0
 
+// Wave layout: kW waves, wave wid owns rows [wm * RW, +RW) and columns
+// [wn * 128, +128) of the tile, wm = wid >> 1, wn = wid & 1.
+template <int kW>
+struct Cfg {
+  static_assert(kW == 4 || kW == 8, "wave layout");
+  static constexpr int kThreads = 64 * kW;
+  static constexpr int kLoads = 16 / kW;  // 1 KiB loads per wave per operand per k-block
+  static constexpr int kTI = 16 / kW;     // 32-row tiles per wave (4 or 2)
+  static constexpr int kTJ = 4;           // 32-column tiles per wave
+  static constexpr int RW = 32 * kTI;     // rows per wave
+  static constexpr int kMfma = kTI * kTJ; // MFMAs per k-step
+};
+
+template <int kTI>
 struct Acc {
-  f32x16 t[4][4];
+  f32x16 t[kTI][4];
 };
 
 __device__ void buffer_load_lds(i32x4 rsrc, lds_ptr_t lds, int size, int voffset, int soffset,
@@ -109,9 +126,10 @@ __device__ inline void wait_vmcnt() {
 __device__ inline int swz(int row, int c) { return c ^ ((row >> 2) & 3); }
 
 // Waits until at most `later` stages of this wave's loads are outstanding
-// (each stage is 2 * kLoadsPerWave loads; vmcnt counts loads in issue order).
+// (each stage is 2 * kLoads loads; vmcnt counts loads in issue order).
+template <int kW>
 __device__ inline void wait_stage(int64_t later) {
-  constexpr int kPer = 2 * kLoadsPerWave;
+  constexpr int kPer = 2 * Cfg<kW>::kLoads;
   static_assert(kPer * 3 < 64, "vmcnt range");
   if (later >= 3) wait_vmcnt<3 * kPer>();
   else if (later == 2) wait_vmcnt<2 * kPer>();
@@ -119,19 +137,21 @@ __device__ inline void wait_stage(int64_t later) {
   else wait_vmcnt<0>();
 }
 
-// Per-thread byte offsets (relative to the tile's first row) of this lane's
-// loads for logical chunk c of LDS row r: row * ld * 2 + chunk * 16.
+// K-major tile loads: rows [row0, row0 + 256) of a [nrows, ld] matrix,
+// out-of-range rows read zeros. Wave load u fills LDS rows
+// [(u * kW + wid) * 16, +16) (1 KiB); off[u] is this lane's byte offset
+// (relative to the tile's first row) of the logical chunk its LDS position
+// holds, at k0 = 0.
+template <int kW>
 struct TileLoader {
   i32x4 rsrc;
-  uint32_t off[kLoadsPerWave];  // byte offset of this lane's chunk at k0 = 0
-  int lds_row0;                 // first LDS row of the wave's first load
+  uint32_t off[Cfg<kW>::kLoads];
 };
 
-// Sets up the loads of one operand: rows [row0, row0 + 256) of a [nrows, ld]
-// matrix; out-of-range rows read zeros.
-__device__ inline TileLoader make_loader(const __bf16* g, int64_t ld, int64_t nrows,
-                                         int64_t row0) {
-  TileLoader t;
+template <int kW>
+__device__ inline TileLoader<kW> make_loader(const __bf16* g, int64_t ld, int64_t nrows,
+                                             int64_t row0) {
+  TileLoader<kW> t;
   const int wid = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   int64_t valid = nrows - row0;
@@ -139,26 +159,28 @@ __device__ inline TileLoader make_loader(const __bf16* g, int64_t ld, int64_t nr
   if (valid < 0) valid = 0;
   t.rsrc = make_rsrc(g + row0 * ld, (uint64_t)valid * (uint64_t)ld * 2);
 #pragma unroll
-  for (int u = 0; u < kLoadsPerWave; ++u) {
-    const int row = (u * 4 + wid) * 16 + (lane >> 2);
+  for (int u = 0; u < Cfg<kW>::kLoads; ++u) {
+    const int row = (u * kW + wid) * 16 + (lane >> 2);
     const int chunk = swz(row, lane & 3);  // the logical chunk LDS position lane&3 holds
     t.off[u] = (uint32_t)(row * ld * 2 + chunk * 16);
   }
-  t.lds_row0 = wid * 16;
   return t;
 }
 
 // Issues this wave's loads of k-block [k0, k0 + 32) into the LDS tile.
-__device__ inline void issue_loads(const TileLoader& t, int64_t k0, int64_t K, uint8_t* lds_tile) {
+template <int kW>
+__device__ inline void issue_loads(const TileLoader<kW>& t, int64_t k0, int64_t K,
+                                   uint8_t* lds_tile) {
   const int lane = threadIdx.x & 63;
+  const int wid = threadIdx.x >> 6;
 #pragma unroll
-  for (int u = 0; u < kLoadsPerWave; ++u) {
+  for (int u = 0; u < Cfg<kW>::kLoads; ++u) {
     // logical chunk of this lane for the load's row (same swizzle as make_loader)
-    const int row = (u * 4 + (threadIdx.x >> 6)) * 16 + (lane >> 2);
+    const int row = (u * kW + wid) * 16 + (lane >> 2);
     const int chunk = swz(row, lane & 3);
     const bool in_k = k0 + chunk * 8 < K;
     const uint32_t voff = in_k ? t.off[u] + (uint32_t)(k0 * 2) : kOob;
-    uint8_t* dst = lds_tile + (u * 4 + (threadIdx.x >> 6)) * 16 * kRowBytes;
+    uint8_t* dst = lds_tile + (u * kW + wid) * 16 * kRowBytes;
     buffer_load_lds(t.rsrc, (lds_ptr_t)dst, 16, (int)voff, 0, 0, 0);
   }
 }
@@ -170,27 +192,29 @@ __device__ inline void issue_loads(const TileLoader& t, int64_t k0, int64_t K, u
 // of 4 consecutive k-rows; the swizzle puts them in the 4 distinct 64-byte
 // quarters of a 256-byte bank window (XOR in 32-byte units instead measured
 // 8% of the kernel's cycles as bank conflicts per operand).
-// Wave load u covers LDS chunks [(4u + wid) * 64, +64): k-rows 2 (4u + wid)
-// and 2 (4u + wid) + 1.
+// Wave load u covers LDS chunks [(u * kW + wid) * 64, +64): k-rows
+// 2 (u * kW + wid) and 2 (u * kW + wid) + 1.
+template <int kW>
 struct TileLoaderT {
-  const __bf16* base;           // element (k = 0, r = r0)
-  int64_t ld;                   // elements between consecutive k
-  uint32_t off[kLoadsPerWave];  // byte offset within a k-block window, kOob past the rows
-  int kr[kLoadsPerWave];        // k-row (0..31) of this lane's chunk
+  const __bf16* base;              // element (k = 0, r = r0)
+  int64_t ld;                      // elements between consecutive k
+  uint32_t off[Cfg<kW>::kLoads];   // byte offset within a k-block window, kOob past the rows
+  int kr[Cfg<kW>::kLoads];         // k-row (0..31) of this lane's chunk
 };
 
 __device__ inline int swz_t(int kr) { return (kr & 3) << 6; }
 
-__device__ inline TileLoaderT make_loader_t(const __bf16* g, int64_t ld, int64_t nrows,
-                                            int64_t r0) {
-  TileLoaderT t;
+template <int kW>
+__device__ inline TileLoaderT<kW> make_loader_t(const __bf16* g, int64_t ld, int64_t nrows,
+                                                int64_t r0) {
+  TileLoaderT<kW> t;
   const int wid = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   t.base = g + r0;
   t.ld = ld;
 #pragma unroll
-  for (int u = 0; u < kLoadsPerWave; ++u) {
-    const int c = (u * 4 + wid) * 64 + lane;  // 16-byte LDS chunk of the tile
+  for (int u = 0; u < Cfg<kW>::kLoads; ++u) {
+    const int c = (u * kW + wid) * 64 + lane;  // 16-byte LDS chunk of the tile
     const int kr = c >> 5;
     const int lbyte = ((c & 31) << 4) ^ swz_t(kr);  // logical byte within the k-row
     const int64_t r = r0 + (lbyte >> 1);
@@ -203,35 +227,39 @@ __device__ inline TileLoaderT make_loader_t(const __bf16* g, int64_t ld, int64_t
 // Issues this wave's loads of k-block [k0, k0 + 32) into the LDS tile. The
 // buffer resource spans the k-block's 32 k-rows, so offsets stay 32-bit
 // whatever the operand's size.
-__device__ inline void issue_loads_t(const TileLoaderT& t, int64_t k0, int64_t K,
+template <int kW>
+__device__ inline void issue_loads_t(const TileLoaderT<kW>& t, int64_t k0, int64_t K,
                                      uint8_t* lds_tile) {
   const i32x4 rsrc = make_rsrc(t.base + k0 * t.ld, (uint64_t)BK * (uint64_t)t.ld * 2);
+  const int wid = threadIdx.x >> 6;
 #pragma unroll
-  for (int u = 0; u < kLoadsPerWave; ++u) {
+  for (int u = 0; u < Cfg<kW>::kLoads; ++u) {
     const uint32_t voff = k0 + t.kr[u] < K ? t.off[u] : kOob;
-    uint8_t* dst = lds_tile + (u * 4 + (threadIdx.x >> 6)) * 1024;
+    uint8_t* dst = lds_tile + (u * kW + wid) * 1024;
     buffer_load_lds(rsrc, (lds_ptr_t)dst, 16, (int)voff, 0, 0, 0);
   }
 }
 
-// Fragments (k-step ks) of four 32-row blocks starting at row r_base of a
+// Fragments (k-step ks) of kN 32-row blocks starting at row r_base of a
 // K-major tile: one ds_read_b128 each.
+template <int kN>
 __device__ inline void read_op_k(const uint8_t* Xs, int r_base, int lane, int ks, bf16x8* f) {
   const int r = lane & 31;
   const int c = ks * 2 + (lane >> 5);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kN; ++i) {
     const int row = r_base + i * 32 + r;
     f[i] = *reinterpret_cast<const bf16x8*>(Xs + row * kRowBytes + (swz(row, c) << 4));
   }
 }
 
 // The same fragments from an MN-major tile: two ds_read_b64_tr_b16 each.
+template <int kN>
 __device__ inline void read_op_t(const uint8_t* Xs, int r_base, int lane, int ks, bf16x8* f) {
   const int g = lane >> 4;
   const int sl = lane & 15;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kN; ++i) {
     const int r = r_base + i * 32 + 16 * (g & 1) + 4 * (sl & 3);
     bf16x4 h[2];
 #pragma unroll
@@ -244,53 +272,55 @@ __device__ inline void read_op_t(const uint8_t* Xs, int r_base, int lane, int ks
   }
 }
 
+template <int kTI>
 struct Frags {
-  bf16x8 a[4];
+  bf16x8 a[kTI];
   bf16x8 b[4];
 };
 
 // Loader of one operand of the given storage.
-template <int kMajor> struct OpLoader;
-template <> struct OpLoader<kKMajor> {
-  TileLoader t;
+template <int kMajor, int kW> struct OpLoader;
+template <int kW> struct OpLoader<kKMajor, kW> {
+  TileLoader<kW> t;
   __device__ inline OpLoader(const __bf16* g, int64_t ld, int64_t nrows, int64_t r0)
-      : t(make_loader(g, ld, nrows, r0)) {}
+      : t(make_loader<kW>(g, ld, nrows, r0)) {}
   __device__ inline void issue(int64_t k0, int64_t K, uint8_t* tile) const {
-    issue_loads(t, k0, K, tile);
+    issue_loads<kW>(t, k0, K, tile);
   }
 };
-template <> struct OpLoader<kMNMajor> {
-  TileLoaderT t;
+template <int kW> struct OpLoader<kMNMajor, kW> {
+  TileLoaderT<kW> t;
   __device__ inline OpLoader(const __bf16* g, int64_t ld, int64_t nrows, int64_t r0)
-      : t(make_loader_t(g, ld, nrows, r0)) {}
+      : t(make_loader_t<kW>(g, ld, nrows, r0)) {}
   __device__ inline void issue(int64_t k0, int64_t K, uint8_t* tile) const {
-    issue_loads_t(t, k0, K, tile);
+    issue_loads_t<kW>(t, k0, K, tile);
   }
 };
 
-template <int kMajor>
+template <int kMajor, int kN>
 __device__ inline void read_op(const uint8_t* Xs, int r_base, int lane, int ks, bf16x8* f) {
-  if constexpr (kMajor == kKMajor) read_op_k(Xs, r_base, lane, ks, f);
-  else read_op_t(Xs, r_base, lane, ks, f);
+  if constexpr (kMajor == kKMajor) read_op_k<kN>(Xs, r_base, lane, ks, f);
+  else read_op_t<kN>(Xs, r_base, lane, ks, f);
 }
 
 // Operand fragments of k-step ks (0 or 1) of a staged k-block.
-template <int kMA, int kMB>
+template <int kMA, int kMB, int kW>
 __device__ inline void read_frags(const uint8_t* As, const uint8_t* Bs, int wm, int wn, int lane,
-                                  int ks, Frags& f) {
-  read_op<kMA>(As, wm * 128, lane, ks, f.a);
-  read_op<kMB>(Bs, wn * 128, lane, ks, f.b);
+                                  int ks, Frags<Cfg<kW>::kTI>& f) {
+  read_op<kMA, Cfg<kW>::kTI>(As, wm * Cfg<kW>::RW, lane, ks, f.a);
+  read_op<kMB, 4>(Bs, wn * 128, lane, ks, f.b);
 }
 
 // LDS read instructions per k-step of read_frags.
-template <int kMA, int kMB>
+template <int kMA, int kMB, int kW>
 constexpr int lds_reads() {
-  return (kMA == kMNMajor ? 8 : 4) + (kMB == kMNMajor ? 8 : 4);
+  return (kMA == kMNMajor ? 2 : 1) * Cfg<kW>::kTI + (kMB == kMNMajor ? 2 : 1) * 4;
 }
 
-__device__ inline void mma_frags(const Frags& f, Acc& acc) {
+template <int kTI>
+__device__ inline void mma_frags(const Frags<kTI>& f, Acc<kTI>& acc) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kTI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       acc.t[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.t[i][j], 0, 0, 0);
@@ -301,59 +331,67 @@ __device__ inline void mma_frags(const Frags& f, Acc& acc) {
 // issue in the shadow of the first for free. These scheduling groups ask the
 // compiler for such an order (the grouped instructions are independent of
 // the MFMAs they sit between).
-//
 template <int kMask, int kCount>
 __device__ inline void sched_group() {
   if constexpr (kCount > 0) __builtin_amdgcn_sched_group_barrier(kMask, kCount, 0);
 }
 
-// 16 MFMAs, the first 8 each followed by kR / 8 LDS reads (kR = 8, 12 or 16
-// reads per k-step: two ds_read_b64_tr_b16 per fragment of an MN-major
-// operand).
-template <int kR, int... I>
+// kM MFMAs of a k-step, the first kM / 2 each followed by LDS reads (kR in
+// all: one ds_read_b128 per K-major fragment, two ds_read_b64_tr_b16 per
+// MN-major one).
+template <int kR, int kM, int... I>
 __device__ inline void sched_mfma_lds_impl(std::integer_sequence<int, I...>) {
-  ((sched_group<0x008, 1>(), sched_group<0x100, (kR + 7 - I) / 8>()), ...);  // MFMA, LDS reads
+  constexpr int kSlots = kM / 2;
+  ((sched_group<0x008, 1>(), sched_group<0x100, (kR + kSlots - 1 - I) / kSlots>()), ...);
 }
-template <int kR>
+template <int kR, int kM>
 __device__ inline void sched_mfma_lds() {
-  sched_mfma_lds_impl<kR>(std::make_integer_sequence<int, 8>());
-  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+  sched_mfma_lds_impl<kR, kM>(std::make_integer_sequence<int, kM / 2>());
+  __builtin_amdgcn_sched_group_barrier(0x008, kM / 2, 0);
 }
 
-// 16 - kPreBarrier MFMAs: 8 each followed by a global->LDS load, then the rest
-// each followed by LDS reads. K-major operands (8 reads): one read per slot,
-// the other two left to the scheduler, the order measured best; MN-major
-// operands: every read placed.
-constexpr int kPreBarrier = 2;  // MFMAs issued before the barrier (see mainloop)
-constexpr int kLdsSlots = 8 - kPreBarrier;
-template <int kR, int... I>
+// The kM - kPre MFMAs after the barrier: the first kV each followed by a
+// global->LDS load (kV = this wave's loads per k-block), the rest by LDS
+// reads. With 4 waves and K-major operands (8 reads): one read per slot,
+// the other two left to the scheduler, the order measured best; otherwise
+// every read placed.
+// MFMAs issued before the barrier (measured best: 2 with 4 waves; 1 with 8,
+// where 0 and 2 were 0.5-1.5% slower at C5).
+template <int kW>
+constexpr int pre_barrier() { return kW == 4 ? 2 : 1; }
+template <int kR, int kW, int... I>
 __device__ inline void sched_slots_impl(std::integer_sequence<int, I...>) {
+  constexpr int kSlots = sizeof...(I);
   ((sched_group<0x008, 1>(),
-    sched_group<0x100, kR == 8 ? 1 : (kR + kLdsSlots - 1 - I) / kLdsSlots>()),
+    sched_group<0x100, (kW == 4 && kR == 8) ? 1 : (kR + kSlots - 1 - I) / kSlots>()),
    ...);
 }
-template <int kR>
+template <int kR, int kW>
 __device__ inline void sched_mfma_vmem_lds() {
+  constexpr int kV = 2 * Cfg<kW>::kLoads;
+  constexpr int kSlots = Cfg<kW>::kMfma - pre_barrier<kW>() - kV;
+  static_assert(kSlots > 0, "schedule slots");
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kV; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (to LDS)
   }
-  sched_slots_impl<kR>(std::make_integer_sequence<int, kLdsSlots>());
+  sched_slots_impl<kR, kW>(std::make_integer_sequence<int, kSlots>());
 }
 
-// MFMA q (0..15) of a k-step: tile (q / 4, q % 4).
-__device__ inline void mma_one(const Frags& f, Acc& acc, int q) {
+// MFMA q (0..kTI*4-1) of a k-step: tile (q / 4, q % 4).
+template <int kTI>
+__device__ inline void mma_one(const Frags<kTI>& f, Acc<kTI>& acc, int q) {
   acc.t[q / 4][q % 4] =
       __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[q / 4], f.b[q % 4], acc.t[q / 4][q % 4], 0, 0, 0);
 }
 
 // Main loop for the tile at (m0, n0). `smem` holds kLdsBytes (16-byte aligned).
 //
-// Steady state, per k-block kt (two 16-deep k-steps, 16 MFMAs each):
+// Steady state, per k-block kt (two 16-deep k-steps):
 //   MFMAs (kt, 0), interleaved with the LDS reads of fragments (kt, 1)
-//   kPreBarrier MFMAs of (kt, 1), so the matrix core stays busy while the
-//   wave waits for stage kt+1 and the workgroup barrier
+//   kPre MFMAs of (kt, 1), so the matrix core stays busy while the wave
+//   waits for stage kt+1 and the workgroup barrier
 //   the other MFMAs of (kt, 1), interleaved with the global->LDS loads of
 //   stage kt+3 (into the buffer of stage kt-1, which every wave finished
 //   reading before the barrier) and the LDS reads of fragments (kt+1, 0)
@@ -362,27 +400,29 @@ __device__ inline void mma_one(const Frags& f, Acc& acc, int q) {
 // branches (a branch there splits the interleaved block and makes the
 // register allocator shuffle the accumulators).
 //
-// Measured at 8192 x 128256 x 4096 (main loop only, on MI355X): 1446
+// Measured at 8192 x 128256 x 4096 (main loop only, on MI355X, 4 waves): 1446
 // TFLOP/s, against 1219 TFLOP/s with the LDS reads and loads issued in
 // blocks between the MFMA groups.
-template <int kMA, int kMB>
+template <int kMA, int kMB, int kW>
 __device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64_t M,
                                 const __bf16* __restrict__ B, int64_t ldb, int64_t N, int64_t K,
-                                int64_t m0, int64_t n0, uint8_t* smem, Acc& acc) {
-  constexpr int kR = lds_reads<kMA, kMB>();
+                                int64_t m0, int64_t n0, uint8_t* smem, Acc<Cfg<kW>::kTI>& acc) {
+  using C = Cfg<kW>;
+  constexpr int kR = lds_reads<kMA, kMB, kW>();
+  constexpr int kPre = pre_barrier<kW>();
   const int wid = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wm = wid >> 1;
   const int wn = wid & 1;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < C::kTI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc.t[i][j][e] = 0.f;
 
-  const OpLoader<kMA> la(A, lda, M, m0);
-  const OpLoader<kMB> lb(B, ldb, N, n0);
+  const OpLoader<kMA, kW> la(A, lda, M, m0);
+  const OpLoader<kMB, kW> lb(B, ldb, N, n0);
   const int64_t KT = (K + BK - 1) / BK;
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s) {
@@ -392,59 +432,53 @@ __device__ inline void mainloop(const __bf16* __restrict__ A, int64_t lda, int64
     }
   }
   // stage 0 landed (stages 1 .. kStages-2 may still be in flight)
-  wait_stage(KT - 1 < kStages - 2 ? KT - 1 : kStages - 2);
+  wait_stage<kW>(KT - 1 < kStages - 2 ? KT - 1 : kStages - 2);
   __builtin_amdgcn_s_barrier();
-  Frags f0, f1;
-  read_frags<kMA, kMB>(smem, smem + kTileBytes, wm, wn, lane, 0, f0);
+  Frags<C::kTI> f0, f1;
+  read_frags<kMA, kMB, kW>(smem, smem + kTileBytes, wm, wn, lane, 0, f0);
 
   int64_t kt = 0;
   for (; kt + kStages - 1 < KT; ++kt) {
     const uint8_t* As = smem + (kt % kStages) * kStageBytes;
-    read_frags<kMA, kMB>(As, As + kTileBytes, wm, wn, lane, 1, f1);
+    read_frags<kMA, kMB, kW>(As, As + kTileBytes, wm, wn, lane, 1, f1);
     mma_frags(f0, acc);
-    sched_mfma_lds<kR>();
+    sched_mfma_lds<kR, C::kMfma>();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < kPreBarrier; ++q) mma_one(f1, acc, q);
+    for (int q = 0; q < kPre; ++q) mma_one(f1, acc, q);
     __builtin_amdgcn_sched_barrier(0);
     // stage kt+1 landed: stages kt+2 .. kt+kStages-2 may remain in flight
-    wait_stage(kStages - 3);
+    wait_stage<kW>(kStages - 3);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     const int s = (int)((kt + kStages - 1) % kStages);
     la.issue((kt + kStages - 1) * BK, K, smem + s * kStageBytes);
     lb.issue((kt + kStages - 1) * BK, K, smem + s * kStageBytes + kTileBytes);
     const uint8_t* An = smem + ((kt + 1) % kStages) * kStageBytes;
-    read_frags<kMA, kMB>(An, An + kTileBytes, wm, wn, lane, 0, f0);
+    read_frags<kMA, kMB, kW>(An, An + kTileBytes, wm, wn, lane, 0, f0);
 #pragma unroll
-    for (int q = kPreBarrier; q < 16; ++q) mma_one(f1, acc, q);
-    sched_mfma_vmem_lds<kR>();
+    for (int q = kPre; q < C::kMfma; ++q) mma_one(f1, acc, q);
+    sched_mfma_vmem_lds<kR, kW>();
     __builtin_amdgcn_sched_barrier(0);
   }
   // drain: the last k-blocks, no loads left to issue
   for (; kt < KT; ++kt) {
     const uint8_t* As = smem + (kt % kStages) * kStageBytes;
-    read_frags<kMA, kMB>(As, As + kTileBytes, wm, wn, lane, 1, f1);
+    read_frags<kMA, kMB, kW>(As, As + kTileBytes, wm, wn, lane, 1, f1);
     __builtin_amdgcn_sched_barrier(0);
     mma_frags(f0, acc);
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < KT) {
       const int64_t later = KT - 2 - kt;
-      wait_stage(later < kStages - 3 ? later : kStages - 3);
+      wait_stage<kW>(later < kStages - 3 ? later : kStages - 3);
       __builtin_amdgcn_s_barrier();
       const uint8_t* An = smem + ((kt + 1) % kStages) * kStageBytes;
-      read_frags<kMA, kMB>(An, An + kTileBytes, wm, wn, lane, 0, f0);
+      read_frags<kMA, kMB, kW>(An, An + kTileBytes, wm, wn, lane, 0, f0);
     }
     __builtin_amdgcn_sched_barrier(0);
     mma_frags(f1, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
 }
-
-// Row / column (within the workgroup tile) of accumulator element e of tile (i, j).
-__device__ inline int acc_row(int wm, int i, int e, int lane) {
-  return wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-}
-__device__ inline int acc_col(int wn, int j, int lane) { return wn * 128 + j * 32 + (lane & 31); }
 
 }  // namespace ts_gemm

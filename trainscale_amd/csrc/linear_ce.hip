@@ -63,11 +63,12 @@ struct GemmArgs {
   float2* stats;          // [M][2 * NT] (max, sum exp) per 128-column slice
 };
 
-// Writes the wave's 128 x 128 accumulator block, rounded to bf16, into its
-// private 32 KiB LDS region as [row][col] with 256-byte rows.
-__device__ inline void stage_bf16(const Acc& acc, uint8_t* region, int lane) {
+// Writes the wave's RW x 128 accumulator block (RW = 32 * kTI), rounded to
+// bf16, into its private LDS region as [row][col] with 256-byte rows.
+template <int kTI>
+__device__ inline void stage_bf16(const Acc<kTI>& acc, uint8_t* region, int lane) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kTI; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -78,25 +79,28 @@ __device__ inline void stage_bf16(const Acc& acc, uint8_t* region, int lane) {
       }
 }
 
-// Writes rows [64 * half, 64 * half + 64) of the wave's 128 x 128 fp32
-// accumulator block into its private 32 KiB LDS region as [row][col] fp32
-// with 512-byte rows (accumulator tiles i = 2 * half, 2 * half + 1).
-__device__ inline void stage_f32_half(const Acc& acc, int half, uint8_t* region, int lane) {
+// Writes rows [32 i, 32 i + 32) of the wave's fp32 accumulator block (tile
+// row i) into its private LDS region as [row][col] fp32 with 512-byte rows
+// (16 KiB).
+template <int kTI>
+__device__ inline void stage_f32_tile(const Acc<kTI>& acc, int i, uint8_t* region, int lane) {
 #pragma unroll
-  for (int ii = 0; ii < 2; ++ii)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = ii * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int col = j * 32 + (lane & 31);
-        *reinterpret_cast<float*>(region + row * 512 + col * 4) = acc.t[2 * half + ii][j][e];
-      }
+    for (int e = 0; e < 16; ++e) {
+      const int row = 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      const int col = j * 32 + (lane & 31);
+      *reinterpret_cast<float*>(region + row * 512 + col * 4) = acc.t[i][j][e];
+    }
 }
 
-template <int kMode, int kMA, int kMB>
-__global__ __launch_bounds__(ts_gemm::kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// One 256 x 256 tile of C = A B^T with kW waves (ts_gemm::Cfg) and the
+// epilogue of kMode.
+template <int kMode, int kMA, int kMB, int kW>
+__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(kW / 4, kW / 4)))
 void flce_gemm(const GemmArgs a) {
+  using Cw = ts_gemm::Cfg<kW>;
+  constexpr int kTI = Cw::kTI;
   __shared__ __attribute__((aligned(16))) uint8_t smem[ts_gemm::kLdsBytes];
   const int64_t MT = (a.M + BM - 1) / BM;
   const int64_t NT = (a.N + BN - 1) / BN;
@@ -104,31 +108,34 @@ void flce_gemm(const GemmArgs a) {
   ts_plan::gemm_tile_of(blockIdx.x, MT, NT, mt, nt);
   const int64_t m0 = mt * BM;
   const int64_t n0 = nt * BN;
-  Acc acc;
-  ts_gemm::mainloop<kMA, kMB>(a.A, a.lda, a.M, a.B, a.ldb, a.N, a.K, m0, n0, smem, acc);
+  Acc<kTI> acc;
+  ts_gemm::mainloop<kMA, kMB, kW>(a.A, a.lda, a.M, a.B, a.ldb, a.N, a.K, m0, n0, smem, acc);
 
   const int wid = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wm = wid >> 1;
   const int wn = wid & 1;
-  const int64_t mb = m0 + wm * 128;  // first row of this wave's block
-  const int64_t nb = n0 + wn * 128;  // first column
+  const int64_t mb = m0 + wm * Cw::RW;  // first row of this wave's block
+  const int64_t nb = n0 + wn * 128;     // first column
   // Every wave is done with the pipeline's LDS before it is reused. Each wave
-  // then works in its own 32 KiB region; LDS operations of one wave complete
-  // in order, so it reads back its own writes without a barrier.
+  // then works in its own region (kLdsBytes / kW: 32 KiB with 4 waves, 16 KiB
+  // with 8); LDS operations of one wave complete in order, so it reads back
+  // its own writes without a barrier.
+  constexpr int kRegion = (int)(ts_gemm::kLdsBytes / kW);
+  static_assert(kRegion >= Cw::RW * kStagePitch && kRegion >= 32 * 512, "epilogue region");
   __syncthreads();
-  uint8_t* region = smem + wid * 32768;
+  uint8_t* region = smem + wid * kRegion;
 
   if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32 || kMode == kEpiAccBf16) {
     // fp32 C32 rows of 128 columns = 512 B: 32 lanes x 16 B per row, 2 rows per step
     const int c4 = lane & 31;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      stage_f32_half(acc, half, region, lane);
+    for (int i = 0; i < kTI; ++i) {
+      stage_f32_tile(acc, i, region, lane);
 #pragma unroll 4
-      for (int it = 0; it < 32; ++it) {
+      for (int it = 0; it < 16; ++it) {
         const int lrow = it * 2 + (lane >> 5);
-        const int64_t gm = mb + half * 64 + lrow;
+        const int64_t gm = mb + i * 32 + lrow;
         const int64_t gc = nb + c4 * 4;
         if (gm < a.M && gc < a.N) {  // N % 8 == 0: 4 columns are all in or all out
           float4 v = *reinterpret_cast<const float4*>(region + lrow * 512 + c4 * 16);
@@ -158,7 +165,7 @@ void flce_gemm(const GemmArgs a) {
     const int c16 = lane & 15;  // 16-byte chunk of the 256-byte row
     const int64_t nparts = 2 * ((a.N + BN - 1) / BN);
 #pragma unroll 4
-    for (int it = 0; it < 32; ++it) {
+    for (int it = 0; it < Cw::RW / 4; ++it) {
       const int lrow = it * 4 + (lane >> 4);
       const int64_t gm = mb + lrow;
       const int64_t gc = nb + c16 * 8;
@@ -376,13 +383,19 @@ Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
   return l;
 }
 
+// The GEMMs run with 8 waves (two per SIMD): measured on MI355X at C5 against
+// the 4-wave layout, logits 7.59 vs 7.88 ms, grad_hidden 6.96 vs 7.12 ms,
+// grad_weight 6.93 vs 7.19 ms, bit-identical results. The matrix cores are busier
+// per clock (69-76% against 58-67%); the box's clock under this load drops to
+// 1.55-1.6 GHz from 1.75-1.85, which takes back part of the gain.
 template <int kMode, int kMA = ts_gemm::kKMajor, int kMB = ts_gemm::kKMajor>
 ts_status launch_gemm(const GemmArgs& a, hipStream_t st, const char* name) {
+  constexpr int kW = 8;
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return TS_OK;
   if (tiles > 0x7fffffffLL) return ts_host::fail(TS_ERR_SHAPE, "%s: too many tiles", name);
-  hipLaunchKernelGGL((flce_gemm<kMode, kMA, kMB>), dim3((unsigned)tiles),
-                     dim3(ts_gemm::kThreads), 0, st, a);
+  hipLaunchKernelGGL((flce_gemm<kMode, kMA, kMB, kW>), dim3((unsigned)tiles),
+                     dim3(ts_gemm::Cfg<kW>::kThreads), 0, st, a);
   return ts_host::check_launch(name);
 }
 
