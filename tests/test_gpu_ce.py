@@ -201,6 +201,99 @@ def test_fused_fwd_bwd_matches_oracle(gpu, V, dtype):
         assert max_ulp_gpu(grad, g2) <= 1
 
 
+def extreme_rows(V, dtype, device):
+    """Rows that push the lse fold off its fast path, with labels on finite values.
+
+    0 plain; 1 every lane's first vector -inf; 2 half the values -inf at random;
+    3 one value 100 above the rest (overflows a sum taken against an earlier
+    reference); 4 values near -300 behind a -inf band (a sum against 0
+    underflows); 5 -inf except two values; 6 values near 100; 7 ignored, all -inf.
+    """
+    g = torch.Generator().manual_seed(V)
+    x = 2 * torch.randn(8, V, generator=g)
+    band = min(8192, V // 2)
+    hi = torch.randint(V // 2, V, (8,), generator=g)
+    x[1, :band] = -math.inf
+    x[2][torch.rand(V, generator=g) < 0.5] = -math.inf
+    x[2, hi[2]] = 1.5
+    x[3, (3 * V) // 5] = 100.0
+    x[4] += -300.0
+    x[4, :band] = -math.inf
+    x[5] = -math.inf
+    x[5, hi[5]] = 3.0
+    x[5, (hi[5] + 1) % V] = 1.0
+    x[6] += 100.0
+    x[7] = -math.inf
+    labels = hi.clone()
+    labels[7] = -100
+    return x.to(dtype).to(device), labels.to(device)
+
+
+def assert_loss_close(loss, lse, ref, ref_lse, valid):
+    """loss within 1e-5 relative, plus the fp32 resolution of lse - z at the row's lse."""
+    loss, lse = loss.cpu().double(), lse.cpu().double()
+    ref, ref_lse = ref.double(), ref_lse.double()
+    slack = 4 * 2.0 ** -23 * ref_lse.abs().clamp(min=1.0)
+    bad = (loss - ref).abs() > 1e-5 * ref.abs() + slack
+    assert not bool(bad.any()), (loss, ref)
+    assert bool(((lse - ref_lse).abs()[valid] <= 2 * slack[valid]).all()), (lse, ref_lse)
+
+
+@pytest.mark.parametrize("schedule", ["fused", "two_pass"])
+@pytest.mark.parametrize("V,dtype", [(128256, BF), (4096, BF), (1000, BF), (50257, BF),
+                                     (128256, torch.float32)])
+def test_extreme_logits(gpu, schedule, V, dtype):
+    """-inf entries (masked vocab), offsets far from 0 and a value far above its
+    neighbours give the oracle's loss and gradient; before the lse fold treated an
+    all -inf first vector, these rows came out NaN."""
+    x, labels = extreme_rows(V, dtype, gpu)
+    n = x.shape[0]
+    dl = torch.full((n,), 0.125, device=gpu)
+    if schedule == "fused":
+        loss, lse, grad = ops.ce_forward_backward(x, V, labels, dl)
+    else:
+        loss, lse = ops.ce_forward(x, V, labels)
+        grad = torch.empty_like(x)
+        ops.ce_backward(x, V, labels, lse, dl, grad, V)
+    ref, ref_lse = oracle.ce_fwd(x.cpu(), labels.cpu())
+    valid = (labels != -100).cpu()
+    assert torch.isfinite(loss).all() and torch.isfinite(grad.float()).all()
+    assert_loss_close(loss, lse, ref, ref_lse, valid)
+    # Row 7 is ignored: zeros, as the reference kernel writes without reading the
+    # row (the eager softmax of an all -inf row would be NaN times 0).
+    assert torch.count_nonzero(grad[7]) == 0
+    ref_g = oracle.ce_bwd(x[:7].cpu(), labels[:7].cpu(), dl[:7].cpu())
+    if dtype == torch.float32:
+        torch.testing.assert_close(grad[:7].cpu(), ref_g, rtol=2e-5, atol=1e-9)
+    else:
+        assert_ulp(grad[:7], ref_g, 1, tiny=TINY, what="grad")
+
+
+@pytest.mark.parametrize("schedule", ["fused", "two_pass"])
+def test_nan_logit_poisons_its_row_only(gpu, schedule):
+    V = 4096
+    torch.manual_seed(9)
+    x = (2 * torch.randn(4, V, device=gpu)).to(BF)
+    x[1, 77] = math.nan
+    x[3, 5] = math.nan
+    labels = torch.tensor([10, 20, 30, -100], device=gpu)
+    dl = torch.full((4,), 0.25, device=gpu)
+    if schedule == "fused":
+        loss, lse, grad = ops.ce_forward_backward(x, V, labels, dl)
+    else:
+        loss, lse = ops.ce_forward(x, V, labels)
+        grad = torch.empty_like(x)
+        ops.ce_backward(x, V, labels, lse, dl, grad, V)
+    ref, _ = oracle.ce_fwd(x.cpu(), labels.cpu())
+    assert torch.isnan(loss[1]) and torch.isnan(ref[1])
+    assert bool(torch.isnan(grad[1].float()).all())
+    keep = torch.tensor([0, 2, 3])
+    torch.testing.assert_close(loss.cpu()[keep], ref[keep], rtol=1e-5, atol=1e-6)
+    ref_g = oracle.ce_bwd(x.cpu()[keep], labels.cpu()[keep], dl.cpu()[keep])
+    assert_ulp(grad[keep.to(gpu)], ref_g, 1, tiny=TINY, what="grad")
+    assert torch.count_nonzero(grad[3]) == 0
+
+
 def max_ulp_gpu(a, b):
     from helpers import max_ulp
     return max_ulp(a.cpu(), b.cpu())

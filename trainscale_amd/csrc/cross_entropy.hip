@@ -120,7 +120,8 @@ __global__ __launch_bounds__(kThreads) void ce_fwd_vec(const T* __restrict__ log
       s = s == 0.f ? 0.f : s * fast_exp2((m - lm) * kLog2e);
       m = lm;
     }
-    const float mb = m * kLog2e;
+    // m is -inf only while every value seen is -inf: their terms are 0.
+    const float mb = m == -INFINITY ? 0.f : m * kLog2e;
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
@@ -141,7 +142,8 @@ __global__ __launch_bounds__(kThreads) void ce_fwd_vec(const T* __restrict__ log
       s = s == 0.f ? 0.f : s * fast_exp2((m - lm) * kLog2e);
       m = lm;
     }
-    const float mb = m * kLog2e;
+    // m is -inf only while every value seen is -inf: their terms are 0.
+    const float mb = m == -INFINITY ? 0.f : m * kLog2e;
 #pragma unroll
     for (int i = 0; i < VE; ++i) s += fast_exp2(__builtin_fmaf(z[i], kLog2e, -mb));
   }
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void ce_fwd_generic(
       s = s == 0.f ? 0.f : s * fast_exp2((m - z) * kLog2e);
       m = z;
     }
-    s += fast_exp2((z - m) * kLog2e);
+    s += z == -INFINITY ? 0.f : fast_exp2((z - m) * kLog2e);
   }
   block_fold(m, s, sz, lds);
   if (threadIdx.x == 0) {
@@ -413,32 +415,69 @@ __global__ __launch_bounds__(kFusedThreads) void ce_fused_vec(
   u32x4 buf[kFusedKv];
 #pragma unroll
   for (int k = 0; k < kFusedKv; ++k) buf[k] = buf_ld16_stream(xi, fused_voff(k, nvec, 16));
-  float m = -INFINITY, s = 0.f, sz = 0.f;
-  // Folds one vector into (m, s): one rescale of the running sum per vector.
-  auto fold = [&](const u32x4& q) {
-    float z[VE];
+  // Each lane sums exp(z - m) over its vectors against one reference m, the
+  // largest value of its first vector (0 if that vector is all -inf): per
+  // element one unpack, one FMA, one exp and one add, with no running max or
+  // rescale. The sum is exact (terms that underflow lie below the resolution
+  // of a sum that holds exp(0) = 1) unless it ends outside [0.5, inf): a
+  // value more than 88 above m overflowed it, a NaN reached it, or an all
+  // -inf first vector left a sum of values far below 0. Such a lane (only
+  // with extreme logits) folds its vectors again from the registers with an
+  // exact online max and rescale. Lanes without vectors keep m = -inf, s = 0.
+  float m = -INFINITY, mb = 0.f, s = 0.f, sz = 0.f;
+  auto sum_exp = [&](const float (&z)[VE], float bias) {
+    float cs = fast_exp2(__builtin_fmaf(z[0], kLog2e, -bias));
+#pragma unroll
+    for (int i = 1; i < VE; ++i) cs += fast_exp2(__builtin_fmaf(z[i], kLog2e, -bias));
+    return cs;
+  };
+  auto values = [&](const u32x4& q, float (&z)[VE]) {
     Elt<T>::unpack(q, z);
 #pragma unroll
-    for (int i = 0; i < VE; ++i) {
-      z[i] = xform<kXform>(z[i], xf);
-      if constexpr (kSmooth) sz += z[i];
-    }
+    for (int i = 0; i < VE; ++i) z[i] = xform<kXform>(z[i], xf);
+  };
+  auto vmax = [&](const float (&z)[VE]) {
     float cm = z[0];
 #pragma unroll
     for (int i = 1; i < VE; ++i) cm = __builtin_fmaxf(cm, z[i]);
-    const float mn = __builtin_fmaxf(m, cm), mb = mn * kLog2e;
-    float cs = fast_exp2(__builtin_fmaf(z[0], kLog2e, -mb));
+    return cm;
+  };
+  auto fold = [&](const u32x4& q, bool first) {
+    float z[VE];
+    values(q, z);
+    if constexpr (kSmooth) {
 #pragma unroll
-    for (int i = 1; i < VE; ++i) cs += fast_exp2(__builtin_fmaf(z[i], kLog2e, -mb));
-    s = (s == 0.f ? 0.f : s * fast_exp2((m - mn) * kLog2e)) + cs;
-    m = mn;
+      for (int i = 0; i < VE; ++i) sz += z[i];
+    }
+    if (first) {
+      const float cm = vmax(z);
+      m = cm == -INFINITY ? 0.f : cm;
+      mb = m * kLog2e;
+    }
+    s += sum_exp(z, mb);
   };
 #pragma unroll
   for (int k = 0; k < kFusedKv; ++k) {
     // Vectors every thread holds take a uniform branch; only the row's last
     // partial sweep tests each lane.
-    if ((k + 1) * kFusedThreads <= nvec) fold(buf[k]);
-    else if (threadIdx.x + k * kFusedThreads < nvec) fold(buf[k]);
+    if ((k + 1) * kFusedThreads <= nvec) fold(buf[k], k == 0);
+    else if (threadIdx.x + k * kFusedThreads < nvec) fold(buf[k], k == 0);
+  }
+  if ((int)threadIdx.x < nvec && !(s >= 0.5f && s < INFINITY)) {
+    m = -INFINITY;
+    s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kFusedKv; ++k) {
+      if ((int)threadIdx.x + k * kFusedThreads < nvec) {
+        float z[VE];
+        values(buf[k], z);
+        const float mn = __builtin_fmaxf(m, vmax(z));
+        if (mn != -INFINITY) {
+          s = (s == 0.f ? 0.f : s * fast_exp2((m - mn) * kLog2e)) + sum_exp(z, mn * kLog2e);
+          m = mn;
+        }
+      }
+    }
   }
   const float l = fused_lse<kSmooth>(m, s, sz, lds);
   // The gradient pass re-unpacks the stored vectors; this keeps the compiler
