@@ -388,9 +388,9 @@ def main():
         "rmsnorm_fwd": bytes_c1["fwd"], "rope_fwd": bytes_c2["fwd"], "ce_fwd_bwd": bytes_c3,
         "ce_bwd_scale": 4, "rope_bwd": bytes_c2["bwd"], "rmsnorm_bwd": bytes_c1["bwd"],
     }
-    kernel_names = {"rmsnorm_fwd": "rms_fwd_reg", "rope_fwd": "rope_vec_kernel",
+    kernel_names = {"rmsnorm_fwd": "rms_fwd_reg", "rope_fwd": "rope_tok_kernel",
                     "ce_fwd_bwd": "ce_fused_vec", "ce_bwd_scale": "scale_inplace",
-                    "rope_bwd": "rope_vec_kernel", "rmsnorm_bwd": "rms_bwd_reg+rms_dw_reduce4"}
+                    "rope_bwd": "rope_tok_kernel", "rmsnorm_bwd": "rms_bwd_reg+rms_dw_reduce4"}
     step_bytes = sum(op_bytes.values())
     order = list(op_bytes)
     state = {}

@@ -141,6 +141,50 @@ def test_layouts_and_dtypes(gpu, D, il, dtype):
     assert_rope(y, x, cos, sin, oracle.rope_positions(B, S, position_offset=5), il)
 
 
+@pytest.mark.parametrize("D,dtype,il,hq,hk", [
+    (128, BF, False, 32, 8), (128, BF, True, 32, 8), (128, torch.float32, False, 16, 4),
+    (64, torch.float16, False, 60, 4), (256, BF, False, 8, 8), (128, BF, False, 128, 8)])
+def test_one_token_per_workgroup_shapes(gpu, D, dtype, il, hq, hk):
+    """Tokens of >= 256 vector tasks (the attention shapes) run one token per
+    workgroup: Q and K together with both directions, a strided Q view, B > 1 with
+    a ragged S, position ids in register with a scaling factor, out-of-range table
+    positions, and a token wider than one pass of its workgroup (128 + 8 heads of
+    128 = 1088 tasks)."""
+    torch.manual_seed(D + hq)
+    B, S = 3, 37
+    q = torch.randn(B, S, hq, D, device=gpu).to(dtype)
+    k = torch.randn(B, S, hk, D, device=gpu).to(dtype)
+    dq, dk = torch.randn_like(q), torch.randn_like(k)
+    cos, sin = oracle.rope_tables(D, S, 10000.0)
+    pos = oracle.rope_positions(B, S)
+    qg, kg = q.clone().requires_grad_(), k.clone().requires_grad_()
+    qo, ko = Fast_RoPE.apply(qg, kg, cos.to(gpu), sin.to(gpu), il)
+    torch.autograd.backward([qo, ko], [dq, dk])
+    assert_rope(qo, q, cos, sin, pos, il, what="q")
+    assert_rope(ko, k, cos, sin, pos, il, what="k")
+    assert_rope(qg.grad, dq, cos, sin, pos, il, backward=True, what="dq")
+    assert_rope(kg.grad, dk, cos, sin, pos, il, backward=True, what="dk")
+    # strided view: Q heads inside a fused [B, S, hq + 2 hk, D] projection
+    qkv = torch.randn(B, S, hq + 2 * hk, D, device=gpu).to(dtype)
+    qv = qkv[:, :, :hq]
+    y = apply_rope(qv, cos.to(gpu), sin.to(gpu), interleaved=il, inplace=False)
+    assert_rope(y, qv.contiguous(), cos, sin, pos, il, what="strided")
+    # in-register, position ids (a permutation per row), scaling factor 2
+    x = torch.cat([q, k], 2).contiguous()
+    pid = torch.stack([torch.randperm(S) for _ in range(B)]).to(gpu)
+    y = apply_rope_theta(x, 10000.0, position_ids=pid, interleaved=il, inplace=False,
+                         scaling_factor=2.0)
+    c2, s2 = oracle.rope_tables(D, S, 10000.0, pos_div=2.0)
+    assert_rope(y, x, c2, s2, oracle.rope_positions(B, S, pid.cpu()), il, what="theta")
+    # table positions beyond the table give NaN for that token only
+    bad = pid.clone()
+    bad[1, 5] = S + 3
+    y = apply_rope(x, cos.to(gpu), sin.to(gpu), position_ids=bad, interleaved=il,
+                   inplace=False).float()
+    assert torch.isnan(y[1, 5]).all()
+    assert not torch.isnan(y[1, :5]).any() and not torch.isnan(y[0]).any()
+
+
 def test_bf16_tables_rotary_embedding(gpu):
     torch.manual_seed(3)
     rot = RotaryEmbedding(128, max_seq_len=512, base=500000.0)

@@ -126,6 +126,29 @@ int main() {
     }
     if (nmax) CHECK(magic_div((unsigned)(nmax - 1), mg) == (nmax - 1) / d, "magic edge %u", d);
   }
+  // 64-bit magic-number division (RoPE token split): exact wherever admitted
+  {
+    const unsigned long long ds[] = {1, 2, 3, 7, 2048, 4095, 4096, 4097, 131071, 1000003,
+                                     (1ull << 31) - 1, (1ull << 32) + 15, (1ull << 40) - 3};
+    for (unsigned long long d : ds) {
+      const unsigned long long mg = magic64_for(d);
+      // largest admitted n: n * d < 2^64
+      const unsigned long long nmax = d == 1 ? ~0ull : (~0ull) / d;
+      CHECK(magic64_exact(nmax, d) || d == 1, "magic64 bound %llu", d);
+      const unsigned long long probes[] = {0, 1, d - 1, d, d + 1, 2 * d - 1, 2 * d,
+                                           nmax / 3, nmax / 2, nmax - 1, nmax};
+      for (unsigned long long n : probes) {
+        if (d > 1 && !magic64_exact(n, d)) continue;
+        CHECK(magic64_div(n, mg) == n / d, "magic64 %llu/%llu", n, d);
+      }
+      for (unsigned long long q = 1; q < 2000 && d > 1; q += 7) {  // both sides of multiples
+        const unsigned __int128 nn = (unsigned __int128)q * d;
+        if (nn >= nmax) break;
+        const unsigned long long n = (unsigned long long)nn;
+        CHECK(magic64_div(n, mg) == q && magic64_div(n - 1, mg) == q - 1, "magic64 edge %llu*%llu", q, d);
+      }
+    }
+  }
   std::printf("%d failures\n", fails);
   return fails != 0;
 }

@@ -167,6 +167,20 @@ inline uint32_t magic_div(uint32_t n, uint32_t magic) {
 }
 inline bool magic_exact(uint64_t n_max, uint64_t d) { return n_max * d < ((uint64_t)1 << 32); }
 
+// The same rule one size up, for the RoPE token -> (batch, position) split:
+// q = mulhi64(n, ceil(2^64 / d)) equals n / d whenever n * d < 2^64 and d > 1
+// (with m = (2^64 + e) / d, 0 <= e < d, the error term n * e / (d * 2^64)
+// stays below 1 / d, which cannot carry floor(n / d) over an integer).
+inline uint64_t magic64_for(uint64_t d) {
+  return d <= 1 ? 0u : (uint64_t)((((unsigned __int128)1 << 64) + d - 1) / d);
+}
+inline uint64_t magic64_div(uint64_t n, uint64_t magic) {
+  return magic == 0 ? n : (uint64_t)(((unsigned __int128)n * magic) >> 64);
+}
+inline bool magic64_exact(uint64_t n_max, uint64_t d) {
+  return (unsigned __int128)n_max * d < ((unsigned __int128)1 << 64);
+}
+
 // ---------------------------------------------------------------------------
 // GEMM tile order. The dispatcher sends workgroup `bid` to XCD bid % 8, and
 // each XCD has its own L2. Workgroups are first renumbered so that each XCD
