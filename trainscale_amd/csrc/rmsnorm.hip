@@ -116,6 +116,20 @@ __global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
   } else {
     rv[0] = u32x4{0, 0, 0, 0};
   }
+  // The weights go out with the row's loads (they are shared by every row and
+  // come from L2): loaded after the reduction they put an L2 round trip
+  // between rstd and the stores of every workgroup.
+  constexpr int kWq = sizeof(W) == 4 ? V / 4 : 1;  // 16-byte weight loads per data vector
+  constexpr int kWe = 16 / (int)sizeof(W);         // weights per 16-byte load
+  static_assert(kWq * kWe == V, "weight loads must cover one data vector");
+  u32x4 wq[KV][kWq];
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const int v = t + k * TPR;
+#pragma unroll
+    for (int h = 0; h < kWq; ++h)
+      wq[k][h] = w != nullptr && v < nvec ? ld16(w + (int64_t)v * V + h * kWe) : u32x4{0, 0, 0, 0};
+  }
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
@@ -145,7 +159,8 @@ __global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
       row_values<T, kAdd>(xv[k], rv[kAdd ? k : 0], f);
       if (w != nullptr) {
         float wf[V];
-        load_w<W, V>(w, (int64_t)v * V, wf);
+#pragma unroll
+        for (int h = 0; h < kWq; ++h) Elt<W>::unpack(wq[k][h], wf + h * kWe);
         if (twice) {
 #pragma unroll
           for (int i = 0; i < V; ++i) f[i] = Elt<T>::round(f[i] * rstd) * wf[i];
