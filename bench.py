@@ -258,8 +258,9 @@ def bench_packed(dev, steps: int, warmup: int):
 
 def bench_next_rows(dev, steps: int, warmup: int):
     """Rows beyond the hot path's five configs: fused residual add + RMSNorm forward at
-    the C1 and C4 shapes, and SwiGLU forward + backward at the Llama-3-8B MLP shape
-    [8, 2048, 14336]. Synthetic seeded inputs, each op timed alone."""
+    the C1 and C4 shapes, SwiGLU forward + backward at the Llama-3-8B MLP shape
+    [8, 2048, 14336], and one rank's vocabulary-parallel CE kernels at C3 / 8 ranks.
+    Synthetic seeded inputs, each op timed alone."""
     import torch
 
     from trainscale_amd import ops
@@ -291,6 +292,26 @@ def bench_next_rows(dev, steps: int, warmup: int):
                      "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
                      "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del gate, up, dout
+    # Vocabulary-parallel CE: one rank's kernels at C3 split over 8 ranks, a
+    # [16384, 16032] bf16 shard (the merge reads 8 ranks' partials).
+    N, P = 16384, 8
+    vp = 128256 // P
+    xs = (2 * torch.randn(N, vp, device=dev, generator=g)).to(torch.bfloat16)
+    tg = torch.randint(0, 128256, (N,), device=dev, generator=g)
+    st_all = ops.ce_vocab_shard_stats(xs, vp, tg, vp).unsqueeze(0).repeat(P, 1, 1).contiguous()
+    lse, _ = ops.ce_vocab_merge(st_all, 1, vp)
+    go = torch.ones((), device=dev)
+    vb = W.vocab_shard_bytes(N, vp, P)
+    for name, fn, b in (
+            ("vocab_shard_stats", lambda: ops.ce_vocab_shard_stats(xs, vp, tg, vp), vb["stats"]),
+            ("vocab_merge", lambda: ops.ce_vocab_merge(st_all, 1, vp), vb["merge"]),
+            ("vocab_shard_bwd",
+             lambda: ops.ce_vocab_shard_backward(xs, vp, tg, lse, go, 1.0 / N, vp), vb["bwd"])):
+        ms = time_ms(fn, steps, warmup)
+        res[name] = {"shape": [N, vp], "ranks": P, "ms": round(ms, 4), "bytes": b,
+                     "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del xs, tg, st_all, lse
     torch.cuda.empty_cache()
     return res
 

@@ -255,6 +255,54 @@ ts_status ts_ce_fwd_bwd(const void* logits, int64_t ld, ts_dtype dtype,
                         void* grad, int64_t ld_grad, ts_dtype grad_dtype, ts_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Vocabulary-parallel cross-entropy (the kernels of one rank)               */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * One rank's partials over its vocabulary shard: logits [N, Vp] (row stride
+ * ld) are the columns vocab_start .. vocab_start + Vp - 1 of the full
+ * vocabulary. For each row r, stats[4r .. 4r + 3] (16-byte aligned) receives
+ *   { lse over the shard, the logit of targets[r] when the target lies in the
+ *     shard (else 0), the sum of the shard's logits, 0 }.
+ * Exchanging these 16 bytes per row (one all-gather over the ranks) replaces
+ * the three all-reduces (row max, sum of exp, target logit) of
+ * VocabParallelCrossEntropyLoss.forward, distributed/tensor_parallel.py:1522-1573.
+ * No ignore_index: like the reference, every row counts.
+ */
+ts_status ts_ce_vocab_shard_stats(const void* logits, int64_t ld, ts_dtype dtype,
+                                  const int64_t* targets, int64_t N, int64_t Vp,
+                                  int64_t vocab_start, float* stats, ts_stream_t stream);
+
+/*
+ * Merges the P ranks' partials, stats_all [P][N][4] (rank-major, as an
+ * all-gather lays them out), into lse[N] and the per-row loss[N] of rank
+ * `self`:
+ *   lse = log sum_p exp(lse_p),  nll = lse - sum_p target_p,
+ *   loss = (1 - a) * nll + a * (lse - sum_z_self / Vp),  a = label_smoothing,
+ * which is VocabParallelCrossEntropyLoss.forward's per-row loss
+ * (tensor_parallel.py:1576-1597; the smoothing term, :1587-1588, uses the rank's own shard
+ * mean, as there).
+ */
+ts_status ts_ce_vocab_merge(const float* stats_all, int64_t P, int64_t self, int64_t N,
+                            int64_t Vp, float label_smoothing, float* lse, float* loss,
+                            ts_stream_t stream);
+
+/*
+ * Gradient over the shard:
+ *   grad[r, j] = dl * ((1 - a) * (exp(z - lse[r]) - [vocab_start + j == targets[r]]) - a / Vp),
+ *   dl = grad_output[0] * dloss_scale,
+ * VocabParallelCrossEntropyLoss.backward, tensor_parallel.py:1600-1632 (its
+ * caller passes dloss_scale = 1 / (B * S) for the mean). grad_dtype is the
+ * logits dtype or fp32; grad may alias the logits when both match.
+ */
+ts_status ts_ce_vocab_shard_bwd(const void* logits, int64_t ld, ts_dtype dtype,
+                                const int64_t* targets, const float* lse,
+                                const float* grad_output, float dloss_scale,
+                                int64_t N, int64_t Vp, int64_t vocab_start,
+                                float label_smoothing, void* grad, int64_t ld_grad,
+                                ts_dtype grad_dtype, ts_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Fused linear cross-entropy                                                */
 /* ------------------------------------------------------------------------ */
 

@@ -24,6 +24,7 @@ __all__ = [
     "ce_fwd",
     "ce_bwd",
     "linear_ce",
+    "vocab_parallel_ce",
     "swiglu_fwd",
     "swiglu_bwd",
 ]
@@ -239,6 +240,56 @@ def ce_bwd(logits: Tensor, labels: Tensor, dloss: Tensor, ignore_index: int = -1
     d = d.expand(n) if d.numel() == 1 else d
     g = g * torch.where(valid, d, torch.zeros_like(d))[:, None]
     return g.to(out_dtype or logits.dtype).reshape(logits.shape)
+
+
+def vocab_parallel_ce(shards, targets: Tensor, label_smoothing: float = 0.0):
+    """Every rank's (loss, grad) of VocabParallelCrossEntropyLoss over P = len(shards)
+    vocabulary shards (rank p holds shards[p], columns p*Vp .. (p+1)*Vp - 1), for an
+    upstream gradient of 1.
+
+    Restates distributed/tensor_parallel.py:1497-1632 with its all-reduces taken
+    over the list of shards: the row max (:1522-1531, MAX), the sum of exp
+    (:1537-1545, SUM), the masked target logit (:1553-1573, SUM), the loss
+    -target + max + log(sum) (:1576), label smoothing with the rank's own shard
+    mean (:1587-1588), loss.mean() (:1597); backward: exp(z - max) / sum
+    (:1607), minus the target mask at the clamped local target (:1623), then
+    (1 - a) * g - a / Vp with smoothing (:1628-1629), times 1 / (B * S) (:1632).
+    No ignore_index: every row counts, as there. The reference computes in the
+    logits' dtype; this restatement computes in fp32 (the north star's fp32
+    accumulation bar) and returns grads in fp32. Like the reference it multiplies
+    the gathered logit by the 0/1 mask (:1569), which is NaN when a shard without
+    the target holds -inf at the clamped index (the kernels take 0 there).
+    """
+    xs = [_cpu(x).reshape(-1, x.shape[-1]).float() for x in shards]
+    t = _cpu(targets).reshape(-1).to(torch.int64)
+    n, vp = xs[0].shape
+    rows = torch.arange(n)
+    m = torch.stack([x.max(dim=-1).values for x in xs]).max(dim=0).values
+    norm = [x - m[:, None] for x in xs]
+    sum_exp = torch.stack([z.exp().sum(dim=-1) for z in norm]).sum(dim=0)
+    lse_d = sum_exp.log()
+    tgt = torch.zeros(n)
+    masks, locals_ = [], []
+    for p, x in enumerate(xs):
+        v0 = p * vp
+        mask = (t >= v0) & (t < v0 + vp)
+        local = (t - v0).clamp(min=0, max=vp - 1)
+        tgt = tgt + x.gather(1, local[:, None]).squeeze(1) * mask.float()
+        masks.append(mask)
+        locals_.append(local)
+    nll = -tgt + m + lse_d
+    out = []
+    for p, z in enumerate(norm):
+        loss = nll
+        if label_smoothing > 0:
+            smooth = -z.mean(dim=-1) + lse_d
+            loss = (1 - label_smoothing) * loss + label_smoothing * smooth
+        g = z.exp() / sum_exp[:, None]
+        g[rows, locals_[p]] -= masks[p].float()
+        if label_smoothing > 0:
+            g = (1 - label_smoothing) * g - label_smoothing / vp
+        out.append((loss.mean(), g / n))
+    return out
 
 
 def linear_ce(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,

@@ -111,6 +111,43 @@ def test_ce_validation(lib):
     assert rc == DTYPE
 
 
+def test_vocab_parallel_validation(lib):
+    st = NULL
+    stats = lambda **k: lib.ts_ce_vocab_shard_stats(
+        k.get("x", FAKE), k.get("ld", 128), k.get("dt", 1), k.get("t", FAKE), k.get("N", 4),
+        k.get("Vp", 128), k.get("v0", 0), k.get("out", FAKE), st)
+    assert stats(ld=64) == SHAPE
+    assert stats(Vp=0) == SHAPE
+    assert stats(N=-1) == SHAPE
+    assert stats(v0=-5) == INVALID
+    assert stats(t=NULL) == INVALID
+    assert stats(out=NULL) == INVALID
+    assert stats(dt=7) == DTYPE
+    assert stats(Vp=1 << 29, ld=1 << 29) == SHAPE
+    assert stats(N=0, out=NULL) == TS_OK
+    merge = lambda **k: lib.ts_ce_vocab_merge(
+        k.get("s", FAKE), k.get("P", 2), k.get("self", 0), k.get("N", 4), k.get("Vp", 64),
+        k.get("a", 0.0), k.get("lse", FAKE), k.get("loss", FAKE), st)
+    assert merge(P=0) == INVALID
+    assert merge(self=2) == INVALID
+    assert merge(self=-1) == INVALID
+    assert merge(Vp=0) == SHAPE
+    assert merge(a=1.5) == INVALID
+    assert merge(loss=NULL) == INVALID
+    assert merge(N=0, s=NULL) == TS_OK
+    bwd = lambda **k: lib.ts_ce_vocab_shard_bwd(
+        k.get("x", FAKE), k.get("ld", 128), k.get("dt", 1), k.get("t", FAKE), FAKE,
+        k.get("go", FAKE), 1.0, k.get("N", 4), k.get("Vp", 128), 0, k.get("a", 0.0),
+        k.get("g", FAKE), k.get("ldg", 128), k.get("gdt", 1), st)
+    assert bwd(gdt=2) == DTYPE  # fp16 grad for bf16 logits
+    assert bwd(gdt=9) == DTYPE
+    assert bwd(ldg=64) == SHAPE
+    assert bwd(a=-0.1) == INVALID
+    assert bwd(go=NULL) == INVALID
+    assert bwd(g=NULL) == INVALID
+    assert bwd(N=0, g=NULL) == TS_OK
+
+
 def test_scale_and_rescale_validation(lib):
     st = NULL
     assert lib.ts_scale_inplace(FAKE, 12, 1, FAKE, st) == SHAPE

@@ -1,0 +1,143 @@
+"""Vocabulary-parallel cross entropy (the kernels of one rank) vs the oracle (GPU).
+
+Each test splits one full-vocabulary logits tensor into P column shards on one
+GPU and runs every rank's forward and backward through
+VocabParallelCrossEntropyLoss, with an exchange hook that hands each rank the
+P partials an all-gather over P ranks would deliver (computed by the same
+shard kernel). The shards are strided views of the full tensor, so the ranks'
+gradients land side by side in its .grad.
+
+Bar (north star): loss within 1e-5 relative in fp32 (plus the fp32 resolution
+of lse - z at the row's lse), gradients within 1 bf16 ulp of the oracle
+(fp32 gradients: 2e-5 relative).
+"""
+import math
+
+import pytest
+import torch
+
+import oracle
+from helpers import assert_ulp
+from trainscale_amd import ops
+from trainscale_amd.distributed import (VocabShardExchange, set_vocab_exchange,
+                                        vocab_parallel_cross_entropy)
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+TINY = 1e-37  # below bf16's normal range: v_exp_f32 flushes what the CPU keeps as a denormal
+
+
+def run_ranks(x, t, P, a):
+    """Every rank's (loss, ) and the full tensor's gradient after all P backwards."""
+    V = x.shape[-1]
+    vp = V // P
+    xg = x.clone().requires_grad_()
+    stats = torch.stack([ops.ce_vocab_shard_stats(*ops.as_rows(x[..., p * vp:(p + 1) * vp]),
+                                                  t.reshape(-1), p * vp) for p in range(P)])
+    losses = []
+    try:
+        for p in range(P):
+            def gather(st, p=p):
+                assert torch.equal(st, stats[p])  # this rank's own partials
+                return stats
+            set_vocab_exchange(VocabShardExchange(gather, p, P))
+            loss = vocab_parallel_cross_entropy(xg[..., p * vp:(p + 1) * vp], t, a)
+            loss.backward()
+            losses.append(loss.detach())
+    finally:
+        set_vocab_exchange(None)
+    return losses, xg.grad, stats
+
+
+def check_against_oracle(x, t, P, a, losses, grad):
+    vp = x.shape[-1] // P
+    ref = oracle.vocab_parallel_ce([x[..., p * vp:(p + 1) * vp].cpu() for p in range(P)],
+                                   t.cpu(), a)
+    lse_mag = torch.logsumexp(x.reshape(-1, x.shape[-1]).float().cpu(), -1).abs().max()
+    slack = 4 * 2.0 ** -23 * max(float(lse_mag), 1.0)
+    for p in range(P):
+        r = ref[p][0].item()
+        assert abs(losses[p].item() - r) <= 1e-5 * abs(r) + slack, (p, losses[p].item(), r)
+    ref_g = torch.cat([g for _, g in ref], 1).reshape(grad.shape)
+    if grad.dtype == torch.float32:
+        torch.testing.assert_close(grad.cpu(), ref_g, rtol=2e-5, atol=1e-10)
+    else:
+        assert_ulp(grad, ref_g, 1, tiny=TINY, what="grad")
+
+
+def make(V, dtype, seed, B=2, S=12):
+    g = torch.Generator().manual_seed(seed)
+    x = (2 * torch.randn(B, S, V, generator=g)).to(dtype)
+    t = torch.randint(0, V, (B, S), generator=g)
+    t[0, 3] = V + 5      # in no shard
+    t[1, 7] = -100       # in no shard (the reference has no ignore_index)
+    return x.cuda(), t.cuda()
+
+
+@pytest.mark.parametrize("V,P,dtype,a", [
+    (128256, 8, BF, 0.0), (128256, 8, BF, 0.1), (4096, 4, BF, 0.0), (1000, 2, BF, 0.1),
+    (50264, 4, torch.float16, 0.0), (32000, 2, torch.float32, 0.1), (128256, 1, BF, 0.0),
+    (262144, 1, BF, 0.0)])
+def test_ranks_match_the_oracle(V, P, dtype, a):
+    """Shard widths through every kernel path: 256 x {2, 4, 8, 16} and 1024 x 16
+    register rows, element-wise rows for widths that are not a multiple of the
+    vector or wider than 131072, bf16/fp16/fp32, smoothing on and off."""
+    x, t = make(V, dtype, V + P)
+    losses, grad, _ = run_ranks(x, t, P, a)
+    check_against_oracle(x, t, P, a, losses, grad)
+
+
+def test_masked_vocabulary_and_empty_shards():
+    """-inf columns (a padded vocabulary), one rank's shard entirely -inf on a row
+    (its partial lse is -inf and the merge skips it), and a value 100 above the
+    rest of its row. Checked against the full-vocabulary CE oracle: the reference
+    multiplies the gathered target logit by the shard's 0/1 mask
+    (tensor_parallel.py:1569), so a -inf logit at the clamped index of a shard
+    that does not hold the target makes its loss NaN; these kernels take 0 there,
+    and every rank's loss is the full CE's."""
+    V, P = 32768, 4
+    x, t = make(V, BF, 3)
+    x[..., V - 300:] = -math.inf
+    x[0, 1, :V // P] = -math.inf
+    t[0, 1] = V // P + 17
+    x[1, 2, 12345] = 100.0
+    losses, grad, stats = run_ranks(x, t, P, 0.0)
+    assert stats[0, 1, 0].item() == -math.inf
+    x2, t2 = x.reshape(-1, V).cpu(), t.reshape(-1).cpu()
+    n = x2.shape[0]
+    bad = (t2 < 0) | (t2 >= V)  # in no shard: the loss is the lse (target logit 0)
+    full, _ = oracle.ce_fwd(x2, t2.clamp(0, V - 1), ignore_index=-(1 << 40))
+    full = torch.where(bad, torch.logsumexp(x2.float(), -1), full)
+    for p in range(P):
+        assert abs(losses[p].item() - full.mean().item()) <= 1e-5 * abs(full.mean().item())
+    ref_g = oracle.ce_bwd(x2, t2.clamp(0, V - 1), torch.tensor(1.0 / n),
+                          ignore_index=-(1 << 40), out_dtype=torch.float32)
+    soft = torch.softmax(x2.float(), -1) / n
+    ref_g[bad] = soft[bad]
+    assert_ulp(grad.reshape(-1, V), ref_g, 1, tiny=TINY, what="grad")
+
+
+def test_merge_of_c3_shards_equals_the_full_ce():
+    """At C3's shape with P = 8 (shards of [16384, 16032], the per-rank size): the
+    merged lse equals the full-vocabulary CE kernel's lse, and the ranks' gradients
+    side by side equal the full kernel's gradient within 1 bf16 ulp."""
+    from trainscale_amd import workloads
+    wl = workloads.ce_workload(torch.device("cuda"))
+    x, labels = wl.tensors["logits"], wl.tensors["labels"]
+    N, V = x.shape
+    t = labels.clamp(min=0)  # every row counts here
+    P, vp = 8, V // 8
+    stats = torch.stack([ops.ce_vocab_shard_stats(x[:, p * vp:(p + 1) * vp], V, t, p * vp)
+                         for p in range(P)])
+    lse, loss = ops.ce_vocab_merge(stats, 0, vp)
+    full_loss, full_lse = ops.ce_forward(x, V, t)
+    torch.testing.assert_close(lse, full_lse, rtol=2e-6, atol=0)
+    torch.testing.assert_close(loss, full_loss, rtol=2e-5, atol=2e-5)
+    go = torch.ones((), device=x.device)
+    g_full = torch.empty_like(x)
+    ops.ce_backward(x, V, t, full_lse, torch.tensor([1.0 / N], device=x.device), g_full, V)
+    for p in (0, 3, 7):
+        gp = ops.ce_vocab_shard_backward(x[:, p * vp:(p + 1) * vp], V, t, lse, go, 1.0 / N, p * vp)
+        d = (gp.float() - g_full[:, p * vp:(p + 1) * vp].float()).abs()
+        ulp = g_full[:, p * vp:(p + 1) * vp].float().abs() * 2.0 ** -7
+        assert bool((d <= ulp + TINY).all()), float((d - ulp).max())

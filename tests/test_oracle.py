@@ -284,6 +284,81 @@ def test_linear_ce_matches_golden():
 # Mutations: plausible mistakes in the oracle must fail the checks above.
 # ---------------------------------------------------------------------------
 
+@pytest.mark.parametrize("P", [1, 3, 4])
+def test_vocab_parallel_equals_full_ce(P):
+    """Without smoothing every rank's loss is the full-vocabulary mean CE and the
+    ranks' gradients side by side are the full gradient / n (the pinned CE oracle,
+    itself checked against golden vectors and torch's cross_entropy)."""
+    torch.manual_seed(P)
+    n, v = 9, 60
+    x = (2 * torch.randn(n, v)).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,))
+    out = oracle.vocab_parallel_ce(list(x.split(v // P, dim=1)), t)
+    full, _ = oracle.ce_fwd(x, t, ignore_index=-(1 << 40))
+    g = oracle.ce_bwd(x, t, torch.tensor(1.0 / n), ignore_index=-(1 << 40), out_dtype=torch.float32)
+    for loss, _ in out:
+        assert abs(loss.item() - full.mean().item()) <= 1e-6 * abs(full.mean().item())
+    torch.testing.assert_close(torch.cat([gp for _, gp in out], 1), g, rtol=1e-5, atol=1e-8)
+
+
+def test_vocab_parallel_smoothing_follows_the_reference():
+    """One rank: the loss is the standard smoothed CE; the reference's backward
+    scales the softmax term by (1 - a), so its gradient is the true smoothed-CE
+    gradient minus a * softmax / n. With P ranks the smoothed loss of rank p is
+    the nll plus a * (lse - mean of p's shard), so two ranks differ by
+    a * (mean_q - mean_p)."""
+    torch.manual_seed(11)
+    n, v, a = 7, 48, 0.1
+    x = (3 * torch.randn(n, v)).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,))
+    (loss, g), = oracle.vocab_parallel_ce([x], t, a)
+    ref, _ = oracle.ce_fwd(x, t, ignore_index=-(1 << 40), label_smoothing=a)
+    assert abs(loss.item() - ref.mean().item()) <= 1e-6 * abs(ref.mean().item())
+    g_std = oracle.ce_bwd(x, t, torch.tensor(1.0 / n), ignore_index=-(1 << 40),
+                          label_smoothing=a, out_dtype=torch.float32)
+    soft = torch.softmax(x.double(), -1)
+    torch.testing.assert_close(g.double(), g_std.double() - a * soft / n, rtol=1e-5, atol=1e-8)
+    shards = list(x.split(v // 4, dim=1))
+    out = oracle.vocab_parallel_ce(shards, t, a)
+    means = [s.double().mean(-1) for s in shards]
+    for p in range(4):
+        for q in range(4):
+            d = (out[p][0] - out[q][0]).item()
+            assert abs(d - a * (means[q] - means[p]).mean().item()) <= 1e-5
+
+
+def test_vocab_parallel_targets_outside_every_shard():
+    """A target outside the vocabulary (or negative) is in no shard: the loss is the
+    lse and the gradient the plain softmax / n, as the reference's masks give."""
+    torch.manual_seed(5)
+    n, v = 4, 32
+    x = torch.randn(n, v)
+    t = torch.tensor([3, v + 7, -100, v])
+    out = oracle.vocab_parallel_ce(list(x.split(8, dim=1)), t)
+    lse = torch.logsumexp(x.double(), -1)
+    nll = lse - torch.tensor([x[0, 3].item(), 0.0, 0.0, 0.0], dtype=torch.float64)
+    assert abs(out[0][0].item() - nll.mean().item()) <= 1e-5
+    g = torch.cat([gp for _, gp in out], 1).double()
+    soft = torch.softmax(x.double(), -1) / n
+    torch.testing.assert_close(g[1:], soft[1:], rtol=1e-5, atol=1e-9)
+    assert abs(g[0, 3].item() - (soft[0, 3].item() - 1.0 / n)) <= 1e-6
+
+
+def test_mutation_vocab_parallel_smoothing_scale_is_caught():
+    """Planted mistake (the true smoothed-CE gradient in place of the reference's
+    (1 - a)-scaled softmax) fails the relation the test above checks."""
+    torch.manual_seed(11)
+    n, v, a = 7, 48, 0.1
+    x = (3 * torch.randn(n, v)).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,))
+    g_std = oracle.ce_bwd(x, t, torch.tensor(1.0 / n), ignore_index=-(1 << 40),
+                          label_smoothing=a, out_dtype=torch.float32)
+    soft = torch.softmax(x.double(), -1)
+    with pytest.raises(AssertionError):
+        torch.testing.assert_close(g_std.double(), g_std.double() - a * soft / n,
+                                   rtol=1e-5, atol=1e-8)
+
+
 def test_mutation_rope_sign_is_caught():
     g = golden("rope_neox_seq")
     x = t32(g["x"]).to(BF)

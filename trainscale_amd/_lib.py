@@ -72,6 +72,10 @@ SIGNATURES = {
                   I32),
     "ts_ce_fwd_bwd": ([P, I64, I32, P, I64, I64, I64, F32, F32, F32, P, I64, F32, P, P, P, I64,
                        I32, P], I32),
+    "ts_ce_vocab_shard_stats": ([P, I64, I32, P, I64, I64, I64, P, P], I32),
+    "ts_ce_vocab_merge": ([P, I64, I64, I64, I64, F32, P, P, P], I32),
+    "ts_ce_vocab_shard_bwd": ([P, I64, I32, P, P, P, F32, I64, I64, I64, F32, P, I64, I32, P],
+                              I32),
     "ts_flce_workspace_size": ([I64, I64, I64, I64, I32], SZ),
     "ts_flce_fwd_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, P, P, P, P, P, I64, P, SZ, P],
                         I32),

@@ -343,6 +343,75 @@ def ce_forward_backward(logits2d: Tensor, ld: int, labels: Tensor, dloss: Tensor
     return loss, lse, grad
 
 
+# ---------------------------------------------------------------------------
+# Vocabulary-parallel cross entropy (the kernels of one rank)
+# ---------------------------------------------------------------------------
+
+def ce_vocab_shard_stats(logits2d: Tensor, ld: int, targets: Tensor, vocab_start: int) -> Tensor:
+    """Per-row partials [N, 4] fp32 of this rank's shard: (lse over the shard,
+    target logit if the target is in the shard else 0, sum of the shard's
+    logits, 0). The tensor an all-gather exchanges between the ranks."""
+    dev = _lib.require_gpu("vocab_parallel_cross_entropy", logits2d, targets)
+    n, vp = logits2d.shape
+    targets = _labels(targets, n)
+    stats = torch.empty((n, 4), dtype=torch.float32, device=dev)
+    if n == 0:
+        return stats
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_ce_vocab_shard_stats(ptr(logits2d), ld,
+                                          _lib.dtype_code(logits2d, "vocab_parallel_cross_entropy"),
+                                          ptr(targets), n, vp, int(vocab_start), ptr(stats),
+                                          _lib.stream_handle(dev)), "ts_ce_vocab_shard_stats")
+    return stats
+
+
+def ce_vocab_merge(stats_all: Tensor, self_index: int, vp: int,
+                   label_smoothing: float = 0.0) -> Tuple[Tensor, Tensor]:
+    """(lse [N], loss [N]) of rank `self_index` from every rank's partials [P, N, 4]."""
+    dev = _lib.require_gpu("vocab_parallel_cross_entropy", stats_all)
+    if stats_all.dim() != 3 or stats_all.shape[2] != 4 or stats_all.dtype != torch.float32:
+        raise ValueError(f"vocab_parallel_cross_entropy: partials must be fp32 [P, N, 4], "
+                         f"got {stats_all.dtype} {tuple(stats_all.shape)}")
+    stats_all = stats_all.contiguous()
+    p, n = stats_all.shape[0], stats_all.shape[1]
+    lse = torch.empty((n,), dtype=torch.float32, device=dev)
+    loss = torch.empty((n,), dtype=torch.float32, device=dev)
+    if n == 0:
+        return lse, loss
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_ce_vocab_merge(ptr(stats_all), p, int(self_index), n, int(vp),
+                                    float(label_smoothing), ptr(lse), ptr(loss),
+                                    _lib.stream_handle(dev)), "ts_ce_vocab_merge")
+    return lse, loss
+
+
+def ce_vocab_shard_backward(logits2d: Tensor, ld: int, targets: Tensor, lse: Tensor,
+                            grad_output: Tensor, dloss_scale: float, vocab_start: int,
+                            label_smoothing: float = 0.0,
+                            grad_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """Gradient [N, Vp] of this rank's shard (a new tensor, the logits dtype or fp32)."""
+    dev = _lib.require_gpu("vocab_parallel_cross_entropy_backward", logits2d, targets, lse,
+                           grad_output)
+    n, vp = logits2d.shape
+    targets = _labels(targets, n)
+    grad = torch.empty((n, vp), dtype=grad_dtype or logits2d.dtype, device=dev)
+    if n == 0:
+        return grad
+    go = grad_output.detach().reshape(-1)[:1].float().contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_ce_vocab_shard_bwd(ptr(logits2d), ld,
+                                        _lib.dtype_code(logits2d, "vocab_parallel_cross_entropy"),
+                                        ptr(targets), ptr(lse.contiguous()), ptr(go),
+                                        float(dloss_scale), n, vp, int(vocab_start),
+                                        float(label_smoothing), ptr(grad), vp,
+                                        _lib.dtype_code(grad, "vocab_parallel grad"),
+                                        _lib.stream_handle(dev)), "ts_ce_vocab_shard_bwd")
+    return grad
+
+
 def scale_(t: Tensor, scale: Tensor) -> Tensor:
     """t *= scale in place (scale: a one-element fp32 device tensor); a no-op on the
     device when scale == 1, without synchronising."""

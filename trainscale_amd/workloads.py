@@ -175,6 +175,16 @@ def ce_bytes_fused(n: int, n_valid: int, v: int, elt: int = 2) -> int:
     return n_valid * v * elt + n * v * elt + n * (8 + 4 + 4)
 
 
+def vocab_shard_bytes(n: int, vp: int, p: int, elt: int = 2) -> Dict[str, int]:
+    """One rank of a P-way vocabulary-parallel CE over a [n, vp] shard. stats: read
+    the shard and the targets, write 16 B of partials per row. merge: read the P
+    ranks' partials, write lse and loss. bwd: read the shard, targets and lse, write
+    the gradient."""
+    shard = n * vp * elt
+    return dict(stats=shard + n * (8 + 16), merge=p * n * 16 + n * 8,
+                bwd=2 * shard + n * (8 + 4) + 4)
+
+
 def linear_ce_flops(n: int, h: int, v: int) -> int:
     """Three GEMMs of 2*N*V*H: logits, grad_hidden, grad_weight."""
     return 3 * 2 * n * v * h
