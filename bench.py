@@ -365,7 +365,10 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md)"}))
+                                   "(every rank would run these kernels on its own shard: "
+                                   "rows for RMSNorm/RoPE/CE, vocabulary columns for the "
+                                   "vocab-parallel CE, whose per-rank kernels are measured "
+                                   "at their shard shape)"}))
         sys.exit(2)
 
     import torch
