@@ -87,6 +87,10 @@ def test_rope_validation(lib):
     assert _rope(lib, il=2) == INVALID
     assert _rope(lib, dtype=9) == DTYPE
     assert _rope(lib, S=0) == TS_OK
+    # empty tensors carry NULL data pointers: no tokens, nothing to check or launch
+    assert _rope(lib, S=0, q_in=NULL, q_out=NULL) == TS_OK
+    assert _rope(lib, B=0, q_in=NULL, q_out=NULL, Hk=2) == TS_OK
+    assert _rope(lib, q_in=NULL) == INVALID  # tokens but no Q data
 
 
 def test_ce_validation(lib):

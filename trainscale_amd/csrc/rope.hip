@@ -384,9 +384,12 @@ extern "C" ts_status ts_rope_apply(
     return fail(TS_ERR_SHAPE, "rope: head_dim must be even and <= %d (got %lld)", 2 * kMaxHalf,
                 (long long)D);
   if (Hq + Hk > 4096) return fail(TS_ERR_SHAPE, "rope: more than 4096 heads per token");
-  if (Hq > 0 && (q_in == nullptr || q_out == nullptr))
+  // Tensors without tokens may have NULL data pointers (torch gives empty
+  // tensors none); nothing is read or written for them.
+  const bool any_tokens = B > 0 && S > 0;
+  if (any_tokens && Hq > 0 && (q_in == nullptr || q_out == nullptr))
     return fail(TS_ERR_INVALID_ARGUMENT, "rope: q pointers are NULL");
-  if (Hk > 0 && (k_in == nullptr || k_out == nullptr))
+  if (any_tokens && Hk > 0 && (k_in == nullptr || k_out == nullptr))
     return fail(TS_ERR_INVALID_ARGUMENT, "rope: k pointers are NULL");
   if (interleaved != 0 && interleaved != 1)
     return fail(TS_ERR_INVALID_ARGUMENT, "rope: interleaved must be 0 or 1");

@@ -158,7 +158,7 @@ def rope_apply(q_in: Optional[Tensor], q_out: Optional[Tensor],
             if t.dim() != 4 or t.shape[0] != B or t.shape[1] != S or t.shape[3] != D:
                 raise ValueError(f"rope: {name} shape {tuple(t.shape)} does not match "
                                  f"[{B}, {S}, H, {D}]")
-            if t.shape[3] > 1 and t.stride(3) != 1:
+            if t.numel() > 0 and t.shape[3] > 1 and t.stride(3) != 1:
                 raise ValueError(f"rope: {name} needs a contiguous head dimension")
             if t.dtype != ref.dtype:
                 raise TypeError(f"rope: {name} dtype {t.dtype} != {ref.dtype}")
