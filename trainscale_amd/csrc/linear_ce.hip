@@ -256,7 +256,7 @@ __global__ __launch_bounds__(256) void flce_loss(const float* __restrict__ loss_
 // over the logits [M, V] (0 on ignored rows, which are not read). One-shot
 // grid: a thread owns kDlKv 16-byte vectors of a row, spaced one workgroup
 // apart; blockIdx.x = row * chunks + chunk.
-constexpr int kDlKv = 2;
+constexpr int kDlKv = 1;
 __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int64_t ldl,
                                                     const float* __restrict__ lse,
                                                     const int64_t* __restrict__ labels,

@@ -21,7 +21,10 @@ namespace {
 using namespace ts;
 
 constexpr int kSwiThreads = 256;
-constexpr int kSwiKv = 2;
+// One 16-byte vector per thread: measured on MI355X at [8, 2048, 14336] bf16, the
+// forward took 216 us against 230 us with two vectors per thread, the backward
+// 376 against 387 us.
+constexpr int kSwiKv = 1;
 
 __device__ inline float sigmoid_f(float g) {
   return __builtin_amdgcn_rcpf(1.f + fast_exp2(-g * kLog2e));
