@@ -259,7 +259,8 @@ def bench_packed(dev, steps: int, warmup: int):
 def bench_next_rows(dev, steps: int, warmup: int):
     """Rows beyond the hot path's five configs: fused residual add + RMSNorm forward at
     the C1 and C4 shapes, SwiGLU forward + backward at the Llama-3-8B MLP shape
-    [8, 2048, 14336], and one rank's vocabulary-parallel CE kernels at C3 / 8 ranks.
+    [8, 2048, 14336], and one rank's vocabulary-parallel CE kernels at C3 / 8 ranks and fused
+    linear-CE phases at C5 / 8 ranks.
     Synthetic seeded inputs, each op timed alone."""
     import torch
 
@@ -312,6 +313,28 @@ def bench_next_rows(dev, steps: int, warmup: int):
                      "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
                      "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del xs, tg, st_all, lse
+    # Vocabulary-parallel fused linear CE: one rank of C5 over 8 ranks, hidden
+    # [8192, 4096] against an LM head shard [16032, 4096]: phase 1 (logits GEMM and
+    # partials) and phase 2 (merge of 8 ranks' partials, dlogits, grad_hidden
+    # partial and grad_weight shard GEMMs).
+    from trainscale_amd.loss.linear_ce import linear_ce_vocab_phase1, linear_ce_vocab_phase2
+    Nt, H = 8192, 4096
+    hid = torch.randn(Nt, H, device=dev, generator=g).to(torch.bfloat16)
+    wsh = (0.02 * torch.randn(vp, H, device=dev, generator=g)).to(torch.bfloat16)
+    lab = torch.randint(0, 128256, (Nt,), device=dev, generator=g)
+    lab[::20] = -100
+
+    def vocab_lce():
+        stats, state = linear_ce_vocab_phase1(hid, wsh, lab, vp)
+        linear_ce_vocab_phase2(state, stats.unsqueeze(0).expand(P, -1, -1), -100, "mean")
+
+    ms = time_ms(vocab_lce, steps, warmup)
+    fl = 3 * 2 * Nt * vp * H
+    res["vocab_linear_ce"] = {"shape": {"hidden": [Nt, H], "weight_shard": [vp, H]}, "ranks": P,
+                              "ms": round(ms, 4), "flop": fl,
+                              "TFLOP_s": round(fl / (ms * 1e-3) / 1e12, 1),
+                              "frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    del hid, wsh, lab
     torch.cuda.empty_cache()
     return res
 

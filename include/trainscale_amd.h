@@ -302,6 +302,46 @@ ts_status ts_ce_vocab_shard_bwd(const void* logits, int64_t ld, ts_dtype dtype,
                                 float label_smoothing, void* grad, int64_t ld_grad,
                                 ts_dtype grad_dtype, ts_stream_t stream);
 
+/*
+ * Vocabulary-parallel fused linear cross-entropy, the two phases of one rank
+ * (no reference function: the vocabulary-parallel form of ts_flce_fwd_bwd for
+ * an LM head split by rows over the tensor-parallel ranks, the layout of
+ * VocabParallelEmbedding / ColumnParallelLinear, distributed/tensor_parallel.py).
+ * weight: this rank's [Vp, H] rows, vocabulary columns vocab_start ..
+ * vocab_start + Vp - 1. N, H and Vp are multiples of 8. Both phases take the
+ * same workspace of ts_flce_vocab_workspace_size(N, Vp) bytes, which carries
+ * the shard's logits from phase 1 to phase 2 and must not change in between.
+ *
+ * Phase 1: logits = hidden @ weight^T (bf16, into the workspace) and the
+ * per-row partials stats[4r .. 4r + 3] = {lse over the shard, the logit of
+ * labels[r] if the shard holds it (else 0), 0, 0}: the layout of
+ * ts_ce_vocab_shard_stats, for the same all-gather.
+ */
+size_t ts_flce_vocab_workspace_size(int64_t N, int64_t Vp);
+ts_status ts_flce_vocab_fwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                            const int64_t* labels, int64_t N, int64_t H, int64_t Vp,
+                            int64_t vocab_start, float* stats, void* workspace,
+                            size_t workspace_bytes, ts_stream_t stream);
+
+/*
+ * Phase 2, after the caller gathered every rank's partials into stats_all
+ * [P][N][4] (rank-major): lse[r] = log sum_p exp(lse_p), the per-row loss
+ * lse - (sum of the target logits) (0 where labels[r] == ignore_index; a
+ * label in no rank's shard contributes a target logit of 0), loss = their
+ * mean over non-ignored rows (reduction 0) or sum (1), the same on every rank.
+ * Then the shard's dlogits ((softmax - onehot) * loss scale, bf16, in the
+ * workspace) give grad_hidden_partial [N, H] = dlogits @ weight (bf16; the
+ * caller sums it over the ranks) and grad_weight_shard [Vp, H] = dlogits^T @
+ * hidden (bf16). Either gradient may be NULL; loss_rows and lse may be NULL.
+ */
+ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                            const int64_t* labels, int64_t N, int64_t H, int64_t Vp,
+                            int64_t vocab_start, const float* stats_all, int64_t P,
+                            int64_t ignore_index, int32_t reduction, float* loss,
+                            float* loss_rows, float* lse, void* grad_hidden_partial,
+                            void* grad_weight_shard, void* workspace, size_t workspace_bytes,
+                            ts_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Fused linear cross-entropy                                                */
 /* ------------------------------------------------------------------------ */

@@ -152,6 +152,34 @@ def test_vocab_parallel_validation(lib):
     assert bwd(N=0, g=NULL) == TS_OK
 
 
+def test_flce_vocab_validation(lib):
+    st = NULL
+    ws_need = lib.ts_flce_vocab_workspace_size(64, 256)
+    assert ws_need > 64 * 256 * 2
+    assert lib.ts_flce_vocab_workspace_size(0, 256) == 0
+    fwd = lambda **k: lib.ts_flce_vocab_fwd(
+        k.get("h", FAKE), k.get("ldh", 128), k.get("w", FAKE), k.get("ldw", 128), k.get("lab", FAKE),
+        k.get("N", 64), k.get("H", 128), k.get("Vp", 256), k.get("v0", 0), k.get("stats", FAKE),
+        k.get("ws", FAKE), k.get("wsb", ws_need), st)
+    assert fwd(N=60) == SHAPE       # not a multiple of 8
+    assert fwd(Vp=0) == SHAPE
+    assert fwd(ldh=64) == SHAPE
+    assert fwd(Vp=1 << 23) == SHAPE
+    assert fwd(v0=-8) == INVALID
+    assert fwd(lab=NULL) == INVALID
+    assert fwd(stats=NULL) == INVALID
+    assert fwd(wsb=ws_need - 1) == WORKSPACE
+    assert fwd(ws=NULL) == WORKSPACE
+    bwd = lambda **k: lib.ts_flce_vocab_bwd(
+        FAKE, 128, FAKE, 128, FAKE, 64, 128, 256, 0, k.get("sa", FAKE), k.get("P", 2), -100,
+        k.get("red", 0), k.get("loss", FAKE), NULL, NULL, FAKE, FAKE, FAKE, k.get("wsb", ws_need), st)
+    assert bwd(P=0) == INVALID
+    assert bwd(sa=NULL) == INVALID
+    assert bwd(red=3) == INVALID
+    assert bwd(loss=NULL) == INVALID
+    assert bwd(wsb=16) == WORKSPACE
+
+
 def test_scale_and_rescale_validation(lib):
     st = NULL
     assert lib.ts_scale_inplace(FAKE, 12, 1, FAKE, st) == SHAPE

@@ -141,3 +141,73 @@ def test_merge_of_c3_shards_equals_the_full_ce():
         d = (gp.float() - g_full[:, p * vp:(p + 1) * vp].float()).abs()
         ulp = g_full[:, p * vp:(p + 1) * vp].float().abs() * 2.0 ** -7
         assert bool((d <= ulp + TINY).all()), float((d - ulp).max())
+
+
+# ---------------------------------------------------------------------------
+# Vocabulary-parallel fused linear CE (one rank's two phases)
+# ---------------------------------------------------------------------------
+
+def lce_ranks(h, w, labels, P, reduction="mean"):
+    """Every rank's (loss, loss_rows, lse, grad_hidden_partial, grad_weight_shard)."""
+    from trainscale_amd.loss.linear_ce import linear_ce_vocab_phase1, linear_ce_vocab_phase2
+    vp = w.shape[0] // P
+    phase1 = [linear_ce_vocab_phase1(h, w[p * vp:(p + 1) * vp], labels, p * vp)
+              for p in range(P)]
+    stats_all = torch.stack([s for s, _ in phase1])
+    return [linear_ce_vocab_phase2(st, stats_all, -100, reduction) for _, st in phase1]
+
+
+@pytest.mark.parametrize("N,H,V,P", [(64, 128, 1024, 4), (264, 40, 2080, 2), (520, 256, 4096, 8),
+                                     (1032, 296, 1552, 2)])
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_linear_ce_ranks_match_the_full_kernel(N, H, V, P, reduction):
+    """The ranks' loss is the full kernel's (and the oracle's), their grad_hidden
+    partials sum to its grad_hidden, and their grad_weight shards side by side are
+    its grad_weight (the full kernel is pinned to the oracle in
+    test_gpu_linear_ce.py)."""
+    from trainscale_amd.loss.linear_ce import linear_ce_forward_backward
+    g = torch.Generator().manual_seed(N + V)
+    h = torch.randn(N, H, generator=g).to(BF).cuda()
+    w = (0.05 * torch.randn(V, H, generator=g)).to(BF).cuda()
+    labels = torch.randint(0, V, (N,), generator=g)
+    labels[::9] = -100
+    labels = labels.cuda()
+    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels, reduction=reduction)
+    outs = lce_ranks(h, w, labels, P, reduction)
+    ref_loss, _, _, _, _ = oracle.linear_ce(h.cpu(), w.cpu(), labels.cpu(), reduction=reduction,
+                                            bf16_logits=True, return_rows=True)
+    for lp, rp, lsep, _, _ in outs:
+        assert abs(lp.item() - loss.item()) <= 2e-6 * abs(loss.item())
+        assert abs(lp.item() - ref_loss.item()) <= 1e-5 * abs(ref_loss.item())
+        torch.testing.assert_close(lsep, lse, rtol=2e-6, atol=0)
+        torch.testing.assert_close(rp, rows, rtol=2e-5, atol=2e-5)
+    gh_sum = sum(o[3].float() for o in outs)
+    d = (gh_sum - gh.float()).abs()
+    assert float(d.max()) <= 2e-2
+    assert float(d.norm() / gh.float().norm()) <= 1e-2
+    gw_cat = torch.cat([o[4] for o in outs], 0)
+    d = (gw_cat.float() - gw.float()).abs()
+    assert float(d.max()) <= 2e-2
+    assert float(d.norm() / gw.float().norm()) <= 1e-2
+
+
+def test_linear_ce_single_rank_autograd_equals_fused():
+    """One rank (world size 1): the autograd class gives fused_linear_cross_entropy's
+    loss and gradients bit for bit (a merge of one partial leaves lse unchanged),
+    including the upstream-gradient scale."""
+    from trainscale_amd.distributed import vocab_parallel_linear_cross_entropy
+    from trainscale_amd.loss import fused_linear_cross_entropy
+    g = torch.Generator().manual_seed(7)
+    h = torch.randn(2, 48, 128, generator=g).to(BF).cuda()
+    w = (0.05 * torch.randn(1000, 128, generator=g)).to(BF).cuda()
+    labels = torch.randint(0, 1000, (2, 48), generator=g)
+    labels[0, :5] = -100
+    labels = labels.cuda()
+    res = []
+    for fn in (fused_linear_cross_entropy, vocab_parallel_linear_cross_entropy):
+        hg, wg = h.clone().requires_grad_(), w.clone().requires_grad_()
+        loss = fn(hg, wg, labels)
+        (0.5 * loss).backward()
+        res.append((loss.detach(), hg.grad, wg.grad))
+    assert torch.equal(res[0][0], res[1][0])
+    assert torch.equal(res[0][1], res[1][1]) and torch.equal(res[0][2], res[1][2])

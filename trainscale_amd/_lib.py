@@ -76,6 +76,10 @@ SIGNATURES = {
     "ts_ce_vocab_merge": ([P, I64, I64, I64, I64, F32, P, P, P], I32),
     "ts_ce_vocab_shard_bwd": ([P, I64, I32, P, P, P, F32, I64, I64, I64, F32, P, I64, I32, P],
                               I32),
+    "ts_flce_vocab_workspace_size": ([I64, I64], SZ),
+    "ts_flce_vocab_fwd": ([P, I64, P, I64, P, I64, I64, I64, I64, P, P, SZ, P], I32),
+    "ts_flce_vocab_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, P, I64, I64, I32, P, P, P, P,
+                           P, P, SZ, P], I32),
     "ts_flce_workspace_size": ([I64, I64, I64, I64, I32], SZ),
     "ts_flce_fwd_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, P, P, P, P, P, I64, P, SZ, P],
                         I32),

@@ -235,6 +235,76 @@ __global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stat
   loss_rows[r] = out;
 }
 
+// Vocabulary-parallel linear CE, one rank. The 16-byte per-row partial the
+// ranks exchange: {lse over the shard, the label's logit if the shard holds
+// it (else 0), 0, 0} (the layout of ts_ce_vocab_shard_stats).
+struct ShardStats {
+  float lse, target, sum_z, pad;
+};
+
+// Per row of the shard's logits (one wave per row): the shard lse from the
+// GEMM's slice statistics and the label's logit when vocab_start <= label <
+// vocab_start + Vp, read from the bf16 logits.
+__global__ __launch_bounds__(256) void flce_shard_rows(const float2* __restrict__ stats,
+                                                       int64_t nparts,
+                                                       const __bf16* __restrict__ logits,
+                                                       int64_t ldl,
+                                                       const int64_t* __restrict__ labels,
+                                                       int64_t M, int64_t Vp,
+                                                       int64_t vocab_start,
+                                                       ShardStats* __restrict__ out) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= M) return;  // wave-uniform
+  const float2* sr = stats + r * nparts;
+  float m = -INFINITY;
+  for (int64_t p = lane; p < nparts; p += 64) m = fmaxf(m, sr[p].x);
+  m = wave_max(m);
+  float s = 0.f;
+  for (int64_t p = lane; p < nparts; p += 64) {
+    const float2 st = sr[p];
+    s += st.y == 0.f ? 0.f : st.y * fast_exp2((st.x - m) * kLog2e);
+  }
+  s = wave_sum(s);
+  if (lane != 0) return;
+  const int64_t tl = labels[r] - vocab_start;
+  const float zt = tl >= 0 && tl < Vp ? Elt<__bf16>::load1(logits + r * ldl + tl) : 0.f;
+  out[r] = ShardStats{m + logf(s), zt, 0.f, 0.f};
+}
+
+// Merges the P ranks' partials (rank-major [P][N]) into lse and the per-row
+// loss: lse - sum of the target logits, 0 on rows whose label is ignore_index.
+// One thread per row, eight ranks' partials loaded before they are folded.
+__global__ __launch_bounds__(64) void flce_vocab_merge(const ShardStats* __restrict__ all,
+                                                       int64_t P, int64_t N,
+                                                       const int64_t* __restrict__ labels,
+                                                       int64_t ignore_index,
+                                                       float* __restrict__ lse_out,
+                                                       float* __restrict__ rows_out) {
+  const int64_t r = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (r >= N) return;
+  float gm = -INFINITY, gs = 0.f, zt = 0.f;
+  constexpr int kU = 8;
+  for (int64_t p0 = 0; p0 < P; p0 += kU) {
+    ShardStats st[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      st[u] = p0 + u < P ? all[(p0 + u) * N + r] : ShardStats{-INFINITY, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (st[u].lse > gm) {  // false for -inf partials and NaN
+        gs = gs == 0.f ? 0.f : gs * fast_exp2((gm - st[u].lse) * kLog2e);
+        gm = st[u].lse;
+      }
+      gs += st[u].lse == -INFINITY ? 0.f : fast_exp2((st[u].lse - gm) * kLog2e);
+      zt += st[u].target;
+    }
+  }
+  const float lse = gm == -INFINITY ? -INFINITY : gm + logf(gs);
+  lse_out[r] = lse;
+  rows_out[r] = labels[r] == ignore_index ? 0.f : lse - zt;
+}
+
 // loss = scale * sum(loss_rows) over all N rows (one workgroup, fixed order);
 // scale = 1/max(n_valid, 1) for the mean, 1 for the sum. Also stores the scale.
 __global__ __launch_bounds__(256) void flce_loss(const float* __restrict__ loss_rows, int64_t N,
@@ -262,13 +332,15 @@ __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int6
                                                     const int64_t* __restrict__ labels,
                                                     int64_t V, int64_t chunks,
                                                     int64_t ignore_index,
-                                                    const float* __restrict__ scale_p) {
+                                                    const float* __restrict__ scale_p,
+                                                    int64_t label_offset) {
   const int64_t r = (int64_t)blockIdx.x / chunks;
   const int64_t c0 = ((int64_t)blockIdx.x % chunks) * (256 * kDlKv) + threadIdx.x;
   const int64_t nvec = V / 8;
-  const int64_t lab = labels[r];
+  const int64_t raw = labels[r];
+  const int64_t lab = raw - label_offset;  // the label's column in these logits
   __bf16* row = L + r * ldl;
-  if (lab == ignore_index) {
+  if (raw == ignore_index) {
     const u32x4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < kDlKv; ++u) {
@@ -503,7 +575,7 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
     if (!grads) continue;
     const int64_t dchunks = (V / 8 + 256 * kDlKv - 1) / (256 * kDlKv);
     hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(Mc * dchunks)), dim3(256), 0, st, Lc, V,
-                       lse_ws + r0, labels + r0, V, dchunks, ignore_index, scale);
+                       lse_ws + r0, labels + r0, V, dchunks, ignore_index, scale, (int64_t)0);
     TS_TRY(ts_host::check_launch("flce_dlogits"));
     using ts_gemm::kKMajor;
     using ts_gemm::kMNMajor;
@@ -547,6 +619,180 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   hipLaunchKernelGGL(flce_loss, dim3(1), dim3(256), 0, st, rows_ws, N, n_valid,
                      reduction == 0 ? 1 : 0, loss, scale);
   return ts_host::check_launch("flce_loss");
+}
+
+// ---------------------------------------------------------------------------
+// Vocabulary-parallel fused linear CE: the two phases one rank runs around the
+// exchange of the per-row partials. The shard's logits [N, Vp] stay in the
+// workspace from phase 1 to phase 2 (no token chunking).
+// ---------------------------------------------------------------------------
+namespace {
+
+struct VocabLayout {
+  int64_t nparts;
+  size_t off_logits, off_stats, off_lse, off_rows, off_misc, total;
+};
+
+VocabLayout vocab_layout(int64_t N, int64_t Vp) {
+  VocabLayout l{};
+  l.nparts = 2 * ((Vp + BN - 1) / BN);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  l.off_logits = take((size_t)N * Vp * 2);
+  l.off_stats = take((size_t)l.nparts * N * sizeof(float2));
+  l.off_lse = take((size_t)N * 4);
+  l.off_rows = take((size_t)N * 4);
+  l.off_misc = take(64);
+  l.total = off;
+  return l;
+}
+
+ts_status check_vocab(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                      const int64_t* labels, int64_t N, int64_t H, int64_t Vp,
+                      int64_t vocab_start, const void* workspace, size_t workspace_bytes,
+                      const char* who) {
+  using ts_host::fail;
+  if (N <= 0 || H <= 0 || Vp <= 0)
+    return fail(TS_ERR_SHAPE, "%s: bad shape N=%lld H=%lld Vp=%lld", who, (long long)N,
+                (long long)H, (long long)Vp);
+  if (N % 8 != 0 || H % 8 != 0 || Vp % 8 != 0)
+    return fail(TS_ERR_SHAPE, "%s: N, H and Vp must be multiples of 8", who);
+  if (ldh < H || ldw < H || ldh % 8 != 0 || ldw % 8 != 0)
+    return fail(TS_ERR_SHAPE, "%s: row strides must be >= H and multiples of 8", who);
+  // 32-bit buffer offsets, as for ts_flce_fwd_bwd (here the logits' row stride is Vp)
+  if (Vp > ((int64_t)1 << 22) || H > ((int64_t)1 << 20) || N > ((int64_t)1 << 22) ||
+      ldh > ((int64_t)1 << 22) || ldw > ((int64_t)1 << 22))
+    return fail(TS_ERR_SHAPE, "%s: shape beyond the kernel's index range", who);
+  if (vocab_start < 0) return fail(TS_ERR_INVALID_ARGUMENT, "%s: vocab_start < 0", who);
+  if (hidden == nullptr || weight == nullptr || labels == nullptr)
+    return fail(TS_ERR_INVALID_ARGUMENT, "%s: hidden, weight or labels is NULL", who);
+  if (!ts_host::aligned16(hidden) || !ts_host::aligned16(weight))
+    return fail(TS_ERR_INVALID_ARGUMENT, "%s: tensors must be 16-byte aligned", who);
+  const VocabLayout lay = vocab_layout(N, Vp);
+  if (workspace == nullptr || workspace_bytes < lay.total || !ts_host::aligned16(workspace))
+    return fail(TS_ERR_WORKSPACE, "%s: workspace needs %zu bytes (16-byte aligned), got %zu", who,
+                lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
+  return TS_OK;
+}
+
+}  // namespace
+
+extern "C" size_t ts_flce_vocab_workspace_size(int64_t N, int64_t Vp) {
+  if (N <= 0 || Vp <= 0) return 0;
+  return vocab_layout(N, Vp).total;
+}
+
+extern "C" ts_status ts_flce_vocab_fwd(const void* hidden, int64_t ldh, const void* weight,
+                                       int64_t ldw, const int64_t* labels, int64_t N, int64_t H,
+                                       int64_t Vp, int64_t vocab_start, float* stats,
+                                       void* workspace, size_t workspace_bytes,
+                                       ts_stream_t stream) {
+  TS_TRY(check_vocab(hidden, ldh, weight, ldw, labels, N, H, Vp, vocab_start, workspace,
+                     workspace_bytes, "flce_vocab_fwd"));
+  if (stats == nullptr || !ts_host::aligned16(stats))
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "flce_vocab_fwd: stats NULL or unaligned");
+  const VocabLayout lay = vocab_layout(N, Vp);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  __bf16* L = reinterpret_cast<__bf16*>(ws + lay.off_logits);
+  float2* part = reinterpret_cast<float2*>(ws + lay.off_stats);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  GemmArgs g{};
+  g.A = static_cast<const __bf16*>(hidden);
+  g.lda = ldh;
+  g.B = static_cast<const __bf16*>(weight);
+  g.ldb = ldw;
+  g.M = N;
+  g.N = Vp;
+  g.K = H;
+  g.C = L;
+  g.ldc = Vp;
+  g.stats = part;
+  TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_vocab_gemm_logits"));
+  hipLaunchKernelGGL(flce_shard_rows, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, part,
+                     lay.nparts, L, Vp, labels, N, Vp, vocab_start,
+                     reinterpret_cast<ShardStats*>(stats));
+  return ts_host::check_launch("flce_shard_rows");
+}
+
+extern "C" ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const void* weight,
+                                       int64_t ldw, const int64_t* labels, int64_t N, int64_t H,
+                                       int64_t Vp, int64_t vocab_start, const float* stats_all,
+                                       int64_t P, int64_t ignore_index, int32_t reduction,
+                                       float* loss, float* loss_rows, float* lse,
+                                       void* grad_hidden_partial, void* grad_weight_shard,
+                                       void* workspace, size_t workspace_bytes,
+                                       ts_stream_t stream) {
+  using ts_host::fail;
+  TS_TRY(check_vocab(hidden, ldh, weight, ldw, labels, N, H, Vp, vocab_start, workspace,
+                     workspace_bytes, "flce_vocab_bwd"));
+  if (P < 1 || P > ((int64_t)1 << 20))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_vocab_bwd: bad rank count %lld", (long long)P);
+  if (stats_all == nullptr || !ts_host::aligned16(stats_all))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_vocab_bwd: stats_all NULL or unaligned");
+  if (reduction != 0 && reduction != 1)
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_vocab_bwd: reduction must be 0 (mean) or 1 (sum)");
+  if (loss == nullptr) return fail(TS_ERR_INVALID_ARGUMENT, "flce_vocab_bwd: loss is NULL");
+  if ((grad_hidden_partial != nullptr && !ts_host::aligned16(grad_hidden_partial)) ||
+      (grad_weight_shard != nullptr && !ts_host::aligned16(grad_weight_shard)))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_vocab_bwd: gradients must be 16-byte aligned");
+  const VocabLayout lay = vocab_layout(N, Vp);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  __bf16* L = reinterpret_cast<__bf16*>(ws + lay.off_logits);
+  float* lse_ws = lse != nullptr ? lse : reinterpret_cast<float*>(ws + lay.off_lse);
+  float* rows_ws = loss_rows != nullptr ? loss_rows : reinterpret_cast<float*>(ws + lay.off_rows);
+  int* n_valid = reinterpret_cast<int*>(ws + lay.off_misc);
+  float* scale = reinterpret_cast<float*>(ws + lay.off_misc + 16);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  hipLaunchKernelGGL(flce_count, dim3(1), dim3(256), 0, st, labels, N, ignore_index, n_valid);
+  TS_TRY(ts_host::check_launch("flce_count"));
+  hipLaunchKernelGGL(flce_vocab_merge, dim3((unsigned)((N + 63) / 64)), dim3(64), 0, st,
+                     reinterpret_cast<const ShardStats*>(stats_all), P, N, labels, ignore_index,
+                     lse_ws, rows_ws);
+  TS_TRY(ts_host::check_launch("flce_vocab_merge"));
+  hipLaunchKernelGGL(flce_loss, dim3(1), dim3(256), 0, st, rows_ws, N, n_valid,
+                     reduction == 0 ? 1 : 0, loss, scale);
+  TS_TRY(ts_host::check_launch("flce_loss"));
+  if (grad_hidden_partial == nullptr && grad_weight_shard == nullptr) return TS_OK;
+  const int64_t dchunks = (Vp / 8 + 256 * kDlKv - 1) / (256 * kDlKv);
+  hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(N * dchunks)), dim3(256), 0, st, L, Vp,
+                     lse_ws, labels, Vp, dchunks, ignore_index, scale, vocab_start);
+  TS_TRY(ts_host::check_launch("flce_dlogits"));
+  const __bf16* Hd = static_cast<const __bf16*>(hidden);
+  const __bf16* Wd = static_cast<const __bf16*>(weight);
+  using ts_gemm::kKMajor;
+  using ts_gemm::kMNMajor;
+  if (grad_hidden_partial != nullptr) {
+    GemmArgs d{};
+    d.A = L;  // dlogits [N, Vp], K-major
+    d.lda = Vp;
+    d.B = Wd;  // weight shard [Vp, H] as the [H, Vp] operand: MN-major
+    d.ldb = ldw;
+    d.M = N;
+    d.N = H;
+    d.K = Vp;
+    d.C = static_cast<__bf16*>(grad_hidden_partial);
+    d.ldc = H;
+    TS_TRY((launch_gemm<kEpiBf16, kKMajor, kMNMajor>(d, st, "flce_vocab_gemm_dhidden")));
+  }
+  if (grad_weight_shard != nullptr) {
+    GemmArgs d{};
+    d.A = L;  // dlogits [N, Vp] as the [Vp, N] operand: MN-major
+    d.lda = Vp;
+    d.B = Hd;  // hidden [N, H] as the [H, N] operand: MN-major
+    d.ldb = ldh;
+    d.M = Vp;
+    d.N = H;
+    d.K = N;
+    d.C = static_cast<__bf16*>(grad_weight_shard);
+    d.ldc = H;
+    TS_TRY((launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(d, st, "flce_vocab_gemm_dweight")));
+  }
+  return TS_OK;
 }
 
 namespace {

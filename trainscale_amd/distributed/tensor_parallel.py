@@ -29,10 +29,15 @@ import torch
 from torch import Tensor
 
 from .. import ops
+from ..loss.linear_ce import linear_ce_vocab_phase1, linear_ce_vocab_phase2
 
 
 def _local_gather(stats: Tensor) -> Tensor:
     return stats.unsqueeze(0)
+
+
+def _identity(t: Tensor) -> Tensor:
+    return t
 
 
 @dataclass
@@ -40,11 +45,13 @@ class VocabShardExchange:
     """How this rank obtains every rank's partials.
 
     gather(stats [N, 4]) returns [world_size, N, 4], rank-major, with this rank's
-    own partials at index ``rank``.
+    own partials at index ``rank``. reduce_sum(t) returns the sum of t over the
+    ranks (the vocabulary-parallel linear CE's grad_hidden partials).
     """
     gather: Callable[[Tensor], Tensor] = _local_gather
     rank: int = 0
     world_size: int = 1
+    reduce_sum: Callable[[Tensor], Tensor] = _identity
 
 
 _exchange = VocabShardExchange()
@@ -118,3 +125,49 @@ def vocab_parallel_cross_entropy(logits: Tensor, targets: Tensor,
     vocab_start = get_tensor_parallel_rank() * vp
     return VocabParallelCrossEntropyLoss.apply(logits, targets, vocab_start, vocab_start + vp,
                                                label_smoothing)
+
+
+class VocabParallelLinearCrossEntropyFunction(torch.autograd.Function):
+    """CE of hidden @ weight_shard.T over a vocabulary split across ranks, each rank
+    holding the LM head rows vocab_start .. vocab_start + Vp - 1, with the
+    gradients formed in the forward (upstream gradient 1) and scaled in the
+    backward. The ranks exchange one 16-byte partial per row and sum their
+    grad_hidden partials (the exchange hooks); grad_weight stays local."""
+
+    @staticmethod
+    def forward(ctx, hidden: Tensor, weight_shard: Tensor, labels: Tensor, vocab_start: int,
+                ignore_index: int = -100, reduction: str = "mean") -> Tensor:
+        shape = hidden.shape
+        ex = _exchange
+        stats, state = linear_ce_vocab_phase1(hidden.reshape(-1, shape[-1]), weight_shard,
+                                              labels, vocab_start)
+        stats_all = ex.gather(stats) if ex.world_size > 1 else stats.unsqueeze(0)
+        loss, _, _, gh, gw = linear_ce_vocab_phase2(
+            state, stats_all, ignore_index, reduction,
+            need_grad_hidden=ctx.needs_input_grad[0], need_grad_weight=ctx.needs_input_grad[1])
+        if gh is not None and ex.world_size > 1:
+            gh = ex.reduce_sum(gh)
+        ctx.hidden_shape = shape
+        ctx.save_for_backward(gh, gw)
+        return loss
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        gh, gw = ctx.saved_tensors
+        scale = grad_output.detach().float().reshape(1).contiguous()
+        if gh is not None:
+            ops.scale_(gh, scale)
+        if gw is not None:
+            ops.scale_(gw, scale)
+        gh = gh.view(ctx.hidden_shape) if gh is not None else None
+        return gh, gw, None, None, None, None
+
+
+def vocab_parallel_linear_cross_entropy(hidden: Tensor, weight_shard: Tensor, labels: Tensor,
+                                        ignore_index: int = -100,
+                                        reduction: str = "mean") -> Tensor:
+    """Mean (or sum) CE of hidden @ lm_head.T with this rank's LM head rows
+    weight_shard [Vp, H] (vocabulary columns rank * Vp .. (rank + 1) * Vp - 1)."""
+    vocab_start = get_tensor_parallel_rank() * weight_shard.shape[0]
+    return VocabParallelLinearCrossEntropyFunction.apply(hidden, weight_shard, labels,
+                                                         vocab_start, ignore_index, reduction)

@@ -24,7 +24,8 @@ from torch import Tensor
 from .. import _lib, ops
 from .._lib import check, ptr
 
-__all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy", "DEFAULT_LOGITS_SCRATCH"]
+__all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy", "DEFAULT_LOGITS_SCRATCH",
+           "VocabShardState", "linear_ce_vocab_phase1", "linear_ce_vocab_phase2"]
 
 # Upper bound on the bf16 logits scratch of one token chunk. 4 GiB keeps a
 # batch of up to 16384 tokens at V = 128256 in one chunk (one grad-weight GEMM
@@ -85,6 +86,90 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
             ptr(hidden), ldh, ptr(weight), ldw, ptr(labels), N, H, V, int(ignore_index),
             _REDUCTIONS[reduction], ptr(loss), ptr(loss_rows), ptr(lse), ptr(gh), ptr(gw),
             chunk, ptr(ws), ws_bytes, _lib.stream_handle(dev)), "ts_flce_fwd_bwd")
+    return loss, loss_rows, lse, gh, gw
+
+
+class VocabShardState:
+    """What phase 2 of the vocabulary-parallel linear CE needs from phase 1: the
+    rank's operands and the workspace that holds its shard's logits."""
+
+    def __init__(self, hidden, weight, labels, vocab_start, ws, ws_bytes, dev):
+        self.hidden, self.weight, self.labels = hidden, weight, labels
+        self.vocab_start, self.ws, self.ws_bytes, self.dev = vocab_start, ws, ws_bytes, dev
+        self.N, self.H = hidden.shape
+        self.Vp = weight.shape[0]
+        self.ldh = hidden.stride(0) if self.N > 1 else self.H
+        self.ldw = weight.stride(0) if self.Vp > 1 else self.H
+
+
+def _rows_operand(t: Tensor) -> Tensor:
+    if t.stride(1) != 1 or (t.shape[0] > 1 and t.stride(0) % 8 != 0):
+        t = t.contiguous()
+    return t
+
+
+def linear_ce_vocab_phase1(hidden: Tensor, weight_shard: Tensor, labels: Tensor,
+                           vocab_start: int):
+    """ts_flce_vocab_fwd: this rank's logits over its shard of the LM head (kept in the
+    workspace) and its per-row partials [N, 4] fp32, the tensor the ranks exchange.
+    Returns (partials, state)."""
+    dev = _lib.require_gpu("vocab_parallel_linear_cross_entropy", hidden, weight_shard, labels)
+    if hidden.dtype != torch.bfloat16 or weight_shard.dtype != torch.bfloat16:
+        raise TypeError("vocab_parallel_linear_cross_entropy: hidden and weight must be bfloat16")
+    if hidden.dim() != 2 or weight_shard.dim() != 2 or hidden.shape[1] != weight_shard.shape[1]:
+        raise ValueError(f"vocab_parallel_linear_cross_entropy: hidden {tuple(hidden.shape)} and "
+                         f"weight {tuple(weight_shard.shape)} must be [N, H] and [Vp, H]")
+    hidden, weight_shard = _rows_operand(hidden), _rows_operand(weight_shard)
+    N = hidden.shape[0]
+    labels = labels.reshape(-1)
+    if labels.shape[0] != N:
+        raise ValueError(f"vocab_parallel_linear_cross_entropy: {labels.shape[0]} labels for "
+                         f"{N} rows")
+    labels = labels.to(torch.int64).contiguous()
+    lib = _lib.load()
+    ws_bytes = int(lib.ts_flce_vocab_workspace_size(N, weight_shard.shape[0]))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    state = VocabShardState(hidden, weight_shard, labels, int(vocab_start), ws, ws_bytes, dev)
+    stats = torch.empty((N, 4), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.ts_flce_vocab_fwd(ptr(hidden), state.ldh, ptr(weight_shard), state.ldw,
+                                    ptr(labels), N, state.H, state.Vp, state.vocab_start,
+                                    ptr(stats), ptr(ws), ws_bytes, _lib.stream_handle(dev)),
+              "ts_flce_vocab_fwd")
+    return stats, state
+
+
+def linear_ce_vocab_phase2(state: VocabShardState, stats_all: Tensor, ignore_index: int = -100,
+                           reduction: str = "mean", need_grad_hidden: bool = True,
+                           need_grad_weight: bool = True):
+    """ts_flce_vocab_bwd from every rank's partials [P, N, 4]: returns (loss, loss_rows,
+    lse, grad_hidden_partial [N, H] or None, grad_weight_shard [Vp, H] or None) for an
+    upstream gradient of 1; grad_hidden_partial is this rank's term of the sum over ranks."""
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f"vocab_parallel_linear_cross_entropy: reduction must be 'mean' or "
+                         f"'sum', got {reduction!r}")
+    if (stats_all.dim() != 3 or stats_all.shape[1] != state.N or stats_all.shape[2] != 4 or
+            stats_all.dtype != torch.float32):
+        raise ValueError(f"vocab_parallel_linear_cross_entropy: partials must be fp32 "
+                         f"[P, {state.N}, 4], got {stats_all.dtype} {tuple(stats_all.shape)}")
+    stats_all = stats_all.contiguous()
+    dev = state.dev
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    loss_rows = torch.empty((state.N,), dtype=torch.float32, device=dev)
+    lse = torch.empty((state.N,), dtype=torch.float32, device=dev)
+    gh = (torch.empty((state.N, state.H), dtype=torch.bfloat16, device=dev)
+          if need_grad_hidden else None)
+    gw = (torch.empty((state.Vp, state.H), dtype=torch.bfloat16, device=dev)
+          if need_grad_weight else None)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        check(lib.ts_flce_vocab_bwd(ptr(state.hidden), state.ldh, ptr(state.weight), state.ldw,
+                                    ptr(state.labels), state.N, state.H, state.Vp,
+                                    state.vocab_start, ptr(stats_all), stats_all.shape[0],
+                                    int(ignore_index), _REDUCTIONS[reduction], ptr(loss),
+                                    ptr(loss_rows), ptr(lse), ptr(gh), ptr(gw), ptr(state.ws),
+                                    state.ws_bytes, _lib.stream_handle(dev)),
+              "ts_flce_vocab_bwd")
     return loss, loss_rows, lse, gh, gw
 
 
