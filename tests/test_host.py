@@ -41,7 +41,7 @@ def test_as_rows_strides():
     assert ld == 16 and v.is_contiguous()
 
 
-def test_survey_byte_counts():
+def test_config_byte_counts():
     # compulsory traffic quoted for the configs (fwd + bwd)
     b = W.rmsnorm_bytes(16384, 4096)
     assert b["fwd"] == 268_509_184 and b["fwd"] + b["bwd"] == 671_244_288
