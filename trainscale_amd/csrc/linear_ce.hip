@@ -175,14 +175,15 @@ void flce_gemm(const GemmArgs a) {
       if constexpr (kMode == kEpiLogits) {
         float f[8];
         Elt<__bf16>::unpack(v, f);
-        float lm = -INFINITY;
+        float lm = f[0];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) lm = in ? fmaxf(lm, f[q]) : lm;
-        const float m = row_max(lm);  // over the 16 lanes of this row
+        for (int q = 1; q < 8; ++q) lm = fmaxf(lm, f[q]);
+        const float m = row_max(in ? lm : -INFINITY);  // over the 16 lanes of this row
         float ls = 0.f;
         if (in) {
+          const float mb = m * kLog2e;
 #pragma unroll
-          for (int q = 0; q < 8; ++q) ls += fast_exp2((f[q] - m) * kLog2e);
+          for (int q = 0; q < 8; ++q) ls += fast_exp2(__builtin_fmaf(f[q], kLog2e, -mb));
         }
         const float s = row_sum(ls);
         if (gm < a.M && c16 == 0) a.stats[gm * nparts + nt * 2 + wn] = make_float2(m, s);
