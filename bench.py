@@ -110,7 +110,7 @@ def cpu_baseline(budget_s: float):
         t0 = time.perf_counter()
         one()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 50:
+        if time.perf_counter() - t_start > budget_s or len(times) >= 1000:
             break
     times.sort()
     t = times[len(times) // 2]
@@ -126,8 +126,20 @@ def cpu_baseline(budget_s: float):
         "sample": (f"oracle (torch CPU fp32 restatement of the reference math) fwd+bwd on "
                    f"C1 {rows1} rows x 4096, C2 {tok2} tokens x (32+8) heads x 128, "
                    f"C3 {rows3} rows x 128256; median of {len(times)} runs, "
-                   f"{t * 1e3:.1f} ms per sample; CPU {platform.processor() or platform.machine()}"),
+                   f"{t * 1e3:.1f} ms per sample; CPU {cpu_model()}"),
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the machine type."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline_linear_ce(budget_s: float):
@@ -148,7 +160,7 @@ def cpu_baseline_linear_ce(budget_s: float):
         t0 = time.perf_counter()
         oracle.linear_ce(hid, wt, lab, bf16_logits=True)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
+        if time.perf_counter() - t_start > budget_s or len(times) >= 100:
             break
     times.sort()
     t = times[len(times) // 2]
@@ -156,7 +168,7 @@ def cpu_baseline_linear_ce(budget_s: float):
     return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s",
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"oracle linear_ce fwd+bwd on 64 tokens of C5 (H 4096, V 128256); "
-                      f"median of {len(times)} runs, {t:.2f} s per sample"}
+                      f"median of {len(times)} runs, {t:.2f} s per sample; CPU {cpu_model()}"}
 
 
 def time_ms(fn, steps: int, warmup: int) -> float:
