@@ -498,15 +498,19 @@ __global__ __launch_bounds__(kFusedThreads) void ce_fused_vec(
     loss[row] = out;
     lse_out[row] = l;
   }
-  const float dl = dloss[row * dloss_stride] * dloss_scale;
+  // One upstream gradient per row, moved to a scalar register: its sign below
+  // is then a wave-uniform mask (one XOR per packed dword, no per-lane select).
+  const float dl = __builtin_bit_cast(
+      float, __builtin_amdgcn_readfirstlane(
+                 __builtin_bit_cast(int, dloss[row * dloss_stride] * dloss_scale)));
   if constexpr (!kXform && !kSmooth) {
     const float adl = fabsf(dl);
     const float l2 = l * kLog2e;
     const float l2d = l2 - __builtin_amdgcn_logf(adl);  // v_log_f32 is log2
-    // The sign of dl and the position of the label are uniform over the
-    // workgroup: both corrections are uniform branches, and only the lane
-    // holding the label runs its correction.
-    const bool neg = (__builtin_bit_cast(uint32_t, dl) >> 31) != 0;
+    // The position of the label is uniform over the workgroup: its
+    // correction is a uniform branch, and only the lane holding the label
+    // runs it.
+    const uint32_t smask = (__builtin_bit_cast(uint32_t, dl) >> 31) != 0 ? sign_bits<G>() : 0u;
     const int64_t lv = label >= 0 && label < V ? label / VE : -1;  // vector holding the label
     const int klab = lv < 0 ? -1 : (int)(lv / kFusedThreads);
     const int tlab = lv < 0 ? -1 : (int)(lv % kFusedThreads);
@@ -525,15 +529,13 @@ __global__ __launch_bounds__(kFusedThreads) void ce_fused_vec(
       const int off = fused_voff(k, nvec, kGradBytes);
       if constexpr (kGradBytes == 32) {
         u32x4 p0 = Elt<float>::pack(g), p1 = Elt<float>::pack(g + 4);
-        if (neg) {
-          p0 ^= sign_bits<G>();
-          p1 ^= sign_bits<G>();
-        }
+        p0 ^= smask;
+        p1 ^= smask;
         buf_st16_stream(p0, go, off);
         buf_st16_stream(p1, go, off + 16);
       } else {
         u32x4 p = Elt<G>::pack(g);
-        if (neg) p ^= sign_bits<G>();
+        p ^= smask;
         buf_st16_stream(p, go, off);
       }
     }
