@@ -361,6 +361,31 @@ def test_c3_full_fused(gpu):
     torch.testing.assert_close(loss, l2, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("V", [4096, 128256])
+@pytest.mark.parametrize("grad_dtype", [BF, torch.float32])
+def test_fused_per_row_upstream_signs(gpu, V, grad_dtype):
+    """Schedule B with one upstream gradient per row: negative, positive, +0, -0 and
+    large values. The kernel applies the row's sign to the packed gradient words,
+    so a row's sign must never leak into another row."""
+    torch.manual_seed(V + 3)
+    N = 24
+    logits = (2 * torch.randn(N, V, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[5] = -100
+    dl = torch.randn(N, device=gpu)
+    dl[0], dl[1], dl[2], dl[3] = 0.0, -0.0, -3.5, 1e3
+    loss, _, grad = ops.ce_forward_backward(logits, V, labels, dl, 0.5, grad_dtype=grad_dtype)
+    ref, _ = oracle.ce_fwd(logits.cpu(), labels.cpu())
+    torch.testing.assert_close(loss.cpu(), ref, rtol=1e-5, atol=1e-6)
+    ref_g = oracle.ce_bwd(logits.cpu(), labels.cpu(), 0.5 * dl.cpu(), out_dtype=torch.float32)
+    if grad_dtype == torch.float32:
+        torch.testing.assert_close(grad.cpu(), ref_g, rtol=2e-5, atol=1e-30)
+    else:
+        assert_ulp(grad, ref_g, 1, tiny=TINY)
+    signs = torch.sign(grad.float().cpu()) * torch.sign(ref_g)
+    assert bool((signs >= 0).all())  # no element has the opposite sign
+
+
 def test_upstream_grad_hint_across_steps(gpu):
     """A loss scaled the same way every step (1/4, as with 4 accumulation steps): the
     first backward rescales the gradient formed for 1, later steps form it for 1/4
