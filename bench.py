@@ -269,9 +269,9 @@ def bench_packed(dev, steps: int, warmup: int):
 
 
 def bench_next_rows(dev, steps: int, warmup: int):
-    """Rows beyond the hot path's five configs: fused residual add + RMSNorm forward at
+    """Rows beyond the headline step: fused residual add + RMSNorm forward at
     the C1 and C4 shapes, SwiGLU forward + backward at the Llama-3-8B MLP shape
-    [8, 2048, 14336], and one rank's vocabulary-parallel CE kernels at C3 / 8 ranks and fused
+    [8, 2048, 14336], the two-pass CE of Fast_CrossEntropyLoss at C3, and one rank's vocabulary-parallel CE kernels at C3 / 8 ranks and fused
     linear-CE phases at C5 / 8 ranks.
     Synthetic seeded inputs, each op timed alone."""
     import torch
@@ -305,6 +305,27 @@ def bench_next_rows(dev, steps: int, warmup: int):
                      "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
                      "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del gate, up, dout
+    # The reference's own CE contract at C3 (Fast_CrossEntropyLoss, schedule A): the
+    # forward reads each labelled row for loss and lse; the backward reads it again
+    # and writes every row's gradient. Written to a separate buffer here so that every
+    # repeat sees the same logits; the bytes are those of the in-place contract.
+    c3 = W.ce_workload(dev)
+    logits, labels = c3.tensors["logits"], c3.tensors["labels"]
+    N3, V3 = logits.shape
+    n_valid = int((labels != -100).sum())
+    _, lse3 = ops.ce_forward(logits, V3, labels)
+    g3 = torch.empty_like(logits)
+    scale3 = torch.tensor([1.0 / n_valid], device=dev)
+    cb = W.ce_bytes(N3, n_valid, V3)
+    for name, fn, b in (
+            ("ce_fwd_schedule_a", lambda: ops.ce_forward(logits, V3, labels), cb["fwd"]),
+            ("ce_bwd_schedule_a",
+             lambda: ops.ce_backward(logits, V3, labels, lse3, scale3, g3, V3), cb["bwd"])):
+        ms = time_ms(fn, steps, warmup)
+        res[name] = {"shape": [N3, V3], "ms": round(ms, 4), "bytes": b,
+                     "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del c3, logits, labels, lse3, g3
     # Vocabulary-parallel CE: one rank's kernels at C3 split over 8 ranks, a
     # [16384, 16032] bf16 shard (the merge reads 8 ranks' partials).
     N, P = 16384, 8
