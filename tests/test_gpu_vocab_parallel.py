@@ -211,3 +211,30 @@ def test_linear_ce_single_rank_autograd_equals_fused():
         res.append((loss.detach(), hg.grad, wg.grad))
     assert torch.equal(res[0][0], res[1][0])
     assert torch.equal(res[0][1], res[1][1]) and torch.equal(res[0][2], res[1][2])
+
+
+def test_linear_ce_ranks_at_c5_over_8_ranks():
+    """The per-rank shape the bench measures: C5 (hidden [8192, 4096], LM head
+    [128256, 4096], 5% ignored) split over 8 ranks of [16032, 4096]. Every rank's two
+    phases against the full single-GPU kernel (pinned to the oracle at this size in
+    test_gpu_linear_ce.py::test_c5_full): the same loss, per-row loss and lse, the ranks'
+    grad_hidden partials summing to its grad_hidden, and its grad_weight rows per shard."""
+    from trainscale_amd import workloads
+    from trainscale_amd.loss.linear_ce import linear_ce_forward_backward
+    wl = workloads.linear_ce_workload(torch.device("cuda"))
+    h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
+    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels)
+    P = 8
+    vp = w.shape[0] // P
+    outs = lce_ranks(h, w, labels, P)
+    for p, (lp, rp, lsep, _, gwp) in enumerate(outs):
+        assert abs(lp.item() - loss.item()) <= 2e-6 * abs(loss.item()), p
+        torch.testing.assert_close(lsep, lse, rtol=2e-6, atol=0)
+        torch.testing.assert_close(rp, rows, rtol=2e-5, atol=2e-5)
+        d = (gwp.float() - gw[p * vp:(p + 1) * vp].float()).abs()
+        assert float(d.max()) <= 2e-2, p
+        assert float(d.norm() / gw[p * vp:(p + 1) * vp].float().norm()) <= 1e-2, p
+    gh_sum = sum(o[3].float() for o in outs)
+    d = (gh_sum - gh.float()).abs()
+    assert float(d.max()) <= 2e-2
+    assert float(d.norm() / gh.float().norm()) <= 1e-2
