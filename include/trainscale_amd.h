@@ -204,7 +204,7 @@ ts_status ts_rope_apply(const void* q_in, void* q_out,
  *   z = softcap != 0 ? softcap * tanh(z / softcap) : z
  *   lse[r] = log(sum_j exp(z_j))                      (fp32, online max)
  *   loss[r] = (1-a)*(lse - z[label]) + a*(lse - mean_j z_j), a = label_smoothing
- *   loss[r] = 0 (and lse still written) when labels[r] == ignore_index.
+ *   loss[r] = 0 and lse[r] = 0 when labels[r] == ignore_index (the row is not read).
  * labels: int64 [N], device. Labels outside [0, V) other than ignore_index
  * give loss NaN for that row.
  * Replaces _cross_entropy_forward_kernel/_chunked_cross_entropy_forward_kernel
@@ -383,9 +383,9 @@ ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight, i
                           void* workspace, size_t workspace_bytes, ts_stream_t stream);
 
 /*
- * x[i] *= *scale for n values of `dtype` (n a multiple of 16 bytes' worth of
- * elements, x 16-byte aligned); scale is a device pointer, and when
- * *scale == 1 nothing is written. Applies an upstream gradient other than 1
+ * x[i] *= *scale for n contiguous values of `dtype` (any n >= 0; 16-byte
+ * vectors where x is 16-byte aligned, single elements for the rest); scale
+ * is a device pointer, and when *scale == 1 nothing is written. Applies an upstream gradient other than 1
  * to gradients formed in a forward pass (ts_ce_fwd_bwd, ts_flce_fwd_bwd)
  * without a host synchronisation. Has no counterpart in the reference, whose
  * backward passes receive the upstream gradient directly.

@@ -182,7 +182,8 @@ def test_flce_vocab_validation(lib):
 
 def test_scale_and_rescale_validation(lib):
     st = NULL
-    assert lib.ts_scale_inplace(FAKE, 12, 1, FAKE, st) == SHAPE
+    assert lib.ts_scale_inplace(FAKE, -1, 1, FAKE, st) == SHAPE
+    assert lib.ts_scale_inplace(NULL, 12, 1, FAKE, st) == INVALID
     assert lib.ts_scale_inplace(FAKE, 16, 9, FAKE, st) == DTYPE
     assert lib.ts_scale_inplace(FAKE, 16, 1, NULL, st) == INVALID
     assert lib.ts_rescale_inplace(FAKE, 16, 1, FAKE, NULL, NULL, st) == INVALID

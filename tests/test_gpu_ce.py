@@ -426,3 +426,47 @@ def test_rescale_inplace_ratio_and_hint(gpu):
     now.fill_(float("inf"))
     ops.rescale_(t[:0], now, used, hint)  # empty tensor: only the hint is written
     assert hint.item() == 1.0
+
+
+@pytest.mark.parametrize("mod_cls", [FusedCrossEntropyLoss, ChunkedCrossEntropyLoss,
+                                     CrossEntropyLoss])
+def test_odd_sizes_through_modules_with_upstream_grad(gpu, mod_cls):
+    # N * V = 5 * 37 elements: not a whole number of 16-byte vectors, so the in-place
+    # application of the upstream gradient runs its element-wise tail
+    g = golden("ce_odd_v")
+    x = torch.from_numpy(g["logits"]).to(BF).to(gpu).requires_grad_()
+    labels = torch.from_numpy(g["labels"]).to(gpu)
+    mod = mod_cls()
+    loss = mod(x, labels)
+    assert abs(loss.item() - float(g["mean_loss"])) <= 1e-5 * float(g["mean_loss"])
+    (2.5 * loss).backward()
+    assert_ulp(x.grad, round_to(2.5 * g["grad"], BF), 1, tiny=TINY, what=mod_cls.__name__)
+    # a second step with another upstream gradient (the hint's correction path)
+    x2 = torch.from_numpy(g["logits"]).to(BF).to(gpu).requires_grad_()
+    (-0.75 * mod(x2, labels)).backward()
+    assert_ulp(x2.grad, round_to(-0.75 * g["grad"], BF), 1, tiny=TINY, what=mod_cls.__name__)
+
+
+def test_scale_inplace_unaligned_and_tails(gpu):
+    for n, off in ((185, 0), (1000, 1), (4099, 3), (7, 0)):
+        base = torch.randn(n + off + 5, device=gpu).to(BF)
+        before = base.clone()
+        t = base[off:off + n]
+        ops.scale_(t, torch.tensor([3.0], device=gpu))
+        assert torch.equal(t, (before[off:off + n].float() * 3.0).to(BF)), (n, off)
+        # nothing outside the view is written
+        assert torch.equal(base[:off], before[:off]) and torch.equal(base[off + n:],
+                                                                     before[off + n:])
+
+
+@pytest.mark.parametrize("red", ["mean", "sum"])
+def test_second_backward_is_refused(gpu, red):
+    torch.manual_seed(3)
+    logits = (2 * torch.randn(64, 1000, device=gpu)).to(BF).requires_grad_()
+    labels = torch.randint(0, 1000, (64,), device=gpu)
+    loss = ChunkedCrossEntropyLoss(reduction=red)(logits, labels)
+    loss.backward(retain_graph=True)
+    first = logits.grad.clone()
+    with pytest.raises(RuntimeError, match="second time"):
+        loss.backward()
+    assert torch.equal(logits.grad, first)

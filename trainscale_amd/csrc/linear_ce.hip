@@ -381,17 +381,18 @@ __global__ __launch_bounds__(256) void fill_zero_u32(uint32_t* __restrict__ p, i
   if (i == 0 && loss != nullptr) *loss = 0.f;
 }
 
-// x[i] *= *scale unless *scale == 1, over nvec 16-byte vectors of element
-// type T. The grid is capped (kScaleGrid workgroups, each thread four vectors
-// per sweep) so that the common no-op case, an upstream gradient of exactly
-// 1, costs little more than a launch.
+// x[i] *= *scale unless *scale == 1, over n elements of type T: nvec 16-byte
+// vectors from x (x 16-byte aligned when nvec > 0), then the n - nvec * VE
+// elements after them one at a time. The grid is capped (kScaleGrid
+// workgroups, each thread four vectors per sweep) so that the common no-op
+// case, an upstream gradient of exactly 1, costs little more than a launch.
 constexpr int kScaleGrid = 2048;
 constexpr int kScaleUnroll = 4;
 // The factor is *num, or *num / *den when den is given. With hint_out, the
 // first thread also stores *num there when it is finite and non-zero (else
 // 1): the prediction a later forward pass uses for the upstream gradient.
 template <typename T>
-__global__ __launch_bounds__(256) void scale_inplace(T* __restrict__ x, int64_t nvec,
+__global__ __launch_bounds__(256) void scale_inplace(T* __restrict__ x, int64_t nvec, int64_t n,
                                                      const float* __restrict__ num,
                                                      const float* __restrict__ den,
                                                      float* __restrict__ hint_out) {
@@ -422,6 +423,10 @@ __global__ __launch_bounds__(256) void scale_inplace(T* __restrict__ x, int64_t 
       }
     }
   }
+  // elements after the last whole vector (all of them when x is not 16-byte aligned)
+  for (int64_t i = nvec * VE + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256)
+    Elt<T>::store1(x + i, Elt<T>::load1(x + i) * s);
 }
 
 // ---------------------------------------------------------------------------
@@ -801,32 +806,33 @@ ts_status scale_launch(const char* what, void* x, int64_t n, ts_dtype dtype, con
                        const float* den, float* hint_out, hipStream_t st) {
   if (!ts_host::valid_dtype(dtype))
     return ts_host::fail(TS_ERR_UNSUPPORTED_DTYPE, "%s: bad dtype", what);
-  const int64_t per = dtype == TS_F32 ? 4 : 8;
-  if (n < 0 || n % per != 0)
-    return ts_host::fail(TS_ERR_SHAPE, "%s: n must be a non-negative multiple of %lld", what,
-                         (long long)per);
+  if (n < 0) return ts_host::fail(TS_ERR_SHAPE, "%s: n must be non-negative", what);
   if (num == nullptr) return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "%s: NULL factor", what);
-  if (n > 0 && (x == nullptr || !ts_host::aligned16(x)))
-    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "%s: bad pointer", what);
+  if (n > 0 && x == nullptr) return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "%s: NULL x", what);
   if (hint_out != nullptr && (hint_out == num || hint_out == den))
     return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "%s: hint_out aliases an input", what);
   if (n == 0 && hint_out == nullptr) return TS_OK;
-  const int64_t nvec = n / per;
+  const int64_t per = dtype == TS_F32 ? 4 : 8;
+  // whole 16-byte vectors when x is aligned; the rest element by element
+  const int64_t nvec = ts_host::aligned16(x) ? n / per : 0;
+  const int64_t tail = n - nvec * per;
   int64_t blocks = (nvec + 256 * kScaleUnroll - 1) / (256 * kScaleUnroll);
+  const int64_t tail_blocks = (tail + 255) / 256;
+  if (tail_blocks > blocks) blocks = tail_blocks;
   if (blocks > kScaleGrid) blocks = kScaleGrid;
   if (blocks < 1) blocks = 1;
   switch (dtype) {
     case TS_BF16:
       hipLaunchKernelGGL(scale_inplace<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st,
-                         static_cast<__bf16*>(x), nvec, num, den, hint_out);
+                         static_cast<__bf16*>(x), nvec, n, num, den, hint_out);
       break;
     case TS_F16:
       hipLaunchKernelGGL(scale_inplace<_Float16>, dim3((unsigned)blocks), dim3(256), 0, st,
-                         static_cast<_Float16*>(x), nvec, num, den, hint_out);
+                         static_cast<_Float16*>(x), nvec, n, num, den, hint_out);
       break;
     case TS_F32:
       hipLaunchKernelGGL(scale_inplace<float>, dim3((unsigned)blocks), dim3(256), 0, st,
-                         static_cast<float*>(x), nvec, num, den, hint_out);
+                         static_cast<float*>(x), nvec, n, num, den, hint_out);
       break;
   }
   return ts_host::check_launch(what);

@@ -30,6 +30,7 @@ from torch import Tensor
 
 from .. import ops
 from ..loss.linear_ce import linear_ce_vocab_phase1, linear_ce_vocab_phase2
+from ..loss.sota_losses import SECOND_BACKWARD_MSG
 
 
 def _local_gather(stats: Tensor) -> Tensor:
@@ -153,6 +154,9 @@ class VocabParallelLinearCrossEntropyFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output: Tensor):
+        if getattr(ctx, "backward_done", False):
+            raise RuntimeError(SECOND_BACKWARD_MSG)
+        ctx.backward_done = True
         gh, gw = ctx.saved_tensors
         scale = grad_output.detach().float().reshape(1).contiguous()
         if gh is not None:

@@ -99,6 +99,12 @@ def _row_weight(labels: Tensor, ignore_index: int, reduction: str, n: int) -> Te
     return torch.ones((1,), dtype=torch.float32, device=labels.device)
 
 
+SECOND_BACKWARD_MSG = (
+    "backward was called a second time through a loss whose gradient is formed in the "
+    "forward pass and scaled in place by the first backward (retain_graph=True); run the "
+    "forward again, or use reduction='none' (two-pass schedule, which supports it)")
+
+
 class UpstreamGradHint:
     """Prediction of a loss's upstream gradient, one fp32 device scalar per device.
 
@@ -167,6 +173,12 @@ class FusedCrossEntropyFunction(torch.autograd.Function):
     def backward(ctx, grad_output: Tensor):
         ignore_index, label_smoothing, reduction = ctx.cfg
         if ctx.fused:
+            # The gradient was formed in the forward and is scaled here in place; a
+            # second backward through the same graph (retain_graph=True) would scale
+            # it again, so it is refused rather than returning a wrong gradient.
+            if getattr(ctx, "backward_done", False):
+                raise RuntimeError(SECOND_BACKWARD_MSG)
+            ctx.backward_done = True
             grad, used = ctx.saved_tensors
             if used is None:
                 ops.scale_(grad, grad_output)

@@ -102,6 +102,14 @@ def _routed_apply(original):
               and q.dim() == 4 and k.dim() == 4 and cos.dim() == 3
               and q.shape[-1] == cos.shape[-1] == k.shape[-1] and q.shape[-1] % 2 == 0
               and q.dtype == k.dtype and sin.shape == cos.shape)
+        if ok:
+            # the table rows the kernel reads: cos/sin [1 or B, S, D] against q and k of
+            # [B, H, S, D] (unsqueeze_dim 1) or [B, S, H, D] (2); other layouts, which
+            # broadcasting might still accept, go to the original function
+            s_dim = 2 if unsqueeze_dim == 1 else 1
+            B, S = q.shape[0], q.shape[s_dim]
+            ok = (k.shape[0] == B and k.shape[s_dim] == S and cos.shape[0] in (1, B)
+                  and cos.shape[1] == S)
         if not ok:
             return original(q, k, cos, sin, *args, **kwargs)
         return hf_apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim)
