@@ -123,6 +123,30 @@ ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy,
                          void* workspace, size_t workspace_bytes,
                          int64_t rows, int64_t cols, ts_stream_t stream);
 
+/*
+ * ts_rmsnorm_bwd without a workspace and without allocating: the dW partial
+ * rows go to a device scratch array of ts_rmsnorm_bwd_noalloc_max_bytes()
+ * bytes (16 MiB: C1 [16384, 4096] and C4 [32768, 8192] in bf16 fit) that the
+ * library holds on every device it runs on until the process ends. Same
+ * arguments, results and kernels as ts_rmsnorm_bwd. Calls whose partials
+ * would not fit (ts_rmsnorm_bwd_workspace_size > the maximum) return
+ * TS_ERR_WORKSPACE before launching anything. Every call on one device
+ * shares that device's scratch, so calls that overlap on one device (two
+ * streams, or two threads) race; calls in one stream are ordered. The
+ * device of `stream` must be the current device.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).
+ */
+size_t ts_rmsnorm_bwd_noalloc_max_bytes(void);
+ts_status ts_rmsnorm_bwd_noalloc(const void* dy, int64_t lddy,
+                                 const void* x, int64_t ldx, ts_dtype x_dtype,
+                                 const void* w, ts_dtype w_dtype,
+                                 const float* rstd,
+                                 void* dx, int64_t lddx,
+                                 void* dw,
+                                 int64_t rows, int64_t cols, ts_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* SwiGLU                                                                    */
 /* ------------------------------------------------------------------------ */

@@ -58,6 +58,8 @@ SIGNATURES = {
                            I32),
     "ts_rmsnorm_bwd_workspace_size": ([I64, I64], SZ),
     "ts_rmsnorm_bwd": ([P, I64, P, I64, I32, P, I32, P, P, I64, P, P, SZ, I64, I64, P], I32),
+    "ts_rmsnorm_bwd_noalloc_max_bytes": ([], SZ),
+    "ts_rmsnorm_bwd_noalloc": ([P, I64, P, I64, I32, P, I32, P, P, I64, P, I64, I64, P], I32),
     "ts_rope_apply": (
         [P, P, I64, I64, I64, I64, I64, I64, I64,   # q
          P, P, I64, I64, I64, I64, I64, I64, I64,   # k

@@ -18,8 +18,18 @@
 // Generic path (row length not a multiple of the 16-byte vector, unaligned
 // pointers, or rows longer than the register plans): one workgroup per row
 // with element-wise loads and two passes over the row.
+#include <mutex>
+
 #include "common.hpp"
 #include "plan.hpp"
+
+// Device scratch of ts_rmsnorm_bwd_noalloc: the fp32 dW partial rows, for
+// callers that cannot allocate. Each device that runs the library holds its
+// own copy for the life of the process. Its contents need no clearing
+// between calls: the dx kernel overwrites every partial row the reduction
+// reads.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 namespace {
 
@@ -746,4 +756,57 @@ extern "C" ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy, const void* x,
   }
 #undef TS_BWD_ARGS
   return fail(TS_ERR_UNSUPPORTED_DTYPE, "rmsnorm_bwd: unsupported dtype");
+}
+
+namespace {
+
+// Device address of `scratch` on each device, looked up once per device with
+// that device current (the name itself is a host-side stand-in that must
+// never reach a kernel).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+ts_status scratch_on_current_device(void** out) {
+  using ts_host::fail;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(TS_ERR_DEVICE, "rmsnorm_bwd_noalloc: no current device (%d)", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(TS_ERR_DEVICE, "rmsnorm_bwd_noalloc: hipGetSymbolAddress failed on device %d: %s",
+                  dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TS_OK;
+}
+
+}  // namespace
+
+extern "C" size_t ts_rmsnorm_bwd_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" ts_status ts_rmsnorm_bwd_noalloc(const void* dy, int64_t lddy, const void* x,
+                                            int64_t ldx, ts_dtype x_dtype, const void* w,
+                                            ts_dtype w_dtype, const float* rstd, void* dx,
+                                            int64_t lddx, void* dw, int64_t rows, int64_t cols,
+                                            ts_stream_t stream) {
+  void* ws = nullptr;
+  size_t need = 0;
+  if (dw != nullptr && rows > 0 && cols > 0) {
+    need = ts_rmsnorm_bwd_workspace_size(rows, cols);
+    if (need > kNoAllocScratchBytes)
+      return ts_host::fail(TS_ERR_WORKSPACE,
+                           "rmsnorm_bwd_noalloc: rows=%lld cols=%lld need %zu bytes of dW "
+                           "partials, above the %zu-byte device scratch; use ts_rmsnorm_bwd "
+                           "with a workspace",
+                           (long long)rows, (long long)cols, need, kNoAllocScratchBytes);
+    const ts_status s = scratch_on_current_device(&ws);
+    if (s != TS_OK) return s;
+  }
+  return ts_rmsnorm_bwd(dy, lddy, x, ldx, x_dtype, w, w_dtype, rstd, dx, lddx, dw, ws,
+                        ws != nullptr ? kNoAllocScratchBytes : 0, rows, cols, stream);
 }
