@@ -407,6 +407,67 @@ ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight, i
                           void* workspace, size_t workspace_bytes, ts_stream_t stream);
 
 /*
+ * Two-pass fused linear cross-entropy (the schedule for any reduction and any
+ * upstream gradient, and for forward-only calls): no [N, V] logits are stored.
+ *
+ * Logits z = bf16(hidden @ weight^T) (MFMA, fp32 accumulation, rounded to bf16
+ * as a bf16 matmul rounds them), transformed in the order of
+ * selective_log_softmax (rl_training.py:114-122):
+ *   t = softcap > 0 ? softcap * tanh(z / softcap) : z;  t *= scale if scale > 0;
+ *   t /= temperature
+ * (softcap = scale = 0, temperature = 1: t = z). Per row, in fp32:
+ *   lse[r] = log sum_j exp(t[r, j]),
+ *   loss_rows[r] = lse[r] - t[r, labels[r]]  (0 where labels[r] == ignore_index,
+ *                                            NaN for other labels outside [0, V)),
+ *   reduction 0 (mean): *loss = sum(loss_rows) / max(n_valid, 1); 1 (sum):
+ *   *loss = sum(loss_rows); 2 (none): loss may be NULL.
+ * hidden [N, H], weight [V, H]: bf16, 16-byte aligned, row strides ldh/ldw
+ * (multiples of 8); H and V multiples of 8; any N >= 0.
+ *
+ * Forward: one logits GEMM whose epilogue keeps per-(row, 128-column slice)
+ * max and sum of exp and the label's t; workspace of
+ * ts_flce_forward_workspace_size(N, V) bytes (N * V / 16 bytes of statistics).
+ * loss_rows and lse may be NULL (lse is what the backward needs).
+ * Replaces chunked_log_softmax + selective_log_softmax (rl_training.py:95-191,
+ * which return -loss_rows, called by GRPOCompute.compute_log_probs :509-552)
+ * and the composition logits = hidden @ lm_head.t() then cross-entropy
+ * (kernels/triton_kernels.py:427-467), without their [B, chunk, V] logits.
+ */
+size_t ts_flce_forward_workspace_size(int64_t N, int64_t V);
+ts_status ts_flce_forward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                          const int64_t* labels, int64_t N, int64_t H, int64_t V,
+                          int64_t ignore_index, int32_t reduction,
+                          float softcap, float scale, float temperature,
+                          float* loss, float* loss_rows, float* lse,
+                          void* workspace, size_t workspace_bytes, ts_stream_t stream);
+
+/*
+ * Backward of ts_flce_forward for the upstream gradient dloss (device fp32:
+ * dloss[r * dloss_stride], stride 0 broadcasts one value; for mean and sum
+ * the scalar upstream gradient of *loss, for none that of each loss_rows[r]):
+ *   dt[r, j] = dloss_r * s * (softmax(t[r])_j - [j == labels[r]]),
+ *   s = 1 / max(n_valid, 1) for mean, else 1; 0 on ignore_index rows,
+ *   dz = bf16(dt * dt/dz),  grad_hidden = dz @ weight,  grad_weight = dz^T @ hidden
+ * (bf16 outputs, fp32 accumulation; either may be NULL). lse: the forward's.
+ * The logits are recomputed one vocabulary chunk of chunk_cols columns at a
+ * time (0: about V / 8, at least 4096; rounded up to 256) by the forward's
+ * GEMM, whose epilogue forms the chunk's dz; grad_hidden accumulates over the
+ * chunks in fp32, grad_weight's rows of a chunk are written once. Workspace:
+ * ts_flce_backward_workspace_size(N, H, V, chunk_cols) bytes (N x chunk bf16
+ * dz, plus N x H fp32 with more than one chunk). Deterministic.
+ * Replaces autograd's backward through chunked_log_softmax /
+ * selective_log_softmax (rl_training.py:95-191) and the lm_head matmul.
+ */
+size_t ts_flce_backward_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk_cols);
+ts_status ts_flce_backward(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                           const int64_t* labels, int64_t N, int64_t H, int64_t V,
+                           int64_t ignore_index, int32_t reduction,
+                           float softcap, float scale, float temperature,
+                           const float* lse, const float* dloss, int64_t dloss_stride,
+                           void* grad_hidden, void* grad_weight, int64_t chunk_cols,
+                           void* workspace, size_t workspace_bytes, ts_stream_t stream);
+
+/*
  * x[i] *= *scale for n contiguous values of `dtype` (any n >= 0; 16-byte
  * vectors where x is 16-byte aligned, single elements for the rest); scale
  * is a device pointer, and when *scale == 1 nothing is written. Applies an upstream gradient other than 1

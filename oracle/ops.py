@@ -24,6 +24,7 @@ __all__ = [
     "ce_fwd",
     "ce_bwd",
     "linear_ce",
+    "rl_logit_xform",
     "vocab_parallel_ce",
     "swiglu_fwd",
     "swiglu_bwd",
@@ -292,9 +293,32 @@ def vocab_parallel_ce(shards, targets: Tensor, label_smoothing: float = 0.0):
     return out
 
 
+def rl_logit_xform(z32: Tensor, logit_softcapping: float = 0.0, logit_scale: float = 0.0,
+                   temperature: float = 1.0) -> Tuple[Tensor, Tensor]:
+    """(t, dt/dz) of selective_log_softmax's logit transforms (rl_training.py:114-122):
+    softcapping t = c * tanh(z / c) when c > 0, then scaling t * s when s > 0, then
+    t / temperature when temperature != 1. fp32 arithmetic (the reference computes
+    in the logits' dtype)."""
+    t = z32
+    d = torch.ones_like(z32)
+    if logit_softcapping > 0:
+        th = torch.tanh(z32 / logit_softcapping)
+        t = logit_softcapping * th
+        d = 1 - th * th
+    if logit_scale > 0:
+        t = t * logit_scale
+        d = d * logit_scale
+    if temperature != 1.0:
+        t = t / temperature
+        d = d / temperature
+    return t, d
+
+
 def linear_ce(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
               reduction: str = "mean", bf16_logits: bool = False,
-              return_rows: bool = False):
+              return_rows: bool = False, logit_softcapping: float = 0.0,
+              logit_scaling: float = 0.0, temperature: float = 1.0,
+              dloss: Optional[Tensor] = None):
     """Fused linear cross-entropy as its composition: logits = hidden @ weight.T -> CE.
 
     hidden [N, H], weight [V, H] (the lm_head layout of rl_training.py:156-177),
@@ -302,20 +326,32 @@ def linear_ce(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int 
     reference's bf16 matmul rounds them (rl_training.py:177, bf16 operands), the
     loss is the fp32 CE of those bf16 logits (kernels/triton_kernels.py:328-337),
     and dlogits are rounded to bf16 as autograd hands them to the bf16 matmul's
-    backward. Returns (loss fp32 scalar, grad_hidden, grad_weight) in the input
-    dtypes for mean (over non-ignored rows) or sum reduction; with return_rows
-    also (loss_rows, lse).
+    backward. The logits pass through rl_logit_xform (softcap, scale,
+    temperature, in rl_training.py:114-122's order) before the CE; the per-row
+    loss is -selective_log_softmax (rl_training.py:123-134).
+
+    reduction "mean" (over non-ignored rows), "sum" or "none" (per-row losses).
+    dloss: the upstream gradient (a scalar for mean/sum, [N] or a scalar for
+    none; default 1). Returns (loss fp32 scalar or [N] rows, grad_hidden,
+    grad_weight) in the input dtypes; with return_rows also (loss_rows, lse).
     """
     hidden, weight, labels = _cpu(hidden), _cpu(weight), _cpu(labels).reshape(-1)
     h32, w32 = hidden.float(), weight.float()
     logits = h32 @ w32.t()
     if bf16_logits:
         logits = logits.to(torch.bfloat16).float()
-    loss_rows, lse = ce_fwd(logits, labels, ignore_index)
+    t, dtdz = rl_logit_xform(logits, logit_softcapping, logit_scaling, temperature)
+    loss_rows, lse = ce_fwd(t, labels, ignore_index)
     n_valid = max(int((labels != ignore_index).sum()), 1)
-    scale = 1.0 / n_valid if reduction == "mean" else 1.0
-    loss = loss_rows.sum() * scale
-    g = ce_bwd(logits, labels, torch.tensor(scale), ignore_index, out_dtype=torch.float32)
+    up = torch.ones(()) if dloss is None else _cpu(dloss).float().reshape(-1)
+    if reduction == "none":
+        loss = loss_rows
+        d = up
+    else:
+        scale = 1.0 / n_valid if reduction == "mean" else 1.0
+        loss = loss_rows.sum() * scale
+        d = up.reshape(()) * scale
+    g = ce_bwd(t, labels, d, ignore_index, out_dtype=torch.float32) * dtdz
     if bf16_logits:
         g = g.to(torch.bfloat16).float()
     grad_h = (g @ w32).to(hidden.dtype)

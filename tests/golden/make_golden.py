@@ -13,6 +13,10 @@ oracle/ (no torch ops, no shared code):
   softmax - onehot; label smoothing as the cross-entropy against the smoothed
   target distribution (1-a)*onehot + a/V.
 * Linear cross-entropy: float64 matmul followed by the above.
+* Linear cross-entropy with the RL logit transforms (softcap, scale,
+  temperature) and per-row upstream gradients: losses from the float64
+  composition, gradients by central finite differences of
+  sum_r dloss_r * loss_r (no derivative formula).
 * SwiGLU: silu(g) = g / (1 + exp(-g)) and its derivative
   1/(1+e^-g) + g e^-g / (1+e^-g)^2 (the quotient rule, not the reference's
   factored form).
@@ -179,6 +183,47 @@ def linear_ce_case(seed, N, H, V, ignore):
                 grad_hidden=G @ W, grad_weight=G.T @ Hh)
 
 
+def linear_ce_rl_case(seed, N, H, V, ignore, softcap, scale, temperature):
+    """Per-token losses (-log-probs) under the RL logit transforms of
+    selective_log_softmax (softcap, then scale, then temperature) with per-row
+    upstream gradients; the gradients of sum_r dloss_r * loss_r are central
+    finite differences in float64, so no derivative formula is assumed."""
+    r = rng(seed)
+    h = bf16_round(r.standard_normal((N, H)).astype(np.float32))
+    w = bf16_round((0.3 * r.standard_normal((V, H))).astype(np.float32))
+    labels = r.integers(0, V, N).astype(np.int64)
+    labels[ignore] = -100
+    dloss = r.standard_normal(N)
+    valid = labels != -100
+    Hh, W = h.astype(np.float64), w.astype(np.float64)
+
+    def rows(Hm, Wm):
+        T = softcap * np.tanh((Hm @ Wm.T) / softcap) * scale / temperature
+        m = T.max(axis=1)
+        lse = m + np.log(np.exp(T - m[:, None]).sum(axis=1))
+        return np.where(valid, lse - T[np.arange(N), np.clip(labels, 0, None)], 0.0), lse
+
+    def f(Hm, Wm):
+        return float((dloss * rows(Hm, Wm)[0]).sum())
+
+    def fd(X, other_first):
+        G = np.zeros_like(X)
+        step = 1e-6
+        for idx in np.ndindex(*X.shape):
+            Xp, Xm = X.copy(), X.copy()
+            Xp[idx] += step
+            Xm[idx] -= step
+            fp = f(Xp, W) if other_first else f(Hh, Xp)
+            fm = f(Xm, W) if other_first else f(Hh, Xm)
+            G[idx] = (fp - fm) / (2 * step)
+        return G
+
+    loss_rows, lse = rows(Hh, W)
+    return dict(hidden=h, weight=w, labels=labels, dloss=dloss, softcap=np.float64(softcap),
+                scale=np.float64(scale), temperature=np.float64(temperature),
+                loss_rows=loss_rows, lse=lse, grad_hidden=fd(Hh, True), grad_weight=fd(W, False))
+
+
 def main():
     cases = {}
     cases["rmsnorm_64"] = rmsnorm_case(10, 4, 64, 1e-6, zero_row=True)
@@ -198,6 +243,8 @@ def main():
     cases["ce_smooth"] = ce_case(32, 4, 128, ignore=[1], smoothing=0.1)
     cases["ce_softcap_scale"] = ce_case(33, 4, 96, ignore=[], scale=0.5, softcap=3.0, std=4.0)
     cases["linear_ce"] = linear_ce_case(40, 6, 32, 50, ignore=[3])
+    cases["linear_ce_rl"] = linear_ce_rl_case(41, 6, 32, 48, ignore=[2], softcap=3.0, scale=0.8,
+                                              temperature=0.7)
     cases["swiglu"] = swiglu_case(50, 4096, 3.0)
     for name, arrays in cases.items():
         np.savez(OUT / f"{name}.npz", **arrays)

@@ -239,3 +239,43 @@ def test_flce_validation(lib):
     assert call(loss=NULL) == INVALID
     assert call(hidden=NULL) == INVALID
     assert call(wsb=ws - 256) == WORKSPACE
+
+
+def test_flce_two_pass_validation(lib):
+    st = NULL
+    N, H, V = 65, 64, 128  # any token count
+    wf = lib.ts_flce_forward_workspace_size(N, V)
+    wb = lib.ts_flce_backward_workspace_size(N, H, V, 0)
+    assert wf > 0 and wb > 0 and lib.ts_flce_forward_workspace_size(0, V) == 0
+    # more vocabulary chunks: a smaller dlogits buffer plus the fp32 grad_hidden sum
+    assert lib.ts_flce_backward_workspace_size(N, H, 4096, 256) < \
+        lib.ts_flce_backward_workspace_size(N, H, 4096, 4096) + N * H * 4
+
+    def fwd(n=N, h=H, v=V, ldh=H, red=0, cap=0.0, sc=0.0, temp=1.0, loss=FAKE, wsb=wf,
+            hidden=FAKE):
+        return lib.ts_flce_forward(hidden, ldh, FAKE, H, FAKE, n, h, v, -100, red, cap, sc, temp,
+                                   loss, NULL, NULL, FAKE, wsb, st)
+
+    assert fwd(h=60, ldh=64) == SHAPE
+    assert fwd(v=100) == SHAPE            # V not a multiple of 8
+    assert fwd(ldh=32) == SHAPE
+    assert fwd(red=3) == INVALID
+    assert fwd(loss=NULL) == INVALID      # mean needs the scalar
+    assert fwd(cap=-1.0) == INVALID
+    assert fwd(temp=0.0) == INVALID
+    assert fwd(sc=float("nan")) == INVALID
+    assert fwd(hidden=NULL) == INVALID
+    assert fwd(wsb=wf - 256) == WORKSPACE
+    assert fwd(n=0, loss=NULL, red=2) == TS_OK  # nothing to do
+
+    def bwd(dl_stride=0, lse=FAKE, dloss=FAKE, wsb=wb, gh=FAKE, gw=FAKE, temp=1.0):
+        return lib.ts_flce_backward(FAKE, H, FAKE, H, FAKE, N, H, V, -100, 2, 0.0, 0.0, temp, lse,
+                                    dloss, dl_stride, gh, gw, 0, FAKE, wsb, st)
+
+    assert bwd(dl_stride=-1) == INVALID
+    assert bwd(lse=NULL) == INVALID
+    assert bwd(dloss=NULL) == INVALID
+    assert bwd(temp=-1.0) == INVALID
+    assert bwd(gh=ctypes.c_void_p(0x1008)) == INVALID   # unaligned
+    assert bwd(wsb=wb - 256) == WORKSPACE
+    assert bwd(gh=NULL, gw=NULL) == TS_OK   # no gradient requested: nothing launched

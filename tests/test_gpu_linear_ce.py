@@ -13,13 +13,16 @@ order).
 """
 import math
 
+import numpy as np
+
 import pytest
 import torch
 
 import oracle
 from trainscale_amd import workloads
-from trainscale_amd.loss import fused_linear_cross_entropy
-from trainscale_amd.loss.linear_ce import linear_ce_forward_backward
+from trainscale_amd.loss import chunked_log_softmax, fused_linear_cross_entropy
+from trainscale_amd.loss.linear_ce import (linear_ce_backward, linear_ce_forward,
+                                           linear_ce_forward_backward)
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
@@ -166,24 +169,15 @@ def test_strided_rows(gpu):
     assert torch.equal(gh, gh_c) and torch.equal(gw, gw_c)
 
 
-def test_c5_full(gpu):
-    """C5 at full size: sampled rows against the CPU oracle, the whole batch against
-    an independent composition on the GPU (torch bf16 matmul + fp32 softmax)."""
-    wl = workloads.linear_ce_workload(gpu)
-    h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
-    N, H = h.shape
-    V = w.shape[0]
-    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels)
+def _c5_reference(h, w, labels, gw_rows):
+    """Loss, grad_hidden and grad_weight[gw_rows] of C5 from torch on the GPU: bf16 matmul
+    logits in row chunks, fp32 softmax, dlogits rounded to bf16 (as autograd hands them
+    to the bf16 matmul's backward), fp32 products for the sampled grad_weight rows."""
+    N = h.shape[0]
     n_valid = int((labels != -100).sum())
-    # per-row loss and lse of 32 rows against the CPU oracle (bf16 logits)
-    sample = torch.arange(0, N, N // 32)
-    logits = (h[sample].float().cpu() @ w.float().cpu().t()).to(BF)
-    ref_rows, ref_lse = oracle.ce_fwd(logits, labels[sample].cpu())
-    _, row_bound = flip_bound(h[sample], w, labels[sample])
-    assert_rows_close(rows[sample], ref_rows, row_bound, "loss rows")
-    # whole batch: torch's bf16 matmul for the logits (row chunks), fp32 softmax
     ref_sum = 0.0
-    ref_gh = torch.empty_like(gh)
+    ref_gh = torch.empty_like(h)
+    d_cols = torch.empty((N, len(gw_rows)), dtype=torch.float32, device=h.device)
     for s in range(0, N, 1024):
         lg = (h[s:s + 1024] @ w.t()).float()
         lab = labels[s:s + 1024]
@@ -196,13 +190,250 @@ def test_c5_full(gpu):
         p[~valid] = 0.0
         d = (p / n_valid).to(BF)
         ref_gh[s:s + 1024] = d @ w
+        d_cols[s:s + 1024] = d[:, gw_rows].float()
         del lg, p, d
-    ref_loss = ref_sum / n_valid
+    ref_gw_rows = d_cols.t() @ h.float()
+    return ref_sum / n_valid, ref_gh, ref_gw_rows
+
+
+def _check_c5(h, w, labels, loss, rows, gh, gw):
+    N, H = h.shape
+    V = w.shape[0]
+    # per-row loss of 32 rows against the CPU oracle (bf16 logits)
+    sample = torch.arange(0, N, N // 32)
+    logits = (h[sample].float().cpu() @ w.float().cpu().t()).to(BF)
+    ref_rows, _ = oracle.ce_fwd(logits, labels[sample].cpu())
+    _, row_bound = flip_bound(h[sample], w, labels[sample])
+    assert_rows_close(rows[sample], ref_rows, row_bound, "loss rows")
+    # 64 grad_weight rows, one in each 1/64 of the vocabulary (every group of eight
+    # 256-row tiles), at varying offsets inside their tiles
+    g = torch.Generator().manual_seed(9)
+    step = V // 64
+    gw_rows = torch.tensor([k * step + int(torch.randint(0, step, (1,), generator=g))
+                            for k in range(64)], device=h.device)
+    ref_loss, ref_gh, ref_gw_rows = _c5_reference(h, w, labels, gw_rows)
     assert abs(loss.item() - ref_loss) <= 1e-5 * abs(ref_loss), (loss.item(), ref_loss)
     assert rel_fro(gh, ref_gh) <= 1e-2
     assert (gh.float() - ref_gh.float()).abs().max().item() <= 2e-2
-    assert torch.isfinite(gw.float()).all()
-    # grad_weight rows: sum over tokens of dlogits * hidden; each row of dlogits sums
-    # to zero, so the column sums of grad_weight vanish: sum_v gW[v, :] = 0
+    got = gw[gw_rows].float()
+    assert rel_fro(got, ref_gw_rows) <= 1e-2, rel_fro(got, ref_gw_rows)
+    assert (got - ref_gw_rows).abs().max().item() <= 2e-2
+    # every row of dlogits sums to zero, so the column sums of grad_weight vanish
     col = gw.float().sum(0)
     assert col.abs().max().item() <= 1e-2 * gw.float().abs().sum(0).max().item()
+
+
+def test_c5_full(gpu):
+    """C5 at full size through the default (two-pass, vocabulary-chunked) schedule:
+    sampled rows against the CPU oracle, the loss, grad_hidden and 64 grad_weight rows
+    spread over the vocabulary against an independent composition on the GPU (torch
+    bf16 matmul + fp32 softmax)."""
+    wl = workloads.linear_ce_workload(gpu)
+    h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
+    loss, rows, lse = linear_ce_forward(h, w, labels)
+    gh, gw = linear_ce_backward(h, w, labels, lse, torch.ones((), device=gpu))
+    _check_c5(h, w, labels, loss, rows, gh, gw)
+
+
+def test_c5_full_fused_schedule(gpu):
+    """C5 through the one-call schedule with the full logits in one chunk (opt-in)."""
+    wl = workloads.linear_ce_workload(gpu)
+    h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
+    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels)
+    _check_c5(h, w, labels, loss, rows, gh, gw)
+
+
+# ---------------------------------------------------------------------------
+# Two-pass schedule (the default): vocabulary-chunked backward, RL transforms,
+# per-row upstream gradients
+# ---------------------------------------------------------------------------
+
+def check_two_pass(h, w, labels, reduction="mean", dloss=None, chunk=None, **xf):
+    loss, rows, lse = linear_ce_forward(h, w, labels, reduction=reduction, **xf)
+    up = dloss if dloss is not None else torch.ones((), device=h.device)
+    gh, gw = linear_ce_backward(h, w, labels, lse, up, reduction=reduction, vocab_chunk=chunk,
+                                **xf)
+    ref_loss, ref_gh, ref_gw, ref_rows, ref_lse = oracle.linear_ce(
+        h, w, labels, reduction=reduction, bf16_logits=True, return_rows=True,
+        dloss=None if dloss is None else dloss.cpu(), **xf)
+    if reduction != "none":
+        assert abs(loss.item() - float(ref_loss)) <= 1e-5 * abs(float(ref_loss)) + 1e-6, (
+            loss.item(), float(ref_loss))
+    else:
+        assert loss is None
+    if not xf:
+        lse_bound, row_bound = flip_bound(h, w, labels)
+    else:  # transformed logits: a flip moves t by at most ulp(z) * max|dt/dz|
+        lse_bound, row_bound = flip_bound(h, w, labels)
+        m = (xf.get("logit_scaling") or 1.0) / xf.get("temperature", 1.0)
+        lse_bound, row_bound = lse_bound * m, row_bound * m
+    assert_rows_close(rows, ref_rows, row_bound, "loss rows")
+    valid = labels.cpu() != -100
+    assert_rows_close(lse[valid.to(lse.device)], ref_lse[valid], lse_bound[valid], "lse")
+    for name, g, r in (("grad_hidden", gh, ref_gh), ("grad_weight", gw, ref_gw)):
+        assert (g.float().cpu() - r.float()).abs().max().item() <= 2e-2, name
+        assert rel_fro(g, r) <= 1e-2, (name, rel_fro(g, r))
+    return loss, rows, lse, gh, gw
+
+
+@pytest.mark.parametrize("N,H,V,chunk", [(512, 256, 1000, None), (523, 64, 2048, 256),
+                                         (257, 512, 4096, 768), (8, 32, 8, None),
+                                         (1, 40, 520, 256), (1035, 296, 776, 512)])
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_two_pass_shapes(gpu, N, H, V, chunk, reduction):
+    torch.manual_seed(N + H + V)
+    h = torch.randn(N, H, device=gpu).to(BF)
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::20] = -100
+    check_two_pass(h, w, labels, reduction, chunk=chunk)
+
+
+@pytest.mark.parametrize("xf", [dict(logit_softcapping=30.0),
+                                dict(logit_scaling=0.5, temperature=0.7),
+                                dict(logit_softcapping=3.0, logit_scaling=0.8, temperature=1.3),
+                                dict(temperature=2.0)])
+@pytest.mark.parametrize("chunk", [None, 256])
+def test_two_pass_rl_transforms_per_row_upstream(gpu, xf, chunk):
+    torch.manual_seed(17)
+    N, H, V = 333, 128, 1536
+    h = torch.randn(N, H, device=gpu).to(BF)
+    w = (0.2 * torch.randn(V, H, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::11] = -100
+    dloss = torch.randn(N, device=gpu)  # per-token weights of both signs (advantages)
+    check_two_pass(h, w, labels, "none", dloss=dloss, chunk=chunk, **xf)
+
+
+def test_two_pass_rl_golden_on_gpu(gpu):
+    from helpers import golden
+    g = golden("linear_ce_rl")
+    h = torch.from_numpy(g["hidden"]).to(BF).to(gpu)
+    w = torch.from_numpy(g["weight"]).to(BF).to(gpu)
+    labels = torch.from_numpy(g["labels"]).to(gpu)
+    dloss = torch.from_numpy(g["dloss"]).float().to(gpu)
+    kw = dict(logit_softcapping=float(g["softcap"]), logit_scaling=float(g["scale"]),
+              temperature=float(g["temperature"]))
+    _, rows, lse = linear_ce_forward(h, w, labels, reduction="none", **kw)
+    gh, gw = linear_ce_backward(h, w, labels, lse, dloss, reduction="none", **kw)
+    # the kernel rounds the logits to bf16, the golden values do not: bound the difference
+    # by the rounding (|dz| <= ulp(z)/2, |dt/dz| <= scale / temperature)
+    z = torch.from_numpy(g["hidden"]).double() @ torch.from_numpy(g["weight"]).double().t()
+    dz = (z - z.to(BF).double()).abs().max().item()
+    m = kw["logit_scaling"] / kw["temperature"]
+    np.testing.assert_allclose(rows.double().cpu().numpy(), g["loss_rows"], atol=2 * m * dz + 1e-5)
+    np.testing.assert_allclose(gh.double().cpu().numpy(), g["grad_hidden"], rtol=0.05, atol=0.02)
+    np.testing.assert_allclose(gw.double().cpu().numpy(), g["grad_weight"], rtol=0.05, atol=0.02)
+
+
+def test_two_pass_equals_one_call_schedule(gpu):
+    torch.manual_seed(21)
+    N, H, V = 520, 192, 2560
+    h = torch.randn(N, H, device=gpu).to(BF)
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::13] = -100
+    loss1, rows1, lse1, gh1, gw1 = linear_ce_forward_backward(h, w, labels)
+    loss2, rows2, lse2 = linear_ce_forward(h, w, labels)
+    # the same GEMM and epilogue arithmetic: statistics and losses bit-identical
+    assert torch.equal(rows1, rows2) and torch.equal(lse1, lse2) and torch.equal(loss1, loss2)
+    one = torch.ones((), device=gpu)
+    gh2, gw2 = linear_ce_backward(h, w, labels, lse2, one, vocab_chunk=V)  # one chunk
+    assert torch.equal(gh1, gh2) and torch.equal(gw1, gw2)
+    gh3, gw3 = linear_ce_backward(h, w, labels, lse2, one, vocab_chunk=512)  # five chunks
+    assert torch.equal(gw1, gw3)  # grad_weight rows of a chunk: the same sums over tokens
+    assert rel_fro(gh3, gh1) <= 4e-3  # grad_hidden: fp32 sums over chunks, rounded once
+
+
+def test_module_api_two_pass_default(gpu):
+    torch.manual_seed(22)
+    B, L, H, V = 2, 67, 128, 1024
+    h = torch.randn(B, L, H, device=gpu).to(BF).requires_grad_()
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF).requires_grad_()
+    labels = torch.randint(0, V, (B, L), device=gpu)
+    labels[0, :5] = -100
+    loss = fused_linear_cross_entropy(h, w, labels)
+    (3.0 * loss).backward(retain_graph=True)
+    ref_loss, ref_gh, ref_gw = oracle.linear_ce(h.detach().reshape(-1, H), w.detach(),
+                                                labels.reshape(-1), bf16_logits=True)
+    assert abs(loss.item() - float(ref_loss)) <= 1e-5 * abs(float(ref_loss))
+    gh1, gw1 = h.grad.clone(), w.grad.clone()
+    assert rel_fro(gh1.reshape(-1, H), 3 * ref_gh.float()) <= 1e-2
+    assert rel_fro(gw1, 3 * ref_gw.float()) <= 1e-2
+    # a second backward through the same graph recomputes: the gradients accumulate
+    loss.backward()
+    torch.testing.assert_close(h.grad.float(), gh1.float() * (4.0 / 3.0), rtol=1e-2, atol=1e-6)
+    # reduction "none" with a per-row upstream gradient through autograd
+    h.grad = None
+    w.grad = None
+    rows = fused_linear_cross_entropy(h, w, labels, reduction="none", logit_softcapping=20.0)
+    assert rows.shape == labels.shape
+    up = torch.randn(B, L, device=gpu)
+    (rows * up).sum().backward()
+    _, ref_gh2, ref_gw2 = oracle.linear_ce(h.detach().reshape(-1, H), w.detach(),
+                                           labels.reshape(-1), reduction="none",
+                                           bf16_logits=True, logit_softcapping=20.0,
+                                           dloss=up.reshape(-1).cpu())
+    assert rel_fro(h.grad.reshape(-1, H), ref_gh2.float()) <= 1e-2
+    assert rel_fro(w.grad, ref_gw2.float()) <= 1e-2
+    # forward only
+    with torch.no_grad():
+        l2 = fused_linear_cross_entropy(h, w, labels)
+    assert torch.equal(l2, loss.detach())
+
+
+def test_one_call_schedule_odd_tokens(gpu):
+    torch.manual_seed(23)
+    N, H, V = 8 * 40 + 3, 64, 512
+    h = torch.randn(N, H, device=gpu).to(BF).requires_grad_()
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF).requires_grad_()
+    labels = torch.randint(0, V, (N,), device=gpu)
+    loss = fused_linear_cross_entropy(h, w, labels, schedule="fused")
+    loss.backward()
+    ref_loss, ref_gh, ref_gw = oracle.linear_ce(h.detach(), w.detach(), labels,
+                                                bf16_logits=True)
+    assert abs(loss.item() - float(ref_loss)) <= 1e-5 * abs(float(ref_loss))
+    assert h.grad.shape == (N, H)
+    assert rel_fro(h.grad, ref_gh.float()) <= 1e-2 and rel_fro(w.grad, ref_gw.float()) <= 1e-2
+    with pytest.raises(RuntimeError, match="second time"):
+        l3 = fused_linear_cross_entropy(h, w, labels, schedule="fused")
+        l3.backward(retain_graph=True)
+        l3.backward()
+
+
+def test_chunked_log_softmax_drop_in(gpu):
+    """rl_training.chunked_log_softmax's call as GRPOCompute.compute_log_probs makes it
+    (rl_training.py:544-550): hidden_states[:, :-1, :] (a strided view), lm_head,
+    input_ids[:, 1:], temperature; log-probs [B, L-1] and their gradients."""
+    torch.manual_seed(24)
+    B, L, H, V = 3, 50, 128, 2048
+    hs = torch.randn(B, L, H, device=gpu).to(BF).requires_grad_()
+    lm_head = (0.1 * torch.randn(V, H, device=gpu)).to(BF).requires_grad_()
+    ids = torch.randint(0, V, (B, L), device=gpu)
+    lp = chunked_log_softmax(hs[:, :-1, :], lm_head, ids[:, 1:], num_chunks=4, temperature=0.9)
+    assert lp.shape == (B, L - 1)
+    up = torch.randn(B, L - 1, device=gpu)
+    (lp * up).sum().backward()
+    h2 = hs.detach()[:, :-1, :].reshape(-1, H)
+    lab = ids[:, 1:].reshape(-1)
+    rows, ref_gh, ref_gw = oracle.linear_ce(h2, lm_head.detach(), lab, reduction="none",
+                                            bf16_logits=True, temperature=0.9,
+                                            dloss=-up.reshape(-1).cpu())
+    torch.testing.assert_close(lp.reshape(-1).cpu(), -rows, rtol=1e-5, atol=2e-5)
+    assert torch.count_nonzero(hs.grad[:, -1]) == 0  # the last position takes no part
+    assert rel_fro(hs.grad[:, :-1].reshape(-1, H), ref_gh.float()) <= 1e-2
+    assert rel_fro(lm_head.grad, ref_gw.float()) <= 1e-2
+
+
+def test_two_pass_strided_rows(gpu):
+    torch.manual_seed(25)
+    N, H, V = 519, 72, 1032
+    hb = torch.randn(N, H + 24, device=gpu).to(BF)
+    wb = (0.05 * torch.randn(V, H + 40, device=gpu)).to(BF)
+    h, w = hb[:, :H], wb[:, :H]
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::9] = -100
+    _, rows, lse, gh, gw = check_two_pass(h, w, labels, "sum", chunk=256)
+    _, rows_c, lse_c, gh_c, gw_c = check_two_pass(h.contiguous(), w.contiguous(), labels, "sum",
+                                                  chunk=256)
+    assert torch.equal(rows, rows_c) and torch.equal(gh, gh_c) and torch.equal(gw, gw_c)

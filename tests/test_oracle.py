@@ -280,6 +280,71 @@ def test_linear_ce_matches_golden():
     assert_ulp(gw, round_to(g["grad_weight"], BF), 1, tiny=1e-6, what="grad_weight")
 
 
+def _rl_case():
+    g = golden("linear_ce_rl")
+    h, w = t32(g["hidden"]).to(BF), t32(g["weight"]).to(BF)
+    kw = dict(logit_softcapping=float(g["softcap"]), logit_scaling=float(g["scale"]),
+              temperature=float(g["temperature"]))
+    return g, h, w, t32(g["labels"]), torch.from_numpy(g["dloss"]).float(), kw
+
+
+def test_linear_ce_rl_transforms_match_golden():
+    """Per-token losses under softcap -> scale -> temperature with per-row upstream
+    gradients, against float64 values whose gradients are finite differences."""
+    g, h, w, labels, dloss, kw = _rl_case()
+    rows, gh, gw, _, lse = oracle.linear_ce(h, w, labels, reduction="none", dloss=dloss,
+                                            return_rows=True, **kw)
+    np.testing.assert_allclose(rows.double().numpy(), g["loss_rows"], rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(lse.double().numpy(), g["lse"], rtol=2e-6, atol=2e-6)
+    # gradients: bf16 outputs of fp32 arithmetic against float64 finite differences
+    assert_ulp(gh, round_to(g["grad_hidden"], BF), 1, tiny=1e-5, what="grad_hidden")
+    assert_ulp(gw, round_to(g["grad_weight"], BF), 1, tiny=1e-5, what="grad_weight")
+
+
+def test_linear_ce_rl_mutations_fail_golden():
+    """Plausible mistakes (scale applied before the softcap, a dropped tanh derivative,
+    temperature multiplied instead of divided) each miss the golden vectors."""
+    g, h, w, labels, dloss, kw = _rl_case()
+    ref = g["loss_rows"]
+    # scale before softcap (the CE kernels' order, not selective_log_softmax's)
+    z = h.float() @ w.float().t()
+    t = kw["logit_softcapping"] * torch.tanh(z * kw["logit_scaling"] / kw["logit_softcapping"])
+    rows_bad, _ = oracle.ce_fwd(t / kw["temperature"], labels)
+    assert np.abs(rows_bad.double().numpy() - ref).max() > 1e-3
+    # temperature multiplied
+    bad = dict(kw, temperature=1.0 / kw["temperature"])
+    rows2, _, _ = oracle.linear_ce(h, w, labels, reduction="none", dloss=dloss, **bad)
+    assert np.abs(rows2.double().numpy() - ref).max() > 1e-3
+    # the softcap's derivative left out: d(loss)/dz without (1 - tanh^2)
+    tt, d = oracle.rl_logit_xform(z, **{"logit_softcapping": kw["logit_softcapping"],
+                                        "logit_scale": kw["logit_scaling"],
+                                        "temperature": kw["temperature"]})
+    gz = oracle.ce_bwd(tt, labels, dloss, out_dtype=torch.float32) * (
+        kw["logit_scaling"] / kw["temperature"])
+    gh_bad = gz @ w.float()
+    assert np.abs(gh_bad.double().numpy() - g["grad_hidden"]).max() > 1e-3
+
+
+def test_linear_ce_reductions_agree():
+    """mean = sum(rows) / n_valid with gradients equal to those of "none" under a
+    constant upstream gradient 1 / n_valid; sum likewise with 1."""
+    torch.manual_seed(11)
+    N, H, V = 12, 32, 40
+    h = torch.randn(N, H).to(BF)
+    w = (0.2 * torch.randn(V, H)).to(BF)
+    labels = torch.randint(0, V, (N,))
+    labels[[1, 7]] = -100
+    n_valid = N - 2
+    for red, up in (("mean", 1.0 / n_valid), ("sum", 1.0)):
+        loss, gh, gw = oracle.linear_ce(h, w, labels, reduction=red, logit_softcapping=5.0,
+                                        temperature=1.3)
+        rows, gh2, gw2 = oracle.linear_ce(h, w, labels, reduction="none",
+                                          dloss=torch.full((N,), up), logit_softcapping=5.0,
+                                          temperature=1.3)
+        assert abs(float(loss) - float(rows.sum()) * (up if red == "mean" else 1.0)) <= 1e-6
+        assert torch.equal(gh, gh2) and torch.equal(gw, gw2)
+
+
 # ---------------------------------------------------------------------------
 # Mutations: plausible mistakes in the oracle must fail the checks above.
 # ---------------------------------------------------------------------------

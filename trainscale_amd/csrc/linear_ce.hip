@@ -43,7 +43,34 @@ enum EpiMode : int {
   kEpiBf16 = 1,       // bf16 C
   kEpiF32 = 2,        // fp32 C32 = acc
   kEpiAccF32 = 3,     // fp32 C32 += acc
-  kEpiAccBf16 = 4     // bf16 C = C32 + acc
+  kEpiAccBf16 = 4,    // bf16 C = C32 + acc
+  kEpiStats = 5,      // row statistics of the transformed logits + the label's value; no C
+  kEpiDlogits = 6     // bf16 C = dlogits of the transformed logits (lse known)
+};
+
+// Transform of the bf16-rounded logits z, in the order of selective_log_softmax
+// (rl_training.py:114-122): softcapping, then scaling, then temperature:
+//   t = (softcap > 0 ? softcap * tanh(z / softcap) : z) * mul,
+//   mul = (scale > 0 ? scale : 1) / temperature,
+//   dt/dz = (softcap > 0 ? 1 - tanh(z / softcap)^2 : 1) * mul.
+struct LogitXform {
+  float softcap;      // 0: off
+  float inv_softcap;  // 1 / softcap
+  float mul;
+  __device__ inline bool on() const { return softcap > 0.f || mul != 1.f; }
+  __device__ inline float apply(float z) const {
+    return (softcap > 0.f ? softcap * tanhf(z * inv_softcap) : z) * mul;
+  }
+  // t and dt/dz
+  __device__ inline float apply_d(float z, float& dt) const {
+    if (softcap > 0.f) {
+      const float th = tanhf(z * inv_softcap);
+      dt = (1.f - th * th) * mul;
+      return softcap * th * mul;
+    }
+    dt = mul;
+    return z * mul;
+  }
 };
 
 // A [M, K] and B [N, K] of C = A B^T; lda / ldb are the strides between
@@ -61,6 +88,13 @@ struct GemmArgs {
   int64_t ldc32;
   // logits epilogue
   float2* stats;          // [M][2 * NT] (max, sum exp) per 128-column slice
+  // statistics / dlogits epilogues (kEpiStats, kEpiDlogits)
+  const int64_t* labels;  // [M]; column of row r's label = labels[r] - label_offset
+  int64_t label_offset;
+  float* zlab;            // [M] transformed logit at the label (kEpiStats)
+  const float* lse;       // [M] (kEpiDlogits)
+  const float* dscale;    // [M] d(loss)/d(row loss), 0 on ignored rows (kEpiDlogits)
+  LogitXform xf;
 };
 
 // Writes the wave's RW x 128 accumulator block (RW = 32 * kTI), rounded to
@@ -164,6 +198,24 @@ void flce_gemm(const GemmArgs a) {
     stage_bf16(acc, region, lane);
     const int c16 = lane & 15;  // 16-byte chunk of the 256-byte row
     const int64_t nparts = 2 * ((a.N + BN - 1) / BN);
+    // Row operands of the statistics and dlogits epilogues: lane i holds those
+    // of the wave's row mb + i; the 16 lanes that handle a row fetch them with
+    // ds_bpermute. rel_lab is the label's column in C, -1 when outside it.
+    int rel_lab = -1;
+    float lse2 = 0.f, dsc = 0.f;
+    if constexpr (kMode == kEpiStats || kMode == kEpiDlogits) {
+      static_assert(Cw::RW == 64, "one row per lane");
+      const int64_t r = mb + lane;
+      if (r < a.M) {
+        const int64_t c = a.labels[r] - a.label_offset;
+        rel_lab = c >= 0 && c < a.N ? (int)c : -1;
+        if constexpr (kMode == kEpiDlogits) {
+          lse2 = a.lse[r] * kLog2e;
+          dsc = a.dscale[r];
+        }
+      }
+    }
+    const bool xf_on = a.xf.on();
 #pragma unroll 4
     for (int it = 0; it < Cw::RW / 4; ++it) {
       const int lrow = it * 4 + (lane >> 4);
@@ -171,7 +223,61 @@ void flce_gemm(const GemmArgs a) {
       const int64_t gc = nb + c16 * 8;
       const u32x4 v = *reinterpret_cast<const u32x4*>(region + lrow * kStagePitch + c16 * 16);
       const bool in = gm < a.M && gc < a.N;  // N % 8 == 0: a chunk is all in or all out
-      if (in) st16(a.C + gm * a.ldc + gc, v);
+      if constexpr (kMode == kEpiLogits || kMode == kEpiBf16) {
+        if (in) st16(a.C + gm * a.ldc + gc, v);
+      }
+      if constexpr (kMode == kEpiStats) {
+        // statistics of t over the row's 128-column slice, and t at the label
+        float f[8];
+        Elt<__bf16>::unpack(v, f);
+        if (xf_on) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) f[q] = a.xf.apply(f[q]);
+        }
+        float lm = f[0];
+#pragma unroll
+        for (int q = 1; q < 8; ++q) lm = fmaxf(lm, f[q]);
+        const float m = row_max(in ? lm : -INFINITY);  // over the 16 lanes of this row
+        float ls = 0.f;
+        if (in) {
+          const float mb2 = m * kLog2e;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) ls += fast_exp2(__builtin_fmaf(f[q], kLog2e, -mb2));
+        }
+        const float s = row_sum(ls);
+        if (gm < a.M && c16 == 0) a.stats[gm * nparts + nt * 2 + wn] = make_float2(m, s);
+        const int d = __shfl(rel_lab, lrow) - (int)gc;
+        if (in && (unsigned)d < 8u) {
+          float zl = f[0];
+#pragma unroll
+          for (int q = 1; q < 8; ++q) zl = d == q ? f[q] : zl;
+          a.zlab[gm] = zl;
+        }
+      }
+      if constexpr (kMode == kEpiDlogits) {
+        // (exp(t - lse) - onehot) * dt/dz * dscale, rounded to bf16
+        const float l2 = __shfl(lse2, lrow);
+        const float ds = __shfl(dsc, lrow);
+        const int d = __shfl(rel_lab, lrow) - (int)gc;
+        float f[8], g[8];
+        Elt<__bf16>::unpack(v, f);
+        if (!xf_on) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float pr = fast_exp2(__builtin_fmaf(f[e], kLog2e, -l2));
+            g[e] = ds * (e == d ? pr - 1.f : pr);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float dt;
+            const float t = a.xf.apply_d(f[e], dt);
+            const float pr = fast_exp2(__builtin_fmaf(t, kLog2e, -l2));
+            g[e] = ds * (e == d ? pr - 1.f : pr) * dt;
+          }
+        }
+        if (in) st16(a.C + gm * a.ldc + gc, Elt<__bf16>::pack(g));
+      }
       if constexpr (kMode == kEpiLogits) {
         float f[8];
         Elt<__bf16>::unpack(v, f);
@@ -234,6 +340,54 @@ __global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stat
   else out = l - Elt<__bf16>::load1(logits + r * ldl + lab);
   lse_out[r] = l;
   loss_rows[r] = out;
+}
+
+// Two-pass schedule, forward: per row (one wave per row) lse from the slice
+// statistics of the transformed logits t, and loss = lse - t[label] with
+// t[label] from zlab, written by the statistics epilogue (0 on ignore_index
+// rows, NaN for other labels outside [0, V)).
+__global__ __launch_bounds__(256) void flce_rows_t(const float2* __restrict__ stats,
+                                                   int64_t nparts, const float* __restrict__ zlab,
+                                                   const int64_t* __restrict__ labels, int64_t M,
+                                                   int64_t V, int64_t ignore_index,
+                                                   float* __restrict__ lse_out,
+                                                   float* __restrict__ loss_rows) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= M) return;  // wave-uniform
+  const float2* sr = stats + r * nparts;
+  float m = -INFINITY;
+  for (int64_t p = lane; p < nparts; p += 64) m = fmaxf(m, sr[p].x);
+  m = wave_max(m);
+  float s = 0.f;
+  for (int64_t p = lane; p < nparts; p += 64) {
+    const float2 st = sr[p];
+    s += st.y == 0.f ? 0.f : st.y * fast_exp2((st.x - m) * kLog2e);
+  }
+  s = wave_sum(s);
+  if (lane != 0) return;
+  const float l = m + logf(s);
+  const int64_t lab = labels[r];
+  float out;
+  if (lab == ignore_index) out = 0.f;
+  else if (lab < 0 || lab >= V) out = __builtin_nanf("");
+  else out = l - zlab[r];
+  lse_out[r] = l;
+  loss_rows[r] = out;
+}
+
+// Two-pass schedule, backward: d(loss)/d(row loss) per row,
+//   dscale[r] = dloss[r * stride] * (mean ? 1 / max(n_valid, 1) : 1),
+// 0 on ignore_index rows.
+__global__ __launch_bounds__(256) void flce_dscale(const int64_t* __restrict__ labels, int64_t N,
+                                                   int64_t ignore_index,
+                                                   const float* __restrict__ dloss,
+                                                   int64_t stride, const int* __restrict__ n_valid,
+                                                   int mean, float* __restrict__ dscale) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= N) return;
+  const float sc = mean ? 1.f / (float)(*n_valid > 0 ? *n_valid : 1) : 1.f;
+  dscale[r] = labels[r] == ignore_index ? 0.f : dloss[r * stride] * sc;
 }
 
 // Vocabulary-parallel linear CE, one rank. The 16-byte per-row partial the
@@ -625,6 +779,283 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   hipLaunchKernelGGL(flce_loss, dim3(1), dim3(256), 0, st, rows_ws, N, n_valid,
                      reduction == 0 ? 1 : 0, loss, scale);
   return ts_host::check_launch("flce_loss");
+}
+
+// ---------------------------------------------------------------------------
+// Two-pass fused linear CE: a forward that keeps only per-row statistics, and a
+// backward that recomputes the logits one vocabulary chunk at a time.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct FwdLayout {
+  int64_t nparts;
+  size_t off_stats, off_zlab, off_rows, off_lse, off_misc, total;
+};
+
+FwdLayout fwd_layout(int64_t N, int64_t V) {
+  FwdLayout l{};
+  l.nparts = 2 * ((V + BN - 1) / BN);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  l.off_stats = take((size_t)l.nparts * (size_t)N * sizeof(float2));
+  l.off_zlab = take((size_t)N * 4);
+  l.off_rows = take((size_t)N * 4);
+  l.off_lse = take((size_t)N * 4);
+  l.off_misc = take(64);
+  l.total = off;
+  return l;
+}
+
+// Vocabulary chunk of the backward: the given width rounded up to whole
+// 256-column tiles, or the default, about an eighth of V (at least 4096
+// columns), so the dlogits buffer holds N x chunk bf16 values.
+int64_t bwd_chunk_cols(int64_t V, int64_t chunk_cols) {
+  int64_t c = chunk_cols > 0 ? chunk_cols : ((V + 7) / 8 + BN - 1) / BN * BN;
+  if (chunk_cols <= 0 && c < 4096) c = 4096;
+  c = (c + BN - 1) / BN * BN;
+  const int64_t v8 = (V + 7) / 8 * 8;
+  return c > v8 ? v8 : c;
+}
+
+struct BwdLayout {
+  int64_t chunk, nchunks;
+  size_t off_d, off_acc, off_dscale, off_misc, total;
+};
+
+BwdLayout bwd_layout(int64_t N, int64_t H, int64_t V, int64_t chunk_cols) {
+  BwdLayout l{};
+  l.chunk = bwd_chunk_cols(V, chunk_cols);
+  l.nchunks = (V + l.chunk - 1) / l.chunk;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  l.off_d = take((size_t)N * (size_t)l.chunk * 2);
+  l.off_acc = l.nchunks > 1 ? take((size_t)N * (size_t)H * 4) : 0;
+  l.off_dscale = take((size_t)N * 4);
+  l.off_misc = take(64);
+  l.total = off;
+  return l;
+}
+
+ts_status check_two_pass(const char* who, const void* hidden, int64_t ldh, const void* weight,
+                         int64_t ldw, const int64_t* labels, int64_t N, int64_t H, int64_t V,
+                         int32_t reduction, float softcap, float scale, float temperature,
+                         LogitXform* xf) {
+  using ts_host::fail;
+  if (N < 0 || H <= 0 || V <= 0)
+    return fail(TS_ERR_SHAPE, "%s: bad shape N=%lld H=%lld V=%lld", who, (long long)N,
+                (long long)H, (long long)V);
+  if (H % 8 != 0 || V % 8 != 0)
+    return fail(TS_ERR_SHAPE, "%s: H and V must be multiples of 8 (H=%lld V=%lld)", who,
+                (long long)H, (long long)V);
+  if (ldh < H || ldw < H || ldh % 8 != 0 || ldw % 8 != 0)
+    return fail(TS_ERR_SHAPE, "%s: row strides must be >= H and multiples of 8", who);
+  // 32-bit buffer offsets within a 256-row K-major tile and a 32-row MN-major k-block
+  if (V > ((int64_t)1 << 22) || H > ((int64_t)1 << 20) || N > ((int64_t)1 << 24) ||
+      ldh > ((int64_t)1 << 22) || ldw > ((int64_t)1 << 22))
+    return fail(TS_ERR_SHAPE, "%s: shape beyond the kernel's index range", who);
+  if (reduction < 0 || reduction > 2)
+    return fail(TS_ERR_INVALID_ARGUMENT, "%s: reduction must be 0 (mean), 1 (sum) or 2 (none)",
+                who);
+  if (N > 0 && (hidden == nullptr || weight == nullptr || labels == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "%s: hidden, weight or labels is NULL", who);
+  if (!ts_host::aligned16(hidden) || !ts_host::aligned16(weight))
+    return fail(TS_ERR_INVALID_ARGUMENT, "%s: hidden and weight must be 16-byte aligned", who);
+  if (!(softcap >= 0.f) || !(scale >= 0.f) || !(temperature > 0.f) ||
+      !__builtin_isfinite(softcap) || !__builtin_isfinite(scale) ||
+      !__builtin_isfinite(temperature))
+    return fail(TS_ERR_INVALID_ARGUMENT,
+                "%s: softcap and scale must be finite and >= 0 (0 = off), temperature > 0", who);
+  xf->softcap = softcap;
+  xf->inv_softcap = softcap > 0.f ? 1.f / softcap : 0.f;
+  xf->mul = (scale > 0.f ? scale : 1.f) / temperature;
+  return TS_OK;
+}
+
+}  // namespace
+
+extern "C" size_t ts_flce_forward_workspace_size(int64_t N, int64_t V) {
+  if (N <= 0 || V <= 0) return 0;
+  return fwd_layout(N, V).total;
+}
+
+extern "C" ts_status ts_flce_forward(const void* hidden, int64_t ldh, const void* weight,
+                                     int64_t ldw, const int64_t* labels, int64_t N, int64_t H,
+                                     int64_t V, int64_t ignore_index, int32_t reduction,
+                                     float softcap, float scale, float temperature, float* loss,
+                                     float* loss_rows, float* lse, void* workspace,
+                                     size_t workspace_bytes, ts_stream_t stream) {
+  using ts_host::fail;
+  LogitXform xf{};
+  TS_TRY(check_two_pass("flce_forward", hidden, ldh, weight, ldw, labels, N, H, V, reduction,
+                        softcap, scale, temperature, &xf));
+  if (reduction != 2 && loss == nullptr)
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_forward: loss is NULL");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (N == 0) {
+    if (loss == nullptr) return TS_OK;
+    hipLaunchKernelGGL(fill_zero_u32, dim3(1), dim3(256), 0, st, nullptr, (int64_t)0, loss);
+    return ts_host::check_launch("fill_zero_u32");
+  }
+  const FwdLayout lay = fwd_layout(N, V);
+  if (workspace == nullptr || workspace_bytes < lay.total || !ts_host::aligned16(workspace))
+    return fail(TS_ERR_WORKSPACE, "flce_forward: workspace needs %zu bytes (16-byte aligned), "
+                "got %zu", lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float2* stats = reinterpret_cast<float2*>(ws + lay.off_stats);
+  float* zlab = reinterpret_cast<float*>(ws + lay.off_zlab);
+  float* rows_ws = loss_rows != nullptr ? loss_rows : reinterpret_cast<float*>(ws + lay.off_rows);
+  float* lse_ws = lse != nullptr ? lse : reinterpret_cast<float*>(ws + lay.off_lse);
+  int* n_valid = reinterpret_cast<int*>(ws + lay.off_misc);
+  float* sc = reinterpret_cast<float*>(ws + lay.off_misc + 16);
+  GemmArgs g{};
+  g.A = static_cast<const __bf16*>(hidden);
+  g.lda = ldh;
+  g.B = static_cast<const __bf16*>(weight);
+  g.ldb = ldw;
+  g.M = N;
+  g.N = V;
+  g.K = H;
+  g.stats = stats;
+  g.labels = labels;
+  g.label_offset = 0;
+  g.zlab = zlab;
+  g.xf = xf;
+  TS_TRY(launch_gemm<kEpiStats>(g, st, "flce_gemm_stats"));
+  hipLaunchKernelGGL(flce_rows_t, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, stats,
+                     lay.nparts, zlab, labels, N, V, ignore_index, lse_ws, rows_ws);
+  TS_TRY(ts_host::check_launch("flce_rows_t"));
+  if (loss == nullptr) return TS_OK;
+  hipLaunchKernelGGL(flce_count, dim3(1), dim3(256), 0, st, labels, N, ignore_index, n_valid);
+  TS_TRY(ts_host::check_launch("flce_count"));
+  hipLaunchKernelGGL(flce_loss, dim3(1), dim3(256), 0, st, rows_ws, N, n_valid,
+                     reduction == 0 ? 1 : 0, loss, sc);
+  return ts_host::check_launch("flce_loss");
+}
+
+extern "C" size_t ts_flce_backward_workspace_size(int64_t N, int64_t H, int64_t V,
+                                                  int64_t chunk_cols) {
+  if (N <= 0 || H <= 0 || V <= 0) return 0;
+  return bwd_layout(N, H, V, chunk_cols).total;
+}
+
+extern "C" ts_status ts_flce_backward(const void* hidden, int64_t ldh, const void* weight,
+                                      int64_t ldw, const int64_t* labels, int64_t N, int64_t H,
+                                      int64_t V, int64_t ignore_index, int32_t reduction,
+                                      float softcap, float scale, float temperature,
+                                      const float* lse, const float* dloss, int64_t dloss_stride,
+                                      void* grad_hidden, void* grad_weight, int64_t chunk_cols,
+                                      void* workspace, size_t workspace_bytes,
+                                      ts_stream_t stream) {
+  using ts_host::fail;
+  LogitXform xf{};
+  TS_TRY(check_two_pass("flce_backward", hidden, ldh, weight, ldw, labels, N, H, V, reduction,
+                        softcap, scale, temperature, &xf));
+  if (dloss_stride < 0)
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_backward: dloss_stride must be >= 0");
+  if (N > 0 && (lse == nullptr || dloss == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_backward: lse or dloss is NULL");
+  if ((grad_hidden != nullptr && !ts_host::aligned16(grad_hidden)) ||
+      (grad_weight != nullptr && !ts_host::aligned16(grad_weight)))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_backward: gradients must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (N == 0) {
+    // no rows: grad_weight is 0 (grad_hidden is empty)
+    if (grad_weight == nullptr) return TS_OK;
+    const int64_t words = V * H / 2;
+    hipLaunchKernelGGL(fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                       static_cast<uint32_t*>(grad_weight), words, nullptr);
+    return ts_host::check_launch("fill_zero_u32");
+  }
+  if (grad_hidden == nullptr && grad_weight == nullptr) return TS_OK;
+  const BwdLayout lay = bwd_layout(N, H, V, chunk_cols);
+  if (workspace == nullptr || workspace_bytes < lay.total || !ts_host::aligned16(workspace))
+    return fail(TS_ERR_WORKSPACE, "flce_backward: workspace needs %zu bytes (16-byte aligned), "
+                "got %zu", lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  __bf16* D = reinterpret_cast<__bf16*>(ws + lay.off_d);
+  float* acc32 = reinterpret_cast<float*>(ws + lay.off_acc);
+  float* dscale = reinterpret_cast<float*>(ws + lay.off_dscale);
+  int* n_valid = reinterpret_cast<int*>(ws + lay.off_misc);
+  const __bf16* Hd = static_cast<const __bf16*>(hidden);
+  const __bf16* Wd = static_cast<const __bf16*>(weight);
+
+  hipLaunchKernelGGL(flce_count, dim3(1), dim3(256), 0, st, labels, N, ignore_index, n_valid);
+  TS_TRY(ts_host::check_launch("flce_count"));
+  hipLaunchKernelGGL(flce_dscale, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, labels, N,
+                     ignore_index, dloss, dloss_stride, n_valid, reduction == 0 ? 1 : 0, dscale);
+  TS_TRY(ts_host::check_launch("flce_dscale"));
+  using ts_gemm::kKMajor;
+  using ts_gemm::kMNMajor;
+  for (int64_t c = 0; c < lay.nchunks; ++c) {
+    const int64_t v0 = c * lay.chunk;
+    const int64_t Vc = V - v0 < lay.chunk ? V - v0 : lay.chunk;
+    // dlogits of the chunk: logits recomputed by the same GEMM as the forward's
+    GemmArgs g{};
+    g.A = Hd;
+    g.lda = ldh;
+    g.B = Wd + v0 * ldw;
+    g.ldb = ldw;
+    g.M = N;
+    g.N = Vc;
+    g.K = H;
+    g.C = D;
+    g.ldc = lay.chunk;
+    g.labels = labels;
+    g.label_offset = v0;
+    g.lse = lse;
+    g.dscale = dscale;
+    g.xf = xf;
+    TS_TRY(launch_gemm<kEpiDlogits>(g, st, "flce_gemm_dlogits"));
+    if (grad_hidden != nullptr) {
+      // grad_hidden (+)= D [N, Vc] @ W[v0 : v0 + Vc] (the chunk read as the MN-major [H, Vc]
+      // operand); carried in fp32 across chunks and rounded once
+      GemmArgs d{};
+      d.A = D;
+      d.lda = lay.chunk;
+      d.B = Wd + v0 * ldw;
+      d.ldb = ldw;
+      d.M = N;
+      d.N = H;
+      d.K = Vc;
+      d.C = static_cast<__bf16*>(grad_hidden);
+      d.ldc = H;
+      d.C32 = acc32;
+      d.ldc32 = H;
+      if (lay.nchunks == 1) {
+        TS_TRY((launch_gemm<kEpiBf16, kKMajor, kMNMajor>(d, st, "flce_gemm_dhidden")));
+      } else if (c == 0) {
+        TS_TRY((launch_gemm<kEpiF32, kKMajor, kMNMajor>(d, st, "flce_gemm_dhidden")));
+      } else if (c + 1 < lay.nchunks) {
+        TS_TRY((launch_gemm<kEpiAccF32, kKMajor, kMNMajor>(d, st, "flce_gemm_dhidden")));
+      } else {
+        TS_TRY((launch_gemm<kEpiAccBf16, kKMajor, kMNMajor>(d, st, "flce_gemm_dhidden")));
+      }
+    }
+    if (grad_weight != nullptr) {
+      // grad_weight[v0 : v0 + Vc] = D^T @ hidden: D as the MN-major [Vc, N] operand, hidden
+      // as the MN-major [H, N] operand
+      GemmArgs d{};
+      d.A = D;
+      d.lda = lay.chunk;
+      d.B = Hd;
+      d.ldb = ldh;
+      d.M = Vc;
+      d.N = H;
+      d.K = N;
+      d.C = static_cast<__bf16*>(grad_weight) + v0 * H;
+      d.ldc = H;
+      TS_TRY((launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
+    }
+  }
+  return TS_OK;
 }
 
 // ---------------------------------------------------------------------------

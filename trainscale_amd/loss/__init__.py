@@ -10,7 +10,8 @@ from __future__ import annotations
 import torch.nn as nn
 from torch import Tensor
 
-from .linear_ce import LinearCrossEntropyFunction, fused_linear_cross_entropy
+from .linear_ce import (FusedLinearCrossEntropyFunction, LinearCrossEntropyFunction,
+                        chunked_log_softmax, fused_linear_cross_entropy)
 from .sota_losses import (
     ChunkedCrossEntropyLoss,
     CrossEntropyRowsFunction,
@@ -28,7 +29,9 @@ __all__ = [
     "CrossEntropyRowsFunction",
     "UpstreamGradHint",
     "LinearCrossEntropyFunction",
+    "FusedLinearCrossEntropyFunction",
     "fused_linear_cross_entropy",
+    "chunked_log_softmax",
 ]
 
 

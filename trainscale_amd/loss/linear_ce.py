@@ -1,18 +1,30 @@
-"""Fused linear cross-entropy: loss of (hidden @ weight.T) without materialising all logits.
+"""Fused linear cross-entropy: loss of (hidden @ weight.T) without materialising the logits.
 
 TrainScale has no such op; its nearest relative is
 ``chunked_log_softmax(hidden, lm_head[V, H], input_ids)`` (rl_training.py:138-191),
-whose weight layout this API follows, with the keywords of
+whose weight layout and logit transforms (softcapping, then scaling, then
+temperature, rl_training.py:114-122) this API follows, with the keywords of
 ``fast_cross_entropy_loss`` (kernels/triton_kernels.py:427-467).
 
-One call of the gfx950 kernel (``ts_flce_fwd_bwd``) computes the loss and both
-gradients for an upstream gradient of 1, token chunk by token chunk (a chunk's
-bf16 logits are the only [rows, V] scratch). The forward keeps the gradients;
-the backward scales them in place by the upstream gradient on the device
-(nothing is written when it is 1). Numerics follow the reference's bf16 path:
-logits are rounded to bf16 as a bf16 matmul rounds them, softmax statistics
-and the loss are fp32, dlogits are bf16, and the gradient GEMMs accumulate in
-fp32.
+Two schedules run on the gfx950 kernels:
+
+* ``"two_pass"`` (the default; any reduction, any upstream gradient): the
+  forward (``ts_flce_forward``) runs the logits GEMM once and keeps only
+  per-row softmax statistics and the label's logit; no logits are stored. The
+  backward (``ts_flce_backward``) recomputes the logits one vocabulary chunk
+  at a time (about V/8 columns), forms the chunk's dlogits in the GEMM's
+  epilogue and runs the two gradient GEMMs on them: grad_hidden accumulates
+  over the chunks in fp32, grad_weight's rows of the chunk are written
+  directly. Scratch: N x chunk bf16 dlogits plus N x H fp32.
+* ``"fused"`` (mean/sum, no transforms): one call (``ts_flce_fwd_bwd``) forms
+  the loss and both gradients for an upstream gradient of 1, token chunk by
+  token chunk (a chunk's bf16 logits are stored, all N rows when the chunk is
+  not bounded); the backward scales them in place. Three GEMMs instead of
+  four, at the price of the logits scratch.
+
+Numerics follow the reference's bf16 path: logits are rounded to bf16 as a
+bf16 matmul rounds them, softmax statistics and the loss are fp32, dlogits are
+bf16, and the gradient GEMMs accumulate in fp32.
 """
 from __future__ import annotations
 
@@ -23,8 +35,11 @@ from torch import Tensor
 
 from .. import _lib, ops
 from .._lib import check, ptr
+from .sota_losses import SECOND_BACKWARD_MSG
 
-__all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy", "DEFAULT_LOGITS_SCRATCH",
+__all__ = ["LinearCrossEntropyFunction", "FusedLinearCrossEntropyFunction",
+           "fused_linear_cross_entropy", "chunked_log_softmax", "DEFAULT_LOGITS_SCRATCH",
+           "linear_ce_forward", "linear_ce_backward", "linear_ce_forward_backward",
            "VocabShardState", "linear_ce_vocab_phase1", "linear_ce_vocab_phase2"]
 
 # Upper bound on the bf16 logits scratch of one token chunk. 4 GiB keeps a
@@ -34,6 +49,7 @@ __all__ = ["LinearCrossEntropyFunction", "fused_linear_cross_entropy", "DEFAULT_
 DEFAULT_LOGITS_SCRATCH = 4 << 30
 
 _REDUCTIONS = {"mean": 0, "sum": 1}
+_REDUCTIONS_2P = {"mean": 0, "sum": 1, "none": 2}
 
 
 def _chunk_rows(N: int, V: int, chunk_tokens: Optional[int]) -> int:
@@ -42,6 +58,88 @@ def _chunk_rows(N: int, V: int, chunk_tokens: Optional[int]) -> int:
     rows = DEFAULT_LOGITS_SCRATCH // (2 * V)
     rows = max(256, rows // 256 * 256)
     return 0 if rows >= N else rows
+
+
+def _operands(what: str, hidden: Tensor, weight: Tensor, labels: Tensor):
+    dev = _lib.require_gpu(what, hidden, weight, labels)
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: hidden and weight must be bfloat16 (got {hidden.dtype}, "
+                        f"{weight.dtype})")
+    if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError(f"{what}: hidden {tuple(hidden.shape)} and weight "
+                         f"{tuple(weight.shape)} must be [N, H] and [V, H]")
+    hidden, weight = _rows_operand(hidden), _rows_operand(weight)
+    labels = labels.reshape(-1)
+    if labels.shape[0] != hidden.shape[0]:
+        raise ValueError(f"{what}: {labels.shape[0]} labels for {hidden.shape[0]} rows")
+    labels = labels.to(torch.int64).contiguous()
+    return dev, hidden, weight, labels
+
+
+def _ld(t: Tensor) -> int:
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
+def linear_ce_forward(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
+                      reduction: str = "mean", logit_softcapping: float = 0.0,
+                      logit_scaling: float = 0.0, temperature: float = 1.0):
+    """ts_flce_forward: returns (loss fp32 0-d or None for reduction "none",
+    loss_rows fp32 [N], lse fp32 [N]). lse is that of the transformed logits and
+    is what linear_ce_backward needs."""
+    if reduction not in _REDUCTIONS_2P:
+        raise ValueError(f"fused_linear_cross_entropy: reduction must be 'mean', 'sum' or "
+                         f"'none', got {reduction!r}")
+    dev, hidden, weight, labels = _operands("fused_linear_cross_entropy", hidden, weight, labels)
+    N, H = hidden.shape
+    V = weight.shape[0]
+    loss = (torch.empty((), dtype=torch.float32, device=dev) if reduction != "none" else None)
+    rows = torch.empty((N,), dtype=torch.float32, device=dev)
+    lse = torch.empty((N,), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws_bytes = int(lib.ts_flce_forward_workspace_size(N, V))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.ts_flce_forward(
+            ptr(hidden), _ld(hidden), ptr(weight), _ld(weight), ptr(labels), N, H, V,
+            int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
+            float(logit_scaling), float(temperature), ptr(loss), ptr(rows), ptr(lse), ptr(ws),
+            ws_bytes, _lib.stream_handle(dev)), "ts_flce_forward")
+    return loss, rows, lse
+
+
+def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tensor,
+                       dloss: Tensor, ignore_index: int = -100, reduction: str = "mean",
+                       logit_softcapping: float = 0.0, logit_scaling: float = 0.0,
+                       temperature: float = 1.0, need_grad_hidden: bool = True,
+                       need_grad_weight: bool = True, vocab_chunk: Optional[int] = None):
+    """ts_flce_backward: (grad_hidden [N, H] or None, grad_weight [V, H] or None) for the
+    upstream gradient dloss (one value for mean/sum, or [N] per-row values for "none";
+    a single value broadcasts). vocab_chunk: columns per recomputed chunk (default
+    about V/8)."""
+    if reduction not in _REDUCTIONS_2P:
+        raise ValueError(f"fused_linear_cross_entropy: bad reduction {reduction!r}")
+    dev, hidden, weight, labels = _operands("fused_linear_cross_entropy", hidden, weight, labels)
+    N, H = hidden.shape
+    V = weight.shape[0]
+    dloss = dloss.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if dloss.numel() not in (1, N):
+        raise ValueError(f"fused_linear_cross_entropy: {dloss.numel()} upstream values for "
+                         f"{N} rows")
+    stride = 1 if dloss.numel() == N and N > 1 else 0
+    lse = lse.detach().to(torch.float32).reshape(-1).contiguous()
+    gh = torch.empty((N, H), dtype=torch.bfloat16, device=dev) if need_grad_hidden else None
+    gw = torch.empty((V, H), dtype=torch.bfloat16, device=dev) if need_grad_weight else None
+    chunk = int(vocab_chunk) if vocab_chunk else 0
+    lib = _lib.load()
+    ws_bytes = int(lib.ts_flce_backward_workspace_size(N, H, V, chunk))
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.ts_flce_backward(
+            ptr(hidden), _ld(hidden), ptr(weight), _ld(weight), ptr(labels), N, H, V,
+            int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
+            float(logit_scaling), float(temperature), ptr(lse), ptr(dloss), stride, ptr(gh),
+            ptr(gw), chunk, ptr(ws), ws_bytes, _lib.stream_handle(dev)), "ts_flce_backward")
+    return gh, gw
 
 
 def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
@@ -69,6 +167,16 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
     if labels.shape[0] != N:
         raise ValueError(f"fused_linear_cross_entropy: {labels.shape[0]} labels for {N} rows")
     labels = labels.to(torch.int64).contiguous()
+    if N % 8 != 0:
+        # the one-call kernel takes whole groups of 8 rows: pad with ignored rows, which
+        # change neither the loss nor grad_weight, and drop their grad_hidden rows
+        pad = 8 - N % 8
+        hidden = torch.cat([hidden, hidden.new_zeros((pad, H))])
+        labels = torch.cat([labels, labels.new_full((pad,), int(ignore_index))])
+        out = linear_ce_forward_backward(hidden, weight, labels, ignore_index, reduction,
+                                         need_grad_hidden, need_grad_weight, chunk_tokens)
+        loss, rows, lse, gh, gw = out
+        return loss, rows[:N], lse[:N], gh[:N] if gh is not None else None, gw
     ldh = hidden.stride(0) if N > 1 else H
     ldw = weight.stride(0) if V > 1 else H
     loss = torch.empty((), dtype=torch.float32, device=dev)
@@ -179,7 +287,40 @@ def _scale_(t: Optional[Tensor], scale: Tensor) -> None:
 
 
 class LinearCrossEntropyFunction(torch.autograd.Function):
-    """loss = CE(hidden @ weight.T, labels) with the gradients formed in the forward."""
+    """loss = CE(t(hidden @ weight.T), labels), two-pass schedule: the forward keeps
+    per-row statistics only, the backward recomputes the logits by vocabulary chunk.
+    Returns the reduced loss, or the per-row losses [N] for reduction "none" (0 on
+    ignore_index rows). Calling backward twice (retain_graph) recomputes again."""
+
+    @staticmethod
+    def forward(ctx, hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
+                reduction: str = "mean", logit_softcapping: float = 0.0,
+                logit_scaling: float = 0.0, temperature: float = 1.0,
+                vocab_chunk: Optional[int] = None) -> Tensor:
+        shape = hidden.shape
+        h2 = hidden.reshape(-1, shape[-1])
+        loss, rows, lse = linear_ce_forward(h2, weight, labels, ignore_index, reduction,
+                                            logit_softcapping, logit_scaling, temperature)
+        ctx.cfg = (ignore_index, reduction, logit_softcapping, logit_scaling, temperature,
+                   vocab_chunk)
+        ctx.hidden_shape = shape
+        ctx.save_for_backward(h2, weight, labels, lse)
+        return loss if reduction != "none" else rows
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor):
+        h2, weight, labels, lse = ctx.saved_tensors
+        ignore_index, reduction, cap, sc, temp, chunk = ctx.cfg
+        gh, gw = linear_ce_backward(h2, weight, labels, lse, grad_output, ignore_index, reduction,
+                                    cap, sc, temp, need_grad_hidden=ctx.needs_input_grad[0],
+                                    need_grad_weight=ctx.needs_input_grad[1], vocab_chunk=chunk)
+        gh = gh.view(ctx.hidden_shape) if gh is not None else None
+        return gh, gw, None, None, None, None, None, None, None
+
+
+class FusedLinearCrossEntropyFunction(torch.autograd.Function):
+    """loss = CE(hidden @ weight.T, labels) with the gradients formed in the forward
+    (schedule "fused": mean or sum, no logit transforms)."""
 
     @staticmethod
     def forward(ctx, hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
@@ -196,6 +337,10 @@ class LinearCrossEntropyFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output: Tensor):
+        # the saved gradients are scaled in place: a second backward would scale them again
+        if getattr(ctx, "backward_done", False):
+            raise RuntimeError(SECOND_BACKWARD_MSG)
+        ctx.backward_done = True
         gh, gw = ctx.saved_tensors
         scale = grad_output.detach().float().reshape(1).contiguous()
         _scale_(gh, scale)
@@ -208,15 +353,54 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
                                ignore_index: int = -100, reduction: str = "mean",
                                logit_softcapping: float = 0.0,
                                logit_scaling: float = 0.0,
+                               temperature: float = 1.0,
+                               schedule: str = "two_pass",
+                               vocab_chunk: Optional[int] = None,
                                chunk_tokens: Optional[int] = None) -> Tensor:
-    """Mean (or sum) cross-entropy of hidden @ weight.T against labels.
+    """Cross-entropy of hidden @ weight.T against labels, without the logits in memory.
 
     hidden [..., H] and weight [V, H] in bfloat16 (the lm_head layout of
-    rl_training.py:156-162); labels [...] int64 with ignore_index rows skipped.
+    rl_training.py:156-162); labels [...] int64, ignore_index rows skipped.
+    The logits z are transformed as selective_log_softmax does
+    (rl_training.py:114-122): t = softcap * tanh(z / softcap) when
+    logit_softcapping > 0, then t * logit_scaling when logit_scaling > 0, then
+    t / temperature. reduction "mean" (over non-ignored rows), "sum", or "none"
+    (per-row losses, shaped like labels). schedule "two_pass" (default) or
+    "fused" (mean/sum without transforms; chunk_tokens bounds its logits
+    scratch, None = one chunk up to 4 GiB).
     """
-    if logit_softcapping != 0.0 or logit_scaling != 0.0:
-        raise NotImplementedError(
-            "fused_linear_cross_entropy: logit softcapping/scaling are not implemented by the "
-            "fused kernel; apply them with fast_cross_entropy_loss on explicit logits")
-    return LinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index, reduction,
-                                            chunk_tokens)
+    if schedule == "fused":
+        if reduction not in _REDUCTIONS:
+            raise ValueError("fused_linear_cross_entropy: schedule 'fused' takes reduction "
+                             "'mean' or 'sum'")
+        if logit_softcapping != 0.0 or logit_scaling != 0.0 or temperature != 1.0:
+            raise ValueError("fused_linear_cross_entropy: schedule 'fused' takes no logit "
+                             "transforms; use schedule 'two_pass'")
+        return FusedLinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index,
+                                                     reduction, chunk_tokens)
+    if schedule != "two_pass":
+        raise ValueError(f"fused_linear_cross_entropy: unknown schedule {schedule!r}")
+    out = LinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index, reduction,
+                                           float(logit_softcapping), float(logit_scaling),
+                                           float(temperature), vocab_chunk)
+    if reduction == "none":
+        out = out.view(labels.shape)
+    return out
+
+
+def chunked_log_softmax(hidden_states: Tensor, lm_head: Tensor, input_ids: Tensor,
+                        num_chunks: int = 4, temperature: float = 1.0,
+                        logit_softcapping: float = 0.0, logit_scale: float = 0.0) -> Tensor:
+    """Drop-in for chunked_log_softmax (rl_training.py:138-191): log-probabilities
+    [B, L] of input_ids under the transformed logits of hidden_states [B, L, H] @
+    lm_head[V, H].T, differentiable in hidden_states and lm_head.
+
+    The reference splits the sequence into num_chunks and materialises each
+    chunk's [B, chunk, V] logits; here the logits are never stored (the two-pass
+    schedule), so num_chunks is accepted for the signature and unused.
+    """
+    del num_chunks
+    rows = fused_linear_cross_entropy(hidden_states, lm_head, input_ids, ignore_index=-(1 << 62),
+                                      reduction="none", logit_softcapping=logit_softcapping,
+                                      logit_scaling=logit_scale, temperature=temperature)
+    return -rows
