@@ -4,18 +4,25 @@ Headline step (the metric's value): forward of C1 (RMSNorm x[8,2048,4096]),
 C2 (RoPE Q[8,2048,32,128] + K[8,2048,8,128], theta 500000, in-register sin/cos)
 and C3 (cross-entropy over logits[16384,128256] with 10% ignored labels), then
 their backwards in reverse order (C3, C2, C1), as a training step runs them.
-Between the forward and the backward of one op the other ops move gigabytes,
-so no op re-reads its inputs from the 256 MB last-level cache. All inputs are
-synthetic, seeded and resident in HBM before timing.
+Two sets of inputs alternate from step to step, so no op reads data that an op
+of the last gigabytes of traffic touched (the last-level cache is 256 MB); a
+second timed run writes a 512 MB buffer before every op, outside the op's
+events, and reports how much the per-op times move. All inputs are synthetic,
+seeded and resident in HBM before timing.
 
-value = algorithmic bytes of the step / step time (GB/s). The roofline object is
-for the dominant kernel of the step, from HIP-event durations taken on torch's
-current stream (the stream every kernel is launched on); its `traffic` is the
-HBM bytes per launch that rocprofv3 --pmc measured (profiles/pmc_traffic.txt).
+value = algorithmic bytes of the step / step time (GB/s), with the per-config
+byte counts of the scope contract (C3 schedule B: 2 N V 2 bytes). The roofline
+object is for the dominant kernel of the step, from HIP-event durations taken
+on torch's current stream (the stream every kernel is launched on); its
+`traffic` is the HBM bytes per launch that rocprofv3 --pmc measured
+(profiles/pmc_traffic.txt). Each op is also set beside the library's flat
+streaming copy of the same bytes (ts_stream_copy).
 
 Also reported, outside the timed step: C4 (packed varlen RMSNorm + RoPE with
 position_ids at 70B shapes, GB/s) and C5 (fused linear cross-entropy, TFLOP/s
-against the bf16 MFMA peak), each with its own timing.
+against the bf16 MFMA peak; the default two-pass schedule, plus the one-call
+schedule with all logits in one chunk and the RL form as separate lines), each
+with its own timing, and the reference's eager CPU path per config.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-extra] [--copy-probe]
@@ -46,8 +53,6 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="skip the C4 and C5 sections")
-    p.add_argument("--cpu-seconds", type=float, default=12.0,
-                   help="approximate CPU time budget of the baseline sample")
     p.add_argument("--copy-probe", action="store_true",
                    help="before warm-up, copy a 1 GiB buffer 3 times (a plain copy of known "
                         "size, the reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -70,64 +75,14 @@ def load_traffic():
     return out
 
 
-def cpu_baseline(budget_s: float):
-    """Times the oracle (a CPU port of the reference math) on bounded samples of C1-C3."""
-    import torch
-
-    import oracle
-    from trainscale_amd import workloads as W
-
-    torch.set_num_threads(os.cpu_count() or 1)
-    cores = torch.get_num_threads()
-    g = torch.Generator().manual_seed(0)
-    bf = torch.bfloat16
-    rows1, tok2, rows3 = 2048, 1024, 48
-    x = torch.randn(rows1, 4096, generator=g).to(bf)
-    w = (1 + 0.02 * torch.randn(4096, generator=g)).to(bf)
-    dy = torch.randn(rows1, 4096, generator=g).to(bf)
-    q = torch.randn(1, tok2, 32, 128, generator=g).to(bf)
-    k = torch.randn(1, tok2, 8, 128, generator=g).to(bf)
-    cos, sin = oracle.rope_tables(128, tok2, 500000.0)
-    pos = oracle.rope_positions(1, tok2)
-    logits = (2 * torch.randn(rows3, 128256, generator=g)).to(bf)
-    labels = torch.randint(0, 128256, (rows3,), generator=g)
-    labels[::10] = -100
-    n_valid = int((labels != -100).sum())
-
-    def one():
-        y, rstd = oracle.rms_norm_fwd(x, w, 1e-6)
-        oracle.rms_norm_bwd(dy, x, w, rstd)
-        for t in (q, k):
-            oracle.rope_apply(t, cos, sin, pos)
-            oracle.rope_apply(t, cos, sin, pos, backward=True)
-        oracle.ce_fwd(logits, labels)
-        oracle.ce_bwd(logits, labels, torch.tensor(1.0 / n_valid))
-
-    one()  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 1000:
-            break
-    times.sort()
-    t = times[len(times) // 2]
-    b1 = W.rmsnorm_bytes(rows1, 4096)
-    b2 = W.rope_bytes(tok2, 40, 128)
-    b3 = W.ce_bytes(rows3, n_valid, 128256)
-    sample_bytes = sum(b1.values()) + sum(b2.values()) + sum(b3.values())
-    return {
-        "value": round(sample_bytes / t / 1e9, 3),
-        "unit": "GB/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": (f"oracle (torch CPU fp32 restatement of the reference math) fwd+bwd on "
-                   f"C1 {rows1} rows x 4096, C2 {tok2} tokens x (32+8) heads x 128, "
-                   f"C3 {rows3} rows x 128256; median of {len(times)} runs, "
-                   f"{t * 1e3:.1f} ms per sample; CPU {cpu_model()}"),
-    }
+def cpu_threads() -> int:
+    """Host threads for the CPU baseline: the cores this process may run on, capped by
+    OMP_NUM_THREADS when the environment sets it (the GPU box's share)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n or 1)
 
 
 def cpu_model() -> str:
@@ -142,33 +97,117 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline_linear_ce(budget_s: float):
-    """The oracle's linear CE (fp32 matmuls + CE) on 64 tokens of C5, in TFLOP/s."""
+def _median_s(fn, reps: int = 3) -> float:
+    fn()  # warm-up
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baseline(gpu_ms: dict, step_bytes: dict):
+    """The reference's eager op sequences (oracle.eager) fwd+bwd on the host cores, per
+    config, each on a slice of rows timed with warm-up 1 and median of 3 and scaled
+    linearly to the full config ("scaled"). gpu_ms: this run's GPU time per config."""
     import torch
 
     import oracle
+    from oracle import eager as E
+    from trainscale_amd import workloads as W
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    g = torch.Generator().manual_seed(4)
-    n, h, v = 64, 4096, 128256
-    hid = torch.randn(n, h, generator=g).to(torch.bfloat16)
-    wt = (0.02 * torch.randn(v, h, generator=g)).to(torch.bfloat16)
-    lab = torch.randint(0, v, (n,), generator=g)
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        oracle.linear_ce(hid, wt, lab, bf16_logits=True)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 100:
-            break
-    times.sort()
-    t = times[len(times) // 2]
-    flops = 3 * 2 * n * h * v
-    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s",
-            "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle linear_ce fwd+bwd on 64 tokens of C5 (H 4096, V 128256); "
-                      f"median of {len(times)} runs, {t:.2f} s per sample; CPU {cpu_model()}"}
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
+    out = {}
+
+    def entry(name, ops, rows, full, sample_s, tokens_full, gb=None, flop=None):
+        s_full = sample_s * full / rows
+        e = {"ops": ops, "sample": f"{rows} of {full} rows, scaled", "sample_s": round(sample_s, 4),
+             "seconds": round(s_full, 4), "tokens_per_s": round(tokens_full / s_full, 1)}
+        if gb is not None:
+            e["GB_s"] = round(gb / s_full / 1e9, 3)
+        if flop is not None:
+            e["TFLOP_s"] = round(flop / s_full / 1e12, 4)
+        if gpu_ms.get(name):
+            e["gpu_ms"] = gpu_ms[name]
+            e["speedup"] = round(s_full * 1e3 / gpu_ms[name], 1)
+        out[name] = e
+
+    # C1 RMSNorm [16384, 4096]
+    rows = 2048
+    x = torch.randn(rows, 4096, generator=g).to(bf)
+    w = (1 + 0.02 * torch.randn(4096, generator=g)).to(bf)
+    dy = torch.randn(rows, 4096, generator=g).to(bf)
+    entry("C1", "triton_kernels.py:612-616 fwd + layernorm_kernels.py:777-781,804-805 bwd", rows,
+          16384, _median_s(lambda: E.rmsnorm(x, w, dy)), 16384, gb=step_bytes["C1"])
+    del x, dy
+    # C2 RoPE Q [8,2048,32,128], K [8,2048,8,128]
+    q = torch.randn(1, 2048, 32, 128, generator=g).to(bf)
+    k = torch.randn(1, 2048, 8, 128, generator=g).to(bf)
+    cos, sin = oracle.rope_tables(128, 2048, 500000.0)
+    cos, sin = cos.to(bf), sin.to(bf)
+    entry("C2", "triton_kernels.py:908-925 fwd, the same rotation with -sin bwd", 2048, 16384,
+          _median_s(lambda: E.rope(q, k, q, k, cos, sin)), 16384, gb=step_bytes["C2"])
+    # C3 CE [16384, 128256], 10% ignored
+    rows = 1024
+    logits = (2 * torch.randn(rows, 128256, generator=g)).to(bf)
+    labels = torch.randint(0, 128256, (rows,), generator=g)
+    labels[::10] = -100
+    entry("C3", "ChunkedCrossEntropyLoss training path, sota_losses.py:695-744, + autograd bwd",
+          rows, 16384, _median_s(lambda: E.ce_chunked(logits, labels)), 16384,
+          gb=step_bytes["C3"])
+    entry("C3_float", "F.cross_entropy(logits.float()), triton_kernels.py:328-337 + "
+          "fast_cross_entropy_loss :459-467, + autograd bwd", rows, 16384,
+          _median_s(lambda: E.ce_float(logits, labels)), 16384, gb=step_bytes["C3"])
+    out["C3_float"].pop("speedup", None)
+    if gpu_ms.get("C3"):
+        out["C3_float"]["speedup"] = round(out["C3_float"]["seconds"] * 1e3 / gpu_ms["C3"], 1)
+    del logits
+    # C4 packed: RMSNorm [32768, 8192] + RoPE 64q + 8k heads with position_ids
+    rows = 2048
+    x = torch.randn(rows, 8192, generator=g).to(bf)
+    w = (1 + 0.02 * torch.randn(8192, generator=g)).to(bf)
+    dy = torch.randn(rows, 8192, generator=g).to(bf)
+    q = torch.randn(1, rows, 64, 128, generator=g).to(bf)
+    k = torch.randn(1, rows, 8, 128, generator=g).to(bf)
+    pos = W.packed_position_ids(W.packed_doc_lengths(rows, 64, 4096, seed=3))[:, :rows]
+    cos, sin = oracle.rope_tables(128, 4096, 500000.0)
+    cos, sin = cos.to(bf), sin.to(bf)
+
+    def c4():
+        E.rmsnorm(x, w, dy)
+        E.rope(q, k, q, k, cos, sin, position_ids=pos)
+
+    entry("C4", "C1's and C2's sequences at the 70B shapes, cos/sin gathered at position_ids "
+          "(rope_kernels.py:975-976)", rows, 32768, _median_s(c4), 32768, gb=step_bytes["C4"])
+    del x, dy, q, k
+    # C5 linear CE: hidden [8192, 4096] @ W[128256, 4096]^T -> CE
+    rows = 128
+    hid = torch.randn(rows, 4096, generator=g).to(bf)
+    wt = (0.02 * torch.randn(128256, 4096, generator=g)).to(bf)
+    lab = torch.randint(0, 128256, (rows,), generator=g)
+    lab[::20] = -100
+    entry("C5", "hidden @ lm_head.t() (bf16, rl_training.py:177) -> F.cross_entropy(fp32) "
+          "+ autograd bwd", rows, 8192, _median_s(lambda: E.linear_ce(hid, wt, lab)), 8192,
+          flop=W.linear_ce_flops(8192, 4096, 128256))
+    del wt
+    head_s = out["C1"]["seconds"] + out["C2"]["seconds"] + out["C3"]["seconds"]
+    head_b = step_bytes["C1"] + step_bytes["C2"] + step_bytes["C3"]
+    return {
+        "value": round(head_b / head_s / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"the reference's eager PyTorch sequences (oracle/eager.py) for C1+C2+C3 "
+                   f"(ChunkedCrossEntropyLoss for C3), fwd+bwd on row slices scaled linearly to "
+                   f"the full configs: {head_s:.2f} s for the headline step's bytes; "
+                   f"warm-up 1, median of 3; CPU {cpu_model()}, {threads} threads"),
+        "cpu_model": cpu_model(),
+        "configs": out,
+    }
 
 
 def time_ms(fn, steps: int, warmup: int) -> float:
@@ -372,8 +411,12 @@ def bench_next_rows(dev, steps: int, warmup: int):
     return res
 
 
-def bench_linear_ce(dev, steps: int, warmup: int, cpu: bool, cpu_seconds: float):
-    """C5: fused linear CE fwd+bwd (loss, grad_hidden, grad_weight) in one call."""
+def bench_linear_ce(dev, steps: int, warmup: int):
+    """C5: fused linear CE fwd+bwd (loss, grad_hidden, grad_weight). The default is the
+    two-pass schedule (ts_flce_forward then ts_flce_backward: no [N, V] logits stored,
+    four GEMMs executed); also timed: the one-call schedule with all logits in one
+    chunk (opt-in, three GEMMs) and the RL form (per-token losses, temperature, per-row
+    upstream gradients) through the two-pass schedule."""
     import torch
 
     from trainscale_amd import _lib
@@ -385,36 +428,119 @@ def bench_linear_ce(dev, steps: int, warmup: int, cpu: bool, cpu_seconds: float)
     N, H = h.shape
     V = w.shape[0]
     lib = _lib.load()
-    chunk = _chunk_rows(N, V, None)
-    ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk, 1))
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(dev)
+    P = _lib.ptr
     loss = torch.empty((), dtype=torch.float32, device=dev)
     rows = torch.empty((N,), dtype=torch.float32, device=dev)
     lse = torch.empty((N,), dtype=torch.float32, device=dev)
     gh = torch.empty_like(h)
     gw = torch.empty_like(w)
-    stream = _lib.stream_handle(dev)
-
-    def step():
-        _lib.check(lib.ts_flce_fwd_bwd(
-            _lib.ptr(h), H, _lib.ptr(w), H, _lib.ptr(labels), N, H, V, -100, 0, _lib.ptr(loss),
-            _lib.ptr(rows), _lib.ptr(lse), _lib.ptr(gh), _lib.ptr(gw), chunk, _lib.ptr(ws),
-            ws_bytes, stream), "ts_flce_fwd_bwd")
-
-    ms = time_ms(step, max(3, steps // 2), max(1, warmup // 2))
+    one = torch.ones((1,), dtype=torch.float32, device=dev)
+    ws_f = int(lib.ts_flce_forward_workspace_size(N, V))
+    ws_b = int(lib.ts_flce_backward_workspace_size(N, H, V, 0))
+    wsf = torch.empty((ws_f,), dtype=torch.uint8, device=dev)
+    wsb = torch.empty((ws_b,), dtype=torch.uint8, device=dev)
     flops = W.linear_ce_flops(N, H, V)
+
+    def fwd(red=0, temp=1.0):
+        _lib.check(lib.ts_flce_forward(
+            P(h), H, P(w), H, P(labels), N, H, V, -100, red, 0.0, 0.0, temp, P(loss), P(rows),
+            P(lse), P(wsf), ws_f, stream), "ts_flce_forward")
+
+    def bwd(red=0, temp=1.0, up=one, stride=0):
+        _lib.check(lib.ts_flce_backward(
+            P(h), H, P(w), H, P(labels), N, H, V, -100, red, 0.0, 0.0, temp, P(lse), P(up),
+            stride, P(gh), P(gw), 0, P(wsb), ws_b, stream), "ts_flce_backward")
+
+    def two_pass():
+        fwd()
+        bwd()
+
+    reps, warm = max(3, steps // 2), max(1, warmup // 2)
+    ms = time_ms(two_pass, reps, warm)
+    ms_f = time_ms(fwd, reps, warm)
     tf = flops / (ms * 1e-3) / 1e12
     out = {"workload": (f"C5 fused linear CE: hidden [{N},{H}] bf16, lm_head [{V},{H}] bf16, "
-                        f"5% ignored, mean; loss + grad_hidden + grad_weight; token chunk "
-                        f"{chunk or N} rows"),
-           "ms": round(ms, 4), "algorithmic_flop": flops, "TFLOP_s": round(tf, 1),
+                        f"5% ignored, mean; loss + grad_hidden + grad_weight; two-pass schedule "
+                        f"(forward keeps row statistics only; backward recomputes the logits in "
+                        f"vocabulary chunks of {N}x{-(-((V + 7) // 8) // 256) * 256} bf16)"),
+           "schedule": "two_pass",
+           "ms": round(ms, 4), "forward_ms": round(ms_f, 4), "backward_ms": round(ms - ms_f, 4),
+           "algorithmic_flop": flops, "executed_flop": flops // 3 * 4,
+           "TFLOP_s": round(tf, 1),
+           "executed_TFLOP_s": round(flops // 3 * 4 / (ms * 1e-3) / 1e12, 1),
+           "workspace_bytes": ws_f + ws_b,
+           "full_logits_bytes": N * V * 2,
            "roofline": {"bound": "mfma", "achieved": round(tf, 1),
                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)},
            "tokens_per_s": round(N / (ms * 1e-3), 1)}
-    if cpu:
-        out["cpu_baseline"] = cpu_baseline_linear_ce(cpu_seconds)
+    del wsf, wsb
+    torch.cuda.empty_cache()
+
+    # RL form: per-token losses at temperature 0.9, per-row upstream gradients
+    up_rows = torch.randn((N,), device=dev, generator=torch.Generator(device=dev).manual_seed(6))
+    ws_f = int(lib.ts_flce_forward_workspace_size(N, V))
+    wsf = torch.empty((ws_f,), dtype=torch.uint8, device=dev)
+    wsb = torch.empty((ws_b,), dtype=torch.uint8, device=dev)
+
+    def rl():
+        fwd(red=2, temp=0.9)
+        bwd(red=2, temp=0.9, up=up_rows, stride=1)
+
+    ms_rl = time_ms(rl, reps, warm)
+    tf_rl = flops / (ms_rl * 1e-3) / 1e12
+    out["rl_form"] = {"what": "reduction none, temperature 0.9, per-row upstream gradients "
+                              "(chunked_log_softmax's use by GRPOCompute)",
+                      "ms": round(ms_rl, 4), "TFLOP_s": round(tf_rl, 1),
+                      "frac": round(tf_rl / MFMA_BF16_PEAK_TFLOPS, 4)}
+    del wsf, wsb
+    torch.cuda.empty_cache()
+
+    # one-call schedule, one token chunk: the full [N, V] logits in the workspace (opt-in)
+    chunk = _chunk_rows(N, V, None)
+    ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk, 1))
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+
+    def one_call():
+        _lib.check(lib.ts_flce_fwd_bwd(
+            P(h), H, P(w), H, P(labels), N, H, V, -100, 0, P(loss), P(rows), P(lse), P(gh),
+            P(gw), chunk, P(ws), ws_bytes, stream), "ts_flce_fwd_bwd")
+
+    ms1 = time_ms(one_call, reps, warm)
+    tf1 = flops / (ms1 * 1e-3) / 1e12
+    out["one_chunk_schedule"] = {
+        "what": "one call, gradients formed in the forward, all [N, V] bf16 logits in one "
+                "chunk (materialised: not the C5 configuration; reported apart)",
+        "ms": round(ms1, 4), "TFLOP_s": round(tf1, 1),
+        "frac": round(tf1 / MFMA_BF16_PEAK_TFLOPS, 4), "workspace_bytes": ws_bytes}
+    del ws, c5, h, w, labels, gh, gw
+    torch.cuda.empty_cache()
     return out
+
+
+def copy_ceiling(dev, nbytes: int, steps: int):
+    """ms of the library's flat streaming copy moving nbytes (nbytes / 2 read, nbytes / 2
+    written), alternating two buffer pairs so no repeat finds its source in the cache."""
+    import torch
+
+    from trainscale_amd import _lib
+
+    half = max(16, (nbytes // 2) // 16 * 16)
+    lib = _lib.load()
+    bufs = [(torch.ones(half, dtype=torch.uint8, device=dev),
+             torch.empty(half, dtype=torch.uint8, device=dev)) for _ in range(2)]
+    stream = _lib.stream_handle(dev)
+    it = iter(range(1 << 30))
+
+    def copy():
+        src, dst = bufs[next(it) % 2]
+        _lib.check(lib.ts_stream_copy(_lib.ptr(dst), _lib.ptr(src), half, stream),
+                   "ts_stream_copy")
+
+    ms = time_ms(copy, steps, 2)
+    del bufs
+    return ms
 
 
 def main():
@@ -435,22 +561,30 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    c1 = W.rmsnorm_workload(dev)
-    c2 = W.rope_workload(dev)
-    c3 = W.ce_workload(dev)
-    x, w, dy = c1.tensors["x"], c1.tensors["w"], c1.tensors["dy"]
-    x2d, ldx = ops.as_rows(x)
-    dy2d, lddy = ops.as_rows(dy)
-    q, k, dq, dk = (c2.tensors[n] for n in ("q", "k", "dq", "dk"))
+    # two input sets (seeds of set 1 offset by 100), alternating from step to step
+    sets = []
+    for k in range(2):
+        c1 = W.rmsnorm_workload(dev, seed_offset=100 * k)
+        c2 = W.rope_workload(dev, seed_offset=100 * k)
+        c3 = W.ce_workload(dev, seed_offset=100 * k)
+        x2d, ldx = ops.as_rows(c1.tensors["x"])
+        dy2d, lddy = ops.as_rows(c1.tensors["dy"])
+        sets.append(dict(x2d=x2d, ldx=ldx, dy2d=dy2d, lddy=lddy, w=c1.tensors["w"],
+                         q=c2.tensors["q"], k=c2.tensors["k"], dq=c2.tensors["dq"],
+                         dk=c2.tensors["dk"], logits=c3.tensors["logits"],
+                         labels=c3.tensors["labels"]))
     inv_freq = _base_inv_freq(500000.0, 128, "cpu")
-    q_out, k_out = torch.empty_like(q), torch.empty_like(k)
-    dq_out, dk_out = torch.empty_like(dq), torch.empty_like(dk)
-    logits, labels = c3.tensors["logits"], c3.tensors["labels"]
-    N, V = logits.shape
-    n_valid = int((labels != -100).sum())
-    grad = torch.empty_like(logits)
-    dloss = torch.full((1,), 1.0 / n_valid, device=dev)
+    S0 = sets[0]
+    q_out, k_out = torch.empty_like(S0["q"]), torch.empty_like(S0["k"])
+    dq_out, dk_out = torch.empty_like(S0["dq"]), torch.empty_like(S0["dk"])
+    N, V = S0["logits"].shape
+    for st in sets:
+        n_valid = int((st["labels"] != -100).sum())
+        st["dloss"] = torch.full((1,), 1.0 / n_valid, device=dev)
+        st["n_valid"] = n_valid
+    grad = torch.empty_like(S0["logits"])
     upstream = torch.ones((1,), dtype=torch.float32, device=dev)
+    tokens = 3 * 16384
     torch.cuda.synchronize()
 
     if args.copy_probe:
@@ -461,12 +595,15 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    bytes_c1 = W.rmsnorm_bytes(x2d.shape[0], x2d.shape[1])
-    bytes_c2 = W.rope_bytes(q.shape[0] * q.shape[1], q.shape[2] + k.shape[2], 128)
-    bytes_c3 = W.ce_bytes_fused(N, n_valid, V)
+    rows1, cols1 = S0["x2d"].shape
+    bytes_c1 = W.rmsnorm_bytes(rows1, cols1)
+    bytes_c2 = W.rope_bytes(S0["q"].shape[0] * S0["q"].shape[1],
+                            S0["q"].shape[2] + S0["k"].shape[2], 128)
+    # the scope contract's schedule-B count: every row read and written (2 N V 2 bytes)
+    bytes_c3 = 2 * N * V * 2
     op_bytes = {
         "rmsnorm_fwd": bytes_c1["fwd"], "rope_fwd": bytes_c2["fwd"], "ce_fwd_bwd": bytes_c3,
-        "ce_bwd_scale": 4, "rope_bwd": bytes_c2["bwd"], "rmsnorm_bwd": bytes_c1["bwd"],
+        "ce_bwd_scale": 0, "rope_bwd": bytes_c2["bwd"], "rmsnorm_bwd": bytes_c1["bwd"],
     }
     kernel_names = {"rmsnorm_fwd": "rms_fwd_reg", "rope_fwd": "rope_tok_kernel",
                     "ce_fwd_bwd": "ce_fused_vec", "ce_bwd_scale": "scale_inplace",
@@ -474,53 +611,72 @@ def main():
     step_bytes = sum(op_bytes.values())
     order = list(op_bytes)
     state = {}
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
 
-    def step(events=None):
+    def step(s, events=None, do_flush=False):
+        st = sets[s % 2]
+
         def mark(i):
             if events is not None:
                 events[i].record()
-        mark(0)
-        state["y"], state["rstd"] = ops.rmsnorm_forward(x2d, ldx, w, 1e-6)
-        mark(1)
-        ops.rope_apply(q, q_out, k, k_out, inv_freq=inv_freq)
-        mark(2)
-        # schedule B: the forward reads each valid row once and writes its gradient
-        state["ce"] = ops.ce_forward_backward(logits, V, labels, dloss, grad=grad)
-        mark(3)
-        # the backward applies the upstream gradient: a device-side no-op when it is 1
-        ops.scale_(grad, upstream)
-        mark(4)
-        ops.rope_apply(dq, dq_out, dk, dk_out, inv_freq=inv_freq, backward=True)
-        mark(5)
-        ops.rmsnorm_backward(dy2d, lddy, x2d, ldx, w, state["rstd"], need_dw=True)
-        mark(6)
 
-    for _ in range(args.warmup):
-        step()
+        def op(i, fn):
+            if do_flush:
+                flush.fill_(s & 0xFF)  # 512 MB written between ops, outside their events
+            mark(2 * i)
+            fn()
+            mark(2 * i + 1)
+
+        def rms_fwd():
+            state["rstd"] = ops.rmsnorm_forward(st["x2d"], st["ldx"], st["w"], 1e-6)[1]
+
+        op(0, rms_fwd)
+        op(1, lambda: ops.rope_apply(st["q"], q_out, st["k"], k_out, inv_freq=inv_freq))
+        # schedule B: the forward reads each valid row once and writes its gradient
+        op(2, lambda: ops.ce_forward_backward(st["logits"], V, st["labels"], st["dloss"],
+                                              grad=grad))
+        # the backward applies the upstream gradient: a device-side no-op when it is 1
+        op(3, lambda: ops.scale_(grad, upstream))
+        op(4, lambda: ops.rope_apply(st["dq"], dq_out, st["dk"], dk_out, inv_freq=inv_freq,
+                                     backward=True))
+        op(5, lambda: ops.rmsnorm_backward(st["dy2d"], st["lddy"], st["x2d"], st["ldx"],
+                                           st["w"], state["rstd"], need_dw=True))
+
+    for s in range(args.warmup):
+        step(s)
     torch.cuda.synchronize()
+
+    def run(do_flush):
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(12)]
+              for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(args.steps):
+            step(s, ev[s], do_flush)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        per_op = {}
+        for i, name in enumerate(order):
+            per_op[name] = sum(ev[s][2 * i].elapsed_time(ev[s][2 * i + 1])
+                               for s in range(args.steps)) / args.steps
+        return elapsed, per_op
 
     # timed region: exactly K steps, synchronised on both sides
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        step(ev[s])
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-
-    per_op = {name: [] for name in order}
-    for s in range(args.steps):
-        for i, name in enumerate(order):
-            per_op[name].append(ev[s][i].elapsed_time(ev[s][i + 1]))  # ms
+    elapsed, per_op = run(False)
     ms_step = elapsed * 1e3 / args.steps
     value = step_bytes / (ms_step * 1e-3) / 1e9
+    # the same steps with 512 MB written before every op (outside the op's events)
+    _, per_op_flushed = run(True)
+    del flush
     kernels = {}
     for name in order:
-        ms = sum(per_op[name]) / len(per_op[name])
-        gbs = op_bytes[name] / (ms * 1e-3) / 1e9
-        kernels[name] = {"kernel": kernel_names[name], "ms": round(ms, 4),
-                         "bytes": op_bytes[name], "GB_s": round(gbs, 1),
-                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        ms = per_op[name]
+        b = op_bytes[name]
+        kernels[name] = {"kernel": kernel_names[name], "ms": round(ms, 4), "bytes": b,
+                         "GB_s": round(b / (ms * 1e-3) / 1e9, 1),
+                         "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "ms_after_512MB_flush": round(per_op_flushed[name], 4)}
+    kernels["ce_fwd_bwd"]["bytes_touched"] = W.ce_bytes_fused(N, S0["n_valid"], V)
     dom = max(order, key=lambda n: kernels[n]["ms"])
     traffic = load_traffic().get(kernel_names[dom])
     roofline = {
@@ -534,7 +690,8 @@ def main():
         "traffic": traffic,
         "algorithmic_bytes": op_bytes[dom],
     }
-    tokens = c1.tokens + c2.tokens + c3.tokens
+    op_sum = sum(per_op.values())
+    op_sum_flushed = sum(per_op_flushed.values())
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -553,30 +710,51 @@ def main():
                          "theta 5e5 in-register + C3 CE logits[16384,128256] 10% ignored "
                          "(schedule B: the forward reads each valid row once and writes the "
                          "gradient; the backward scales it by the upstream gradient, a "
-                         "device-side no-op at 1); fwd C1,C2,C3 then bwd C3,C2,C1"),
+                         "device-side no-op at 1); fwd C1,C2,C3 then bwd C3,C2,C1; two input "
+                         "sets alternating between steps"),
             "ce_schedule": "B",
             "step_bytes": step_bytes,
+            "byte_count": ("scope contract: C1 671,244,288 + C2 671,088,640 + C3 schedule B "
+                           "2*N*V*2 = 8,405,385,216 (the kernel skips the reads of ignored "
+                           "rows: bytes_touched)"),
             "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
             "tokens_per_s": round(tokens / (ms_step * 1e-3), 1),
             "parallelism": "single GPU",
         },
         "roofline": roofline,
         "kernels": kernels,
+        "llc_check": {
+            "what": "sum of per-op event times without and with a 512 MB write before every "
+                    "op (outside the events)",
+            "op_sum_ms": round(op_sum, 4), "op_sum_ms_flushed": round(op_sum_flushed, 4),
+            "ratio": round(op_sum_flushed / op_sum, 4)},
         "device": torch.cuda.get_device_name(dev),
     }
-    # free the headline step's buffers before the extra sections
-    del c1, c2, c3, x, w, dy, x2d, dy2d, q, k, dq, dk, q_out, k_out, dq_out, dk_out
-    del logits, labels, grad, state, upstream
+    del sets, S0, q_out, k_out, dq_out, dk_out, grad, state, upstream
     torch.cuda.empty_cache()
+    # each op beside the flat streaming copy of the same bytes
+    for name in order:
+        if op_bytes[name] > 0:
+            cms = copy_ceiling(dev, op_bytes[name], args.steps)
+            kernels[name]["copy_same_bytes_GB_s"] = round(op_bytes[name] / (cms * 1e-3) / 1e9, 1)
+            kernels[name]["frac_of_copy"] = round(cms / kernels[name]["ms"], 4)
     out["device_reference"] = device_reference(dev)
+    gpu_ms = {"C1": round(kernels["rmsnorm_fwd"]["ms"] + kernels["rmsnorm_bwd"]["ms"], 4),
+              "C2": round(kernels["rope_fwd"]["ms"] + kernels["rope_bwd"]["ms"], 4),
+              "C3": round(kernels["ce_fwd_bwd"]["ms"] + kernels["ce_bwd_scale"]["ms"], 4)}
     if not args.no_extra:
         out["c4_packed"] = bench_packed(dev, args.steps, args.warmup)
-        out["c5_linear_ce"] = bench_linear_ce(dev, args.steps, args.warmup,
-                                              cpu=not args.no_cpu_baseline,
-                                              cpu_seconds=args.cpu_seconds)
+        gpu_ms["C4"] = out["c4_packed"]["ms"]
+        out["c5_linear_ce"] = bench_linear_ce(dev, args.steps, args.warmup)
+        gpu_ms["C5"] = out["c5_linear_ce"]["ms"]
         out["next_rows"] = bench_next_rows(dev, args.steps, args.warmup)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        c4b = W.rmsnorm_bytes(32768, 8192)
+        c4r = W.rope_bytes(32768, 72, 128, pos_bytes=32768 * 8)
+        out["cpu_baseline"] = cpu_baseline(gpu_ms, {
+            "C1": op_bytes["rmsnorm_fwd"] + op_bytes["rmsnorm_bwd"],
+            "C2": op_bytes["rope_fwd"] + op_bytes["rope_bwd"], "C3": bytes_c3,
+            "C4": sum(c4b.values()) + sum(c4r.values())})
     print(json.dumps(out), flush=True)
 
 

@@ -492,6 +492,19 @@ ts_status ts_scale_inplace(void* x, int64_t n, ts_dtype dtype, const float* scal
 ts_status ts_rescale_inplace(void* x, int64_t n, ts_dtype dtype, const float* now,
                              const float* used, float* hint_out, ts_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Measurement                                                               */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * dst[0 .. bytes) = src[0 .. bytes) with the flat streaming copy kernel (one
+ * 16-byte vector per thread, 256-thread workgroups, non-temporal accesses);
+ * bytes a multiple of 16, both buffers 16-byte aligned and not overlapping.
+ * No counterpart in the reference: the copy against which the benchmark sets
+ * each memory-bound kernel, for the same number of bytes moved.
+ */
+ts_status ts_stream_copy(void* dst, const void* src, int64_t bytes, ts_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -529,3 +529,53 @@ def test_swiglu_invariants():
     out = oracle.swiglu_fwd(g, u)
     assert out[0].item() == 0.0 and out[3].item() == 0.0   # silu(0) = 0; up = 0
     assert out[1].item() == 40.0 and abs(out[2].item()) < 1e-15  # saturation
+
+
+# ---------------------------------------------------------------------------
+# The reference's eager sequences (oracle/eager.py, the CPU baseline) compute
+# the same functions as the pinned oracle.
+# ---------------------------------------------------------------------------
+def test_eager_sequences_agree_with_oracle():
+    from oracle import eager as E
+    torch.manual_seed(12)
+    x = torch.randn(16, 256).to(BF)
+    w = (1 + 0.02 * torch.randn(256)).to(BF)
+    dy = torch.randn(16, 256).to(BF)
+    y, dx, dw = E.rmsnorm(x, w, dy)
+    y_ref, rstd = oracle.rms_norm_fwd(x, w)
+    dx_ref, dw_ref = oracle.rms_norm_bwd(dy, x, w, rstd)
+    assert max_ulp(y, y_ref) <= 1
+    # the eager backward rounds dy * w to bf16 before the products (the kernels do not)
+    torch.testing.assert_close(dx.float(), dx_ref.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(dw.float(), dw_ref.float(), rtol=2e-2, atol=2e-2)
+    q = torch.randn(2, 9, 4, 32).to(BF)
+    k = torch.randn(2, 9, 2, 32).to(BF)
+    cos, sin = oracle.rope_tables(32, 9, 10000.0)
+    # fp32 tables: the products promote to fp32 (as the reference's fallback does with
+    # precompute_freqs_cis's fp32 tables), rounded once here
+    qo, ko, dqo, _ = (t.to(BF) for t in E.rope(q, k, q, k, cos, sin))
+    pos = oracle.rope_positions(2, 9)
+    assert max_ulp(qo, oracle.rope_apply(q, cos, sin, pos)) <= 1
+    assert max_ulp(ko, oracle.rope_apply(k, cos, sin, pos)) <= 1
+    assert max_ulp(dqo, oracle.rope_apply(q, cos, sin, pos, backward=True)) <= 1
+    pid = torch.tensor([[0, 1, 2, 0, 1, 2, 3, 0, 1]] * 2)
+    qp = E.rope(q, k, q, k, cos, sin, position_ids=pid)[0].to(BF)
+    assert max_ulp(qp, oracle.rope_apply(q, cos, sin, pid)) <= 1
+    logits = (2 * torch.randn(8, 300)).to(BF)
+    labels = torch.randint(0, 300, (8,))
+    labels[2] = -100
+    rows, _ = oracle.ce_fwd(logits, labels)
+    n_valid = 7
+    for fn in (E.ce_chunked, E.ce_float):
+        loss, g = fn(logits, labels) if fn is E.ce_float else fn(logits, labels, chunk_size=128)
+        assert abs(float(loss) - float(rows.sum()) / n_valid) <= 1e-5
+        ref_g = oracle.ce_bwd(logits, labels, torch.tensor(1.0 / n_valid))
+        torch.testing.assert_close(g.float(), ref_g.float(), rtol=1e-2, atol=1e-4)
+    h = torch.randn(6, 32).to(BF)
+    wt = (0.1 * torch.randn(40, 32)).to(BF)
+    lab = torch.randint(0, 40, (6,))
+    loss, gh, gw = E.linear_ce(h, wt, lab)
+    ref_loss, ref_gh, ref_gw = oracle.linear_ce(h, wt, lab, bf16_logits=True)
+    assert abs(float(loss) - float(ref_loss)) <= 1e-4 * abs(float(ref_loss))
+    torch.testing.assert_close(gh.float(), ref_gh.float(), rtol=2e-2, atol=2e-3)
+    torch.testing.assert_close(gw.float(), ref_gw.float(), rtol=2e-2, atol=2e-3)

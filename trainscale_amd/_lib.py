@@ -95,6 +95,7 @@ SIGNATURES = {
     "ts_swiglu_fwd": ([P, P, P, I64, I32, P], I32),
     "ts_swiglu_bwd": ([P, P, P, P, P, I64, I32, P], I32),
     "ts_rescale_inplace": ([P, I64, I32, P, P, P, P], I32),
+    "ts_stream_copy": ([P, P, I64, P], I32),
 }
 
 _lock = threading.Lock()

@@ -57,19 +57,20 @@ class Workload:
 
 
 def rmsnorm_workload(device, scale: float = 1.0, dtype=torch.bfloat16, H: Optional[int] = None,
-                     cfg=C1) -> Workload:
+                     cfg=C1, seed_offset: int = 0) -> Workload:
     B, S = cfg["B"], max(1, int(cfg["S"] * scale))
     H = H or cfg["H"]
-    g = _gen(device, cfg["seed"])
+    g = _gen(device, cfg["seed"] + seed_offset)
     x = _randn((B, S, H), g, device, dtype)
     w = _randn((H,), g, device, dtype, std=0.02, mean=1.0)
     dy = _randn((B, S, H), g, device, dtype)
     return Workload(cfg["name"], dict(x=x, w=w, dy=dy), dict(eps=cfg["eps"]), tokens=B * S)
 
 
-def rope_workload(device, scale: float = 1.0, dtype=torch.bfloat16, cfg=C2) -> Workload:
+def rope_workload(device, scale: float = 1.0, dtype=torch.bfloat16, cfg=C2,
+                  seed_offset: int = 0) -> Workload:
     B, S = cfg["B"], max(1, int(cfg["S"] * scale))
-    g = _gen(device, cfg["seed"])
+    g = _gen(device, cfg["seed"] + seed_offset)
     q = _randn((B, S, cfg["Hq"], cfg["D"]), g, device, dtype)
     k = _randn((B, S, cfg["Hk"], cfg["D"]), g, device, dtype)
     dq = _randn((B, S, cfg["Hq"], cfg["D"]), g, device, dtype)
@@ -79,10 +80,10 @@ def rope_workload(device, scale: float = 1.0, dtype=torch.bfloat16, cfg=C2) -> W
 
 
 def ce_workload(device, scale: float = 1.0, dtype=torch.bfloat16, V: Optional[int] = None,
-                cfg=C3) -> Workload:
+                cfg=C3, seed_offset: int = 0) -> Workload:
     N = max(1, int(cfg["N"] * scale))
     V = V or cfg["V"]
-    g = _gen(device, cfg["seed"])
+    g = _gen(device, cfg["seed"] + seed_offset)
     logits = _randn((N, V), g, device, dtype, std=2.0)
     labels = _labels(N, V, cfg["ignore_frac"], g, device)
     return Workload(cfg["name"], dict(logits=logits, labels=labels), dict(V=V), tokens=N)
