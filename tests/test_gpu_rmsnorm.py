@@ -244,3 +244,29 @@ def test_add_c1_full(gpu):
     y_ref, h_ref, _ = oracle.add_rms_norm_fwd(x2[sample], r2[sample], w, 1e-6)
     assert_ulp(y.reshape(-1, y.shape[-1])[sample], y_ref, 1, what="y")
     assert torch.equal(h.reshape(-1, h.shape[-1])[sample].cpu(), h_ref)
+
+
+def test_c4_full_rmsnorm(gpu):
+    """C4 at its full 32768 tokens x 8192 through the ops the benchmark times: y, rstd and
+    dx against the oracle in row chunks on the CPU; dW against the float64 sum over all
+    rows (bf16 result: within 1 ulp, or 2e-2)."""
+    wl = workloads.packed_workload(gpu)
+    x, w, dy = wl.tensors["x"], wl.tensors["w"], wl.tensors["dy"]
+    x2d, ldx = ops.as_rows(x)
+    dy2d, lddy = ops.as_rows(dy)
+    y, rstd = ops.rmsnorm_forward(x2d, ldx, w, 1e-6)
+    dx, dw = ops.rmsnorm_backward(dy2d, lddy, x2d, ldx, w, rstd, need_dw=True)
+    wc = w.cpu()
+    dw64 = torch.zeros(x.shape[1], dtype=torch.float64)
+    for s in range(0, x.shape[0], 4096):
+        xs, dys = x2d[s:s + 4096].cpu(), dy2d[s:s + 4096].cpu()
+        y_ref, rstd_ref = oracle.rms_norm_fwd(xs, wc, 1e-6)
+        assert_ulp(y[s:s + 4096], y_ref, 1, what=f"y rows {s}")
+        torch.testing.assert_close(rstd[s:s + 4096].cpu(), rstd_ref, rtol=1e-6, atol=0)
+        dx_ref, _ = oracle.rms_norm_bwd(dys, xs, wc, rstd_ref)
+        assert_ulp(dx[s:s + 4096], dx_ref, 1, tiny=1e-4, what=f"dx rows {s}")
+        dw64 += (dys.double() * (xs.double() * rstd_ref.double()[:, None])).sum(0)
+    ref = dw64.float()
+    ulp = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp(min=1e-30))) - 7)
+    assert bool(((dw.float().cpu() - ref).abs() <= torch.clamp(ulp, min=2e-2)).all())
+    assert_ulp(dw, ref.to(BF), 1, tiny=1e-4, what="dw")

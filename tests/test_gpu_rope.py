@@ -340,3 +340,76 @@ def test_packed_rows_from_cu_seqlens(gpu):
             assert torch.equal(yt[r:r + 1, start:start + n],
                                apply_rope_theta(doc, theta, inplace=False))
             start += n
+
+
+def assert_rope_rows(outs, x, cos, sin, pos, backward=False, chunk=4096, what=""):
+    """assert_rope for large [1, T, H, D] tensors, token chunk by token chunk: the oracle
+    (and the products' size) is computed once per chunk and every output in `outs`
+    (e.g. table mode and in-register mode) is held to it."""
+    T = x.shape[1]
+    for s in range(0, T, chunk):
+        xs = x[:, s:s + chunk].cpu()
+        ps = pos[:, s:s + chunk]
+        ref = oracle_pair(xs, cos, sin, ps, False, backward)
+        mag = term_mag(xs, cos, sin, ps, False)
+        for name, out in outs.items():
+            a = out[:, s:s + chunk].detach().cpu()
+            from helpers import ulp_diff
+            ok = (ulp_diff(a, ref) <= 1) | ((a.float() - ref.float()).abs() <=
+                                             4 * 2.0 ** -24 * mag)
+            if not bool(ok.all()):
+                idx = (~ok).nonzero()[0].tolist()
+                raise AssertionError(f"{what} {name}: tokens {s}..: {int((~ok).sum())} "
+                                     f"elements off; first at {idx}")
+
+
+def test_c4_full_position_ids_fwd_bwd(gpu):
+    """C4 at its full 32768 tokens: Q (64 heads) and K (8 heads) forward and backward
+    with the packed position_ids, in table mode and in-register mode, through the op
+    the benchmark times (ops.rope_apply), against the oracle in token chunks."""
+    from trainscale_amd import ops
+    from trainscale_amd.kernels.rope_kernels import _base_inv_freq
+    wl = workloads.packed_workload(gpu)
+    q, k, dq, dk, pos = (wl.tensors[n] for n in ("q", "k", "dq", "dk", "position_ids"))
+    theta = wl.params["theta"]
+    cos, sin = oracle.rope_tables(128, 4096, theta)
+    cg, sg = cos.to(gpu), sin.to(gpu)
+    inv = _base_inv_freq(theta, 128, "cpu")
+    pos_cpu = oracle.rope_positions(1, q.shape[1], pos)
+    for backward, (xq, xk) in ((False, (q, k)), (True, (dq, dk))):
+        outs_q, outs_k = {}, {}
+        for mode in ("table", "register"):
+            qo, ko = torch.empty_like(xq), torch.empty_like(xk)
+            if mode == "table":
+                ops.rope_apply(xq, qo, xk, ko, cos=cg, sin=sg, position_ids=pos,
+                               backward=backward)
+            else:
+                ops.rope_apply(xq, qo, xk, ko, inv_freq=inv, position_ids=pos,
+                               backward=backward)
+            outs_q[mode], outs_k[mode] = qo, ko
+        d = "bwd" if backward else "fwd"
+        assert_rope_rows(outs_q, xq, cos, sin, pos_cpu, backward, what=f"C4 q {d}")
+        assert_rope_rows(outs_k, xk, cos, sin, pos_cpu, backward, what=f"C4 k {d}")
+        del outs_q, outs_k
+
+
+def test_c2_full_in_register_as_benched(gpu):
+    """C2 at full size through the exact calls the benchmark times: Q and K together,
+    in-register sin/cos, forward and backward (ops.rope_apply with inv_freq)."""
+    from trainscale_amd import ops
+    from trainscale_amd.kernels.rope_kernels import _base_inv_freq
+    wl = workloads.rope_workload(gpu)
+    q, k, dq, dk = (wl.tensors[n] for n in ("q", "k", "dq", "dk"))
+    B, S, _, D = q.shape
+    inv = _base_inv_freq(wl.params["theta"], D, "cpu")
+    cos, sin = oracle.rope_tables(D, S, wl.params["theta"])
+    pos = oracle.rope_positions(B, S)
+    for backward, (xq, xk) in ((False, (q, k)), (True, (dq, dk))):
+        qo, ko = torch.empty_like(xq), torch.empty_like(xk)
+        ops.rope_apply(xq, qo, xk, ko, inv_freq=inv, backward=backward)
+        for b in range(B):
+            sl = slice(b, b + 1)
+            assert_rope_rows({"q": qo[sl]}, xq[sl], cos, sin, pos[sl], backward,
+                             what=f"C2 batch {b}")
+            assert_rope_rows({"k": ko[sl]}, xk[sl], cos, sin, pos[sl], backward,
+                             what=f"C2 batch {b}")
