@@ -20,9 +20,10 @@ streaming copy of the same bytes (ts_stream_copy).
 
 Also reported, outside the timed step: C4 (packed varlen RMSNorm + RoPE with
 position_ids at 70B shapes, GB/s) and C5 (fused linear cross-entropy, TFLOP/s
-against the bf16 MFMA peak; the default two-pass schedule, plus the one-call
-schedule with all logits in one chunk and the RL form as separate lines), each
-with its own timing, and the reference's eager CPU path per config.
+against the bf16 MFMA peak: the default schedule for the call, token chunks of a
+quarter of the tokens; the two-pass schedule, the RL form and the one-call
+schedule with all logits in one chunk as separate lines), each with its own
+timing, and the reference's eager CPU path per config.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--no-extra] [--copy-probe]
@@ -412,16 +413,18 @@ def bench_next_rows(dev, steps: int, warmup: int):
 
 
 def bench_linear_ce(dev, steps: int, warmup: int):
-    """C5: fused linear CE fwd+bwd (loss, grad_hidden, grad_weight). The default is the
-    two-pass schedule (ts_flce_forward then ts_flce_backward: no [N, V] logits stored,
-    four GEMMs executed); also timed: the one-call schedule with all logits in one
-    chunk (opt-in, three GEMMs) and the RL form (per-token losses, temperature, per-row
-    upstream gradients) through the two-pass schedule."""
+    """C5: fused linear CE fwd+bwd (loss, grad_hidden, grad_weight). The default schedule
+    for this call (mean, gradients needed) is the one-call schedule in token chunks of a
+    quarter of the tokens, grad_weight summed in its bf16 output: no more than a quarter
+    of the [N, V] logits exists at a time, three GEMMs. Also timed: the two-pass schedule
+    (no logits stored, four GEMMs), the RL form through it (per-token losses,
+    temperature, per-row upstream gradients), and the one-call schedule with all logits
+    in one chunk (opt-in, not the C5 configuration)."""
     import torch
 
     from trainscale_amd import _lib
     from trainscale_amd import workloads as W
-    from trainscale_amd.loss.linear_ce import _chunk_rows
+    from trainscale_amd.loss.linear_ce import TS_FLCE_ACCUM_BF16, TS_FLCE_GRADS, _chunk_rows
 
     c5 = W.linear_ce_workload(dev)
     h, w, labels = c5.tensors["hidden"], c5.tensors["weight"], c5.tensors["labels"]
@@ -436,11 +439,55 @@ def bench_linear_ce(dev, steps: int, warmup: int):
     gh = torch.empty_like(h)
     gw = torch.empty_like(w)
     one = torch.ones((1,), dtype=torch.float32, device=dev)
+    flops = W.linear_ce_flops(N, H, V)
+    reps, warm = max(3, steps // 2), max(1, warmup // 2)
+
+    def line(ms, **kw):
+        tf = flops / (ms * 1e-3) / 1e12
+        return dict(ms=round(ms, 4), TFLOP_s=round(tf, 1),
+                    frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4), **kw)
+
+    def one_call_timer(chunk, flags):
+        ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk, TS_FLCE_GRADS | flags))
+        ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+
+        def one_call():
+            _lib.check(lib.ts_flce_fwd_bwd(
+                P(h), H, P(w), H, P(labels), N, H, V, -100, 0, P(loss), P(rows), P(lse), P(gh),
+                P(gw), chunk, flags, P(ws), ws_bytes, stream), "ts_flce_fwd_bwd")
+
+        ms = time_ms(one_call, reps, warm)
+        del ws
+        torch.cuda.empty_cache()
+        return ms, ws_bytes
+
+    # the default: token chunks of a quarter of the tokens, grad_weight summed in bf16
+    chunk = _chunk_rows(N, V, None)
+    ms, ws_bytes = one_call_timer(chunk, TS_FLCE_ACCUM_BF16)
+    tf = flops / (ms * 1e-3) / 1e12
+    out = {"workload": (f"C5 fused linear CE: hidden [{N},{H}] bf16, lm_head [{V},{H}] bf16, "
+                        f"5% ignored, mean; loss + grad_hidden + grad_weight; default schedule: "
+                        f"one call in token chunks of {chunk} rows (at most {chunk}x{V} bf16 "
+                        f"logits at a time, a quarter of the full logits), grad_weight summed "
+                        f"over the chunks in its bf16 output"),
+           "schedule": "fused, token chunk N/4, bf16 grad_weight sum",
+           "ms": round(ms, 4), "algorithmic_flop": flops, "executed_flop": flops,
+           "TFLOP_s": round(tf, 1), "workspace_bytes": ws_bytes,
+           "full_logits_bytes": N * V * 2,
+           "roofline": {"bound": "mfma", "achieved": round(tf, 1),
+                        "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)},
+           "tokens_per_s": round(N / (ms * 1e-3), 1)}
+    ms32, ws32 = one_call_timer(chunk, 0)
+    out["fp32_grad_weight_sum"] = line(ms32, workspace_bytes=ws32,
+                                       what="the same chunks, grad_weight summed in an fp32 "
+                                            "V x H workspace and rounded once")
+
+    # two-pass: forward keeps row statistics only, backward recomputes by vocabulary chunk
     ws_f = int(lib.ts_flce_forward_workspace_size(N, V))
     ws_b = int(lib.ts_flce_backward_workspace_size(N, H, V, 0))
     wsf = torch.empty((ws_f,), dtype=torch.uint8, device=dev)
     wsb = torch.empty((ws_b,), dtype=torch.uint8, device=dev)
-    flops = W.linear_ce_flops(N, H, V)
 
     def fwd(red=0, temp=1.0):
         _lib.check(lib.ts_flce_forward(
@@ -456,65 +503,33 @@ def bench_linear_ce(dev, steps: int, warmup: int):
         fwd()
         bwd()
 
-    reps, warm = max(3, steps // 2), max(1, warmup // 2)
-    ms = time_ms(two_pass, reps, warm)
+    ms2 = time_ms(two_pass, reps, warm)
     ms_f = time_ms(fwd, reps, warm)
-    tf = flops / (ms * 1e-3) / 1e12
-    out = {"workload": (f"C5 fused linear CE: hidden [{N},{H}] bf16, lm_head [{V},{H}] bf16, "
-                        f"5% ignored, mean; loss + grad_hidden + grad_weight; two-pass schedule "
-                        f"(forward keeps row statistics only; backward recomputes the logits in "
-                        f"vocabulary chunks of {N}x{-(-((V + 7) // 8) // 256) * 256} bf16)"),
-           "schedule": "two_pass",
-           "ms": round(ms, 4), "forward_ms": round(ms_f, 4), "backward_ms": round(ms - ms_f, 4),
-           "algorithmic_flop": flops, "executed_flop": flops // 3 * 4,
-           "TFLOP_s": round(tf, 1),
-           "executed_TFLOP_s": round(flops // 3 * 4 / (ms * 1e-3) / 1e12, 1),
-           "workspace_bytes": ws_f + ws_b,
-           "full_logits_bytes": N * V * 2,
-           "roofline": {"bound": "mfma", "achieved": round(tf, 1),
-                        "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)},
-           "tokens_per_s": round(N / (ms * 1e-3), 1)}
-    del wsf, wsb
-    torch.cuda.empty_cache()
-
-    # RL form: per-token losses at temperature 0.9, per-row upstream gradients
+    vc = -(-((V + 7) // 8) // 256) * 256
+    out["two_pass"] = line(ms2, forward_ms=round(ms_f, 4), backward_ms=round(ms2 - ms_f, 4),
+                           executed_flop=flops // 3 * 4,
+                           executed_TFLOP_s=round(flops // 3 * 4 / (ms2 * 1e-3) / 1e12, 1),
+                           workspace_bytes=ws_f + ws_b,
+                           what=(f"forward keeps row statistics only (no logits stored); "
+                                 f"backward recomputes the logits in vocabulary chunks of "
+                                 f"{vc} columns, dlogits formed in the GEMM epilogue"))
     up_rows = torch.randn((N,), device=dev, generator=torch.Generator(device=dev).manual_seed(6))
-    ws_f = int(lib.ts_flce_forward_workspace_size(N, V))
-    wsf = torch.empty((ws_f,), dtype=torch.uint8, device=dev)
-    wsb = torch.empty((ws_b,), dtype=torch.uint8, device=dev)
 
     def rl():
         fwd(red=2, temp=0.9)
         bwd(red=2, temp=0.9, up=up_rows, stride=1)
 
-    ms_rl = time_ms(rl, reps, warm)
-    tf_rl = flops / (ms_rl * 1e-3) / 1e12
-    out["rl_form"] = {"what": "reduction none, temperature 0.9, per-row upstream gradients "
-                              "(chunked_log_softmax's use by GRPOCompute)",
-                      "ms": round(ms_rl, 4), "TFLOP_s": round(tf_rl, 1),
-                      "frac": round(tf_rl / MFMA_BF16_PEAK_TFLOPS, 4)}
+    out["rl_form"] = line(time_ms(rl, reps, warm),
+                          what="two-pass, reduction none, temperature 0.9, per-row upstream "
+                               "gradients (chunked_log_softmax's use by GRPOCompute)")
     del wsf, wsb
     torch.cuda.empty_cache()
-
-    # one-call schedule, one token chunk: the full [N, V] logits in the workspace (opt-in)
-    chunk = _chunk_rows(N, V, None)
-    ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk, 1))
-    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
-
-    def one_call():
-        _lib.check(lib.ts_flce_fwd_bwd(
-            P(h), H, P(w), H, P(labels), N, H, V, -100, 0, P(loss), P(rows), P(lse), P(gh),
-            P(gw), chunk, P(ws), ws_bytes, stream), "ts_flce_fwd_bwd")
-
-    ms1 = time_ms(one_call, reps, warm)
-    tf1 = flops / (ms1 * 1e-3) / 1e12
-    out["one_chunk_schedule"] = {
-        "what": "one call, gradients formed in the forward, all [N, V] bf16 logits in one "
-                "chunk (materialised: not the C5 configuration; reported apart)",
-        "ms": round(ms1, 4), "TFLOP_s": round(tf1, 1),
-        "frac": round(tf1 / MFMA_BF16_PEAK_TFLOPS, 4), "workspace_bytes": ws_bytes}
-    del ws, c5, h, w, labels, gh, gw
+    ms1, ws1 = one_call_timer(0, 0)
+    out["one_chunk_schedule"] = line(
+        ms1, workspace_bytes=ws1,
+        what="one call, all [N, V] bf16 logits in one chunk (materialised: not the C5 "
+             "configuration; opt-in, reported apart)")
+    del c5, h, w, labels, gh, gw
     torch.cuda.empty_cache()
     return out
 

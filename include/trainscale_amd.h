@@ -370,13 +370,23 @@ ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const void* weight,
 /* Fused linear cross-entropy                                                */
 /* ------------------------------------------------------------------------ */
 
+/* flags of ts_flce_workspace_size / ts_flce_fwd_bwd */
+enum {
+  TS_FLCE_GRADS = 1,       /* workspace size: with the gradients' scratch */
+  TS_FLCE_ACCUM_BF16 = 2   /* sum grad_weight over token chunks in the bf16 output (rounded
+                              after each chunk, as autograd sums the per-chunk bf16 gradients
+                              of the reference's chunked_log_softmax, rl_training.py:167-191)
+                              instead of an fp32 V x H workspace rounded once */
+};
+
 /*
  * Bytes of workspace ts_flce_fwd_bwd needs for hidden [N, H], weight [V, H]
  * and a token chunk of `chunk` rows (chunk <= 0 or >= N: one chunk), with
- * (with_grads != 0) or without the backward scratch.
+ * (flags & TS_FLCE_GRADS) or without the backward scratch, and with
+ * (TS_FLCE_ACCUM_BF16) or without the fp32 grad_weight sum.
  */
 size_t ts_flce_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk,
-                              int32_t with_grads);
+                              int32_t flags);
 
 /*
  * Loss and gradients of logits = hidden @ weight^T without a library GEMM:
@@ -394,6 +404,11 @@ size_t ts_flce_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk,
  * are fp32. loss_rows, lse ([N] fp32) may be NULL. grad_hidden and
  * grad_weight may be NULL (then their GEMM is skipped; both NULL: forward
  * only). Deterministic: every reduction has a fixed order.
+ * The rows are processed in token chunks of `chunk` rows (0: one chunk); a
+ * chunk's bf16 logits are the only [rows, V] scratch. Per chunk the two
+ * gradient GEMMs run as one grid. grad_weight sums over the chunks in fp32 in
+ * the workspace (rounded once), or with flags & TS_FLCE_ACCUM_BF16 in the
+ * bf16 output (no V x H workspace). flags: 0 or TS_FLCE_ACCUM_BF16.
  * Has no counterpart in the reference, which has no fused linear-CE; it
  * replaces the composition logits = hidden @ lm_head.t() (rl_training.py:177,
  * chunked_log_softmax :138-191) followed by cross-entropy
@@ -404,7 +419,8 @@ ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight, i
                           int64_t ignore_index, int32_t reduction,
                           float* loss, float* loss_rows, float* lse,
                           void* grad_hidden, void* grad_weight, int64_t chunk,
-                          void* workspace, size_t workspace_bytes, ts_stream_t stream);
+                          int32_t flags, void* workspace, size_t workspace_bytes,
+                          ts_stream_t stream);
 
 /*
  * Two-pass fused linear cross-entropy (the schedule for any reduction and any

@@ -224,9 +224,9 @@ def test_flce_validation(lib):
     ws = lib.ts_flce_workspace_size(N, H, V, 0, 1)
     assert ws > 0 and lib.ts_flce_workspace_size(0, H, V, 0, 1) == 0
 
-    def call(ldh=H, ldw=H, n=N, h=H, v=V, reduction=0, loss=FAKE, wsb=ws, hidden=FAKE):
+    def call(ldh=H, ldw=H, n=N, h=H, v=V, reduction=0, loss=FAKE, wsb=ws, hidden=FAKE, flags=0):
         return lib.ts_flce_fwd_bwd(hidden, ldh, FAKE, ldw, FAKE, n, h, v, -100, reduction, loss,
-                                   NULL, NULL, FAKE, FAKE, 0, FAKE, wsb, st)
+                                   NULL, NULL, FAKE, FAKE, 0, flags, FAKE, wsb, st)
 
     assert call(h=60, ldh=64, ldw=64) == SHAPE          # H not a multiple of 8
     assert call(ldh=32) == SHAPE                        # row stride below H
@@ -239,6 +239,10 @@ def test_flce_validation(lib):
     assert call(loss=NULL) == INVALID
     assert call(hidden=NULL) == INVALID
     assert call(wsb=ws - 256) == WORKSPACE
+    assert call(flags=4) == INVALID
+    # bf16 accumulation needs no V x H fp32 sum: smaller than fp32 accumulation over chunks
+    assert lib.ts_flce_workspace_size(1024, 256, 4096, 256, 3) + 4096 * 256 * 4 == \
+        lib.ts_flce_workspace_size(1024, 256, 4096, 256, 1)
 
 
 def test_flce_two_pass_validation(lib):

@@ -72,16 +72,21 @@ def test_add_rmsnorm_empty(gpu):
     assert y.shape == (0, 4096) and h.shape == (0, 4096)
 
 
-def test_linear_ce_empty(gpu):
+@pytest.mark.parametrize("schedule", ["auto", "fused", "two_pass"])
+def test_linear_ce_empty(gpu, schedule):
     H, V = 128, 1000
     hidden = torch.randn(0, H, device=gpu).to(BF).requires_grad_()
-    weight = (0.02 * torch.randn(V, H, device=gpu)).to(BF).requires_grad_()
+    weight = (0.02 * torch.randn(V, H, device=gpu)).to(BF)
+    weight.fill_(1.0)  # grad_weight must come back zero, not a leftover
+    weight.requires_grad_()
     labels = torch.zeros(0, dtype=torch.int64, device=gpu)
-    loss = fused_linear_cross_entropy(hidden, weight, labels)
+    loss = fused_linear_cross_entropy(hidden, weight, labels, schedule=schedule)
     assert loss.item() == 0.0
     loss.backward()
     assert hidden.grad.shape == (0, H)
     assert torch.count_nonzero(weight.grad) == 0
+    rows = fused_linear_cross_entropy(hidden, weight, labels, reduction="none")
+    assert rows.shape == (0,)
 
 
 def test_vocab_parallel_empty(gpu):

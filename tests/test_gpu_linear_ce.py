@@ -65,9 +65,10 @@ def assert_rows_close(got, ref, bound, what):
     assert bool((d <= 1e-5 + 1e-5 * ref.abs() + bound).all()), (what, float(d.max()))
 
 
-def check_against_oracle(h, w, labels, reduction="mean", chunk=None):
+def check_against_oracle(h, w, labels, reduction="mean", chunk=None, accum="fp32"):
     loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels, reduction=reduction,
-                                                         chunk_tokens=chunk)
+                                                         chunk_tokens=chunk,
+                                                         grad_weight_accum=accum)
     ref_loss, ref_gh, ref_gw, ref_rows, ref_lse = oracle.linear_ce(
         h, w, labels, reduction=reduction, bf16_logits=True, return_rows=True)
     assert abs(loss.item() - float(ref_loss)) <= 1e-5 * abs(float(ref_loss)), (loss.item(),
@@ -94,18 +95,28 @@ def test_small_shapes(gpu, N, H, V):
 
 
 @pytest.mark.parametrize("chunk", [256, 512])
-def test_token_chunks_accumulate_grad_weight(gpu, chunk):
+@pytest.mark.parametrize("accum", ["fp32", "bf16"])
+def test_token_chunks_accumulate_grad_weight(gpu, chunk, accum):
     torch.manual_seed(5)
     N, H, V = 1040, 128, 768
     h = torch.randn(N, H, device=gpu).to(BF)
     w = (0.05 * torch.randn(V, H, device=gpu)).to(BF)
     labels = torch.randint(0, V, (N,), device=gpu)
     labels[::7] = -100
-    _, gh1, gw1 = check_against_oracle(h, w, labels, chunk=chunk)
-    # chunking changes only where the fp32 sum of grad_weight is rounded
+    _, gh1, gw1 = check_against_oracle(h, w, labels, chunk=chunk, accum=accum)
+    # chunking changes only where (fp32) or how often (bf16) the sum of grad_weight is
+    # rounded
     _, _, _, gh0, gw0 = linear_ce_forward_backward(h, w, labels, chunk_tokens=0)
     assert torch.equal(gh0, gh1)
-    assert rel_fro(gw1, gw0) <= 4e-3
+    assert rel_fro(gw1, gw0) <= (4e-3 if accum == "fp32" else 8e-3)
+    if accum == "bf16":
+        # the first chunk's partial sum, then one bf16 rounding per further chunk: the
+        # same as summing the per-chunk bf16 results the way autograd does
+        parts = [linear_ce_forward_backward(h[s:s + chunk], w, labels[s:s + chunk],
+                                            reduction="sum", chunk_tokens=0)[4]
+                 for s in range(0, N, chunk)]
+        n_valid = int((labels != -100).sum())
+        assert rel_fro(gw1.float() * n_valid, sum(p.float() for p in parts)) <= 8e-3
 
 
 def test_exact_logits_pin_the_gemms(gpu):
@@ -235,11 +246,13 @@ def test_c5_full(gpu):
     _check_c5(h, w, labels, loss, rows, gh, gw)
 
 
-def test_c5_full_fused_schedule(gpu):
-    """C5 through the one-call schedule with the full logits in one chunk (opt-in)."""
+@pytest.mark.parametrize("chunk", [None, 0])
+def test_c5_full_fused_schedule(gpu, chunk):
+    """C5 through the one-call schedule: its default token chunk (a quarter of the
+    tokens, grad_weight summed in fp32 over the chunks) and one chunk (opt-in)."""
     wl = workloads.linear_ce_workload(gpu)
     h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
-    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels)
+    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels, chunk_tokens=chunk)
     _check_c5(h, w, labels, loss, rows, gh, gw)
 
 
@@ -333,7 +346,7 @@ def test_two_pass_equals_one_call_schedule(gpu):
     w = (0.05 * torch.randn(V, H, device=gpu)).to(BF)
     labels = torch.randint(0, V, (N,), device=gpu)
     labels[::13] = -100
-    loss1, rows1, lse1, gh1, gw1 = linear_ce_forward_backward(h, w, labels)
+    loss1, rows1, lse1, gh1, gw1 = linear_ce_forward_backward(h, w, labels, chunk_tokens=0)
     loss2, rows2, lse2 = linear_ce_forward(h, w, labels)
     # the same GEMM and epilogue arithmetic: statistics and losses bit-identical
     assert torch.equal(rows1, rows2) and torch.equal(lse1, lse2) and torch.equal(loss1, loss2)
@@ -345,15 +358,23 @@ def test_two_pass_equals_one_call_schedule(gpu):
     assert rel_fro(gh3, gh1) <= 4e-3  # grad_hidden: fp32 sums over chunks, rounded once
 
 
-def test_module_api_two_pass_default(gpu):
+def test_module_api_schedules(gpu):
     torch.manual_seed(22)
     B, L, H, V = 2, 67, 128, 1024
     h = torch.randn(B, L, H, device=gpu).to(BF).requires_grad_()
     w = (0.05 * torch.randn(V, H, device=gpu)).to(BF).requires_grad_()
     labels = torch.randint(0, V, (B, L), device=gpu)
     labels[0, :5] = -100
-    loss = fused_linear_cross_entropy(h, w, labels)
+    # the default (auto: the one-call schedule here) against the two-pass schedule
+    loss0 = fused_linear_cross_entropy(h, w, labels)
+    (3.0 * loss0).backward()
+    gh0, gw0 = h.grad.clone(), w.grad.clone()
+    h.grad = None
+    w.grad = None
+    loss = fused_linear_cross_entropy(h, w, labels, schedule="two_pass")
+    assert torch.equal(loss, loss0)
     (3.0 * loss).backward(retain_graph=True)
+    assert rel_fro(h.grad, gh0) <= 4e-3 and rel_fro(w.grad, gw0) <= 8e-3
     ref_loss, ref_gh, ref_gw = oracle.linear_ce(h.detach().reshape(-1, H), w.detach(),
                                                 labels.reshape(-1), bf16_logits=True)
     assert abs(loss.item() - float(ref_loss)) <= 1e-5 * abs(float(ref_loss))
@@ -368,6 +389,8 @@ def test_module_api_two_pass_default(gpu):
     w.grad = None
     rows = fused_linear_cross_entropy(h, w, labels, reduction="none", logit_softcapping=20.0)
     assert rows.shape == labels.shape
+    node = rows.grad_fn.next_functions[0][0]  # behind the view to labels' shape
+    assert type(node).__name__ == "LinearCrossEntropyFunctionBackward"
     up = torch.randn(B, L, device=gpu)
     (rows * up).sum().backward()
     _, ref_gh2, ref_gw2 = oracle.linear_ce(h.detach().reshape(-1, H), w.detach(),

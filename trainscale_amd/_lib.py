@@ -83,8 +83,8 @@ SIGNATURES = {
     "ts_flce_vocab_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, P, I64, I64, I32, P, P, P, P,
                            P, P, SZ, P], I32),
     "ts_flce_workspace_size": ([I64, I64, I64, I64, I32], SZ),
-    "ts_flce_fwd_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, P, P, P, P, P, I64, P, SZ, P],
-                        I32),
+    "ts_flce_fwd_bwd": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, P, P, P, P, P, I64, I32, P,
+                         SZ, P], I32),
     "ts_flce_forward_workspace_size": ([I64, I64], SZ),
     "ts_flce_forward": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, F32, F32, F32, P, P, P, P,
                          SZ, P], I32),

@@ -45,7 +45,8 @@ enum EpiMode : int {
   kEpiAccF32 = 3,     // fp32 C32 += acc
   kEpiAccBf16 = 4,    // bf16 C = C32 + acc
   kEpiStats = 5,      // row statistics of the transformed logits + the label's value; no C
-  kEpiDlogits = 6     // bf16 C = dlogits of the transformed logits (lse known)
+  kEpiDlogits = 6,    // bf16 C = dlogits of the transformed logits (lse known)
+  kEpiAddBf16 = 7     // bf16 C = bf16(C + acc): a running sum kept in the bf16 output
 };
 
 // Transform of the bf16-rounded logits z, in the order of selective_log_softmax
@@ -129,17 +130,16 @@ __device__ inline void stage_f32_tile(const Acc<kTI>& acc, int i, uint8_t* regio
 }
 
 // One 256 x 256 tile of C = A B^T with kW waves (ts_gemm::Cfg) and the
-// epilogue of kMode.
+// epilogue of kMode: tile number `bid` of the GEMM (ts_plan::gemm_tile_of
+// maps it to a tile), `smem` the workgroup's kLdsBytes of LDS.
 template <int kMode, int kMA, int kMB, int kW>
-__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(kW / 4, kW / 4)))
-void flce_gemm(const GemmArgs a) {
+__device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) {
   using Cw = ts_gemm::Cfg<kW>;
   constexpr int kTI = Cw::kTI;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[ts_gemm::kLdsBytes];
   const int64_t MT = (a.M + BM - 1) / BM;
   const int64_t NT = (a.N + BN - 1) / BN;
   int64_t mt, nt;
-  ts_plan::gemm_tile_of(blockIdx.x, MT, NT, mt, nt);
+  ts_plan::gemm_tile_of(bid, MT, NT, mt, nt);
   const int64_t m0 = mt * BM;
   const int64_t n0 = nt * BN;
   Acc<kTI> acc;
@@ -160,7 +160,8 @@ void flce_gemm(const GemmArgs a) {
   __syncthreads();
   uint8_t* region = smem + wid * kRegion;
 
-  if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32 || kMode == kEpiAccBf16) {
+  if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32 || kMode == kEpiAccBf16 ||
+                kMode == kEpiAddBf16) {
     // fp32 C32 rows of 128 columns = 512 B: 32 lanes x 16 B per row, 2 rows per step
     const int c4 = lane & 31;
 #pragma unroll
@@ -173,6 +174,21 @@ void flce_gemm(const GemmArgs a) {
         const int64_t gc = nb + c4 * 4;
         if (gm < a.M && gc < a.N) {  // N % 8 == 0: 4 columns are all in or all out
           float4 v = *reinterpret_cast<const float4*>(region + lrow * 512 + c4 * 16);
+          if constexpr (kMode == kEpiAddBf16) {
+            uint2* q = reinterpret_cast<uint2*>(a.C + gm * a.ldc + gc);
+            const uint2 o = *q;
+            v.x += __builtin_bit_cast(float, o.x << 16);
+            v.y += __builtin_bit_cast(float, o.x & 0xffff0000u);
+            v.z += __builtin_bit_cast(float, o.y << 16);
+            v.w += __builtin_bit_cast(float, o.y & 0xffff0000u);
+            bf16x2_t lo = {(__bf16)v.x, (__bf16)v.y};
+            bf16x2_t hi = {(__bf16)v.z, (__bf16)v.w};
+            uint2 pk;
+            pk.x = __builtin_bit_cast(uint32_t, lo);
+            pk.y = __builtin_bit_cast(uint32_t, hi);
+            *q = pk;
+            continue;
+          }
           float* p = a.C32 + gm * a.ldc32 + gc;
           if constexpr (kMode != kEpiF32) {
             const float4 o = *reinterpret_cast<const float4*>(p);
@@ -296,6 +312,28 @@ void flce_gemm(const GemmArgs a) {
       }
     }
   }
+}
+
+template <int kMode, int kMA, int kMB, int kW>
+__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(kW / 4, kW / 4)))
+void flce_gemm(const GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[ts_gemm::kLdsBytes];
+  gemm_tile<kMode, kMA, kMB, kW>(a, blockIdx.x, smem);
+}
+
+// Two independent GEMMs in one grid: workgroups [0, tiles1) compute the first,
+// the others the second. The two gradient GEMMs of a token chunk read the same
+// dlogits; with few tokens per chunk the grad_hidden GEMM has fewer (and much
+// longer) tiles than the GPU has CUs, and the grad_weight tiles, dispatched
+// after them, fill the remaining CUs. With tiles1 a multiple of 8 both GEMMs
+// keep their XCD tile grouping.
+template <int kMode1, int kMA1, int kMB1, int kMode2, int kMA2, int kMB2, int kW>
+__global__ __launch_bounds__(64 * kW) __attribute__((amdgpu_waves_per_eu(kW / 4, kW / 4)))
+void flce_gemm_pair(const GemmArgs a1, const GemmArgs a2, int64_t tiles1) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[ts_gemm::kLdsBytes];
+  const int64_t bid = blockIdx.x;
+  if (bid < tiles1) gemm_tile<kMode1, kMA1, kMB1, kW>(a1, bid, smem);
+  else gemm_tile<kMode2, kMA2, kMB2, kW>(a2, bid - tiles1, smem);
 }
 
 // n_valid = #labels != ignore_index over all N rows (one workgroup, fixed order).
@@ -593,7 +631,7 @@ struct Layout {
   size_t off_logits, off_stats, off_lse, off_rows, off_misc, off_acc, total;
 };
 
-Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
+Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads, bool acc_bf16) {
   Layout l{};
   l.chunk = chunk <= 0 || chunk >= N ? round_up(N, 8) : round_up(chunk, 256);
   if (l.chunk > round_up(N, 8)) l.chunk = round_up(N, 8);
@@ -610,7 +648,7 @@ Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads) {
   l.off_lse = take((size_t)N * 4);
   l.off_rows = take((size_t)N * 4);
   l.off_misc = take(64);
-  l.off_acc = grads && l.nchunks > 1 ? take((size_t)V * H * 4) : 0;
+  l.off_acc = grads && !acc_bf16 && l.nchunks > 1 ? take((size_t)V * H * 4) : 0;
   l.total = off;
   return l;
 }
@@ -631,6 +669,20 @@ ts_status launch_gemm(const GemmArgs& a, hipStream_t st, const char* name) {
   return ts_host::check_launch(name);
 }
 
+template <int kMode1, int kMA1, int kMB1, int kMode2, int kMA2, int kMB2>
+ts_status launch_gemm_pair(const GemmArgs& a1, const GemmArgs& a2, hipStream_t st,
+                           const char* name) {
+  constexpr int kW = 8;
+  const int64_t t1 = ((a1.M + BM - 1) / BM) * ((a1.N + BN - 1) / BN);
+  const int64_t t2 = ((a2.M + BM - 1) / BM) * ((a2.N + BN - 1) / BN);
+  if (t1 + t2 <= 0) return TS_OK;
+  if (t1 + t2 > 0x7fffffffLL) return ts_host::fail(TS_ERR_SHAPE, "%s: too many tiles", name);
+  hipLaunchKernelGGL((flce_gemm_pair<kMode1, kMA1, kMB1, kMode2, kMA2, kMB2, kW>),
+                     dim3((unsigned)(t1 + t2)), dim3(ts_gemm::Cfg<kW>::kThreads), 0, st, a1, a2,
+                     t1);
+  return ts_host::check_launch(name);
+}
+
 }  // namespace
 
 #define TS_TRY(x)                  \
@@ -640,9 +692,10 @@ ts_status launch_gemm(const GemmArgs& a, hipStream_t st, const char* name) {
   } while (0)
 
 extern "C" size_t ts_flce_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk,
-                                         int32_t with_grads) {
+                                         int32_t flags) {
   if (N <= 0 || H <= 0 || V <= 0) return 0;
-  return layout(N, H, V, chunk, with_grads != 0).total;
+  return layout(N, H, V, chunk, (flags & TS_FLCE_GRADS) != 0, (flags & TS_FLCE_ACCUM_BF16) != 0)
+      .total;
 }
 
 extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight,
@@ -650,12 +703,15 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
                                      int64_t V, int64_t ignore_index, int32_t reduction,
                                      float* loss, float* loss_rows, float* lse,
                                      void* grad_hidden, void* grad_weight, int64_t chunk,
-                                     void* workspace, size_t workspace_bytes,
+                                     int32_t flags, void* workspace, size_t workspace_bytes,
                                      ts_stream_t stream) {
   using ts_host::fail;
   if (N < 0 || H <= 0 || V <= 0)
     return fail(TS_ERR_SHAPE, "flce: bad shape N=%lld H=%lld V=%lld", (long long)N, (long long)H,
                 (long long)V);
+  if ((flags & ~TS_FLCE_ACCUM_BF16) != 0)
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce: unknown flags 0x%x", (unsigned)flags);
+  const bool acc_bf16 = (flags & TS_FLCE_ACCUM_BF16) != 0;
   if (N % 8 != 0 || H % 8 != 0 || V % 8 != 0)
     return fail(TS_ERR_SHAPE, "flce: N, H and V must be multiples of 8 (N=%lld H=%lld V=%lld)",
                 (long long)N, (long long)H, (long long)V);
@@ -688,7 +744,7 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
                        grad_weight != nullptr ? words : 0, loss);
     return ts_host::check_launch("fill_zero_u32");
   }
-  const Layout lay = layout(N, H, V, chunk, grads);
+  const Layout lay = layout(N, H, V, chunk, grads, acc_bf16);
   if (workspace == nullptr || workspace_bytes < lay.total || !ts_host::aligned16(workspace))
     return fail(TS_ERR_WORKSPACE, "flce: workspace needs %zu bytes (16-byte aligned), got %zu",
                 lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
@@ -739,40 +795,59 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
     TS_TRY(ts_host::check_launch("flce_dlogits"));
     using ts_gemm::kKMajor;
     using ts_gemm::kMNMajor;
-    if (grad_hidden != nullptr) {
-      GemmArgs d{};
-      d.A = Lc;  // dlogits [Mc, V], K-major
-      d.lda = V;
-      d.B = Wd;  // weight [V, H] as the [H, V] operand: MN-major, k = v
-      d.ldb = ldw;
-      d.M = Mc;
-      d.N = H;
-      d.K = V;
-      d.C = static_cast<__bf16*>(grad_hidden) + r0 * H;
-      d.ldc = H;
-      TS_TRY((launch_gemm<kEpiBf16, kKMajor, kMNMajor>(d, st, "flce_gemm_dhidden")));
-    }
-    if (grad_weight != nullptr) {
-      GemmArgs d{};
-      d.A = Lc;             // dlogits [Mc, V] as the [V, Mc] operand: MN-major, k = token
-      d.lda = V;
-      d.B = Hd + r0 * ldh;  // hidden rows r0 .. r0 + Mc as the [H, Mc] operand: MN-major
-      d.ldb = ldh;
-      d.M = V;
-      d.N = H;
-      d.K = Mc;
-      d.C = static_cast<__bf16*>(grad_weight);
-      d.ldc = H;
-      d.C32 = acc32;
-      d.ldc32 = H;
-      if (lay.nchunks == 1) {
-        TS_TRY((launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
-      } else if (c == 0) {
-        TS_TRY((launch_gemm<kEpiF32, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
-      } else if (c + 1 < lay.nchunks) {
-        TS_TRY((launch_gemm<kEpiAccF32, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
+    GemmArgs dh{};
+    dh.A = Lc;  // dlogits [Mc, V], K-major
+    dh.lda = V;
+    dh.B = Wd;  // weight [V, H] as the [H, V] operand: MN-major, k = v
+    dh.ldb = ldw;
+    dh.M = Mc;
+    dh.N = H;
+    dh.K = V;
+    dh.C = static_cast<__bf16*>(grad_hidden) + r0 * H;
+    dh.ldc = H;
+    GemmArgs dw{};
+    dw.A = Lc;             // dlogits [Mc, V] as the [V, Mc] operand: MN-major, k = token
+    dw.lda = V;
+    dw.B = Hd + r0 * ldh;  // hidden rows r0 .. r0 + Mc as the [H, Mc] operand: MN-major
+    dw.ldb = ldh;
+    dw.M = V;
+    dw.N = H;
+    dw.K = Mc;
+    dw.C = static_cast<__bf16*>(grad_weight);
+    dw.ldc = H;
+    dw.C32 = acc32;
+    dw.ldc32 = H;
+    // grad_weight sums over the chunks: fp32 in the workspace, rounded once at the
+    // end, or (TS_FLCE_ACCUM_BF16) in the bf16 output, rounded after every chunk
+    const int wmode = lay.nchunks == 1 ? kEpiBf16
+                      : acc_bf16       ? (c == 0 ? kEpiBf16 : kEpiAddBf16)
+                      : c == 0         ? kEpiF32
+                      : c + 1 < lay.nchunks ? kEpiAccF32
+                                            : kEpiAccBf16;
+    if (grad_hidden != nullptr && grad_weight != nullptr) {
+      // both gradient GEMMs in one grid (grad_hidden's few long tiles first)
+#define TS_PAIR(WM)                                                                         \
+  TS_TRY((launch_gemm_pair<kEpiBf16, kKMajor, kMNMajor, WM, kMNMajor, kMNMajor>(dh, dw, st,   \
+                                                                                "flce_gemm_grads")))
+      if (wmode == kEpiBf16) TS_PAIR(kEpiBf16);
+      else if (wmode == kEpiAddBf16) TS_PAIR(kEpiAddBf16);
+      else if (wmode == kEpiF32) TS_PAIR(kEpiF32);
+      else if (wmode == kEpiAccF32) TS_PAIR(kEpiAccF32);
+      else TS_PAIR(kEpiAccBf16);
+#undef TS_PAIR
+    } else if (grad_hidden != nullptr) {
+      TS_TRY((launch_gemm<kEpiBf16, kKMajor, kMNMajor>(dh, st, "flce_gemm_dhidden")));
+    } else if (grad_weight != nullptr) {
+      if (wmode == kEpiBf16) {
+        TS_TRY((launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(dw, st, "flce_gemm_dweight")));
+      } else if (wmode == kEpiAddBf16) {
+        TS_TRY((launch_gemm<kEpiAddBf16, kMNMajor, kMNMajor>(dw, st, "flce_gemm_dweight")));
+      } else if (wmode == kEpiF32) {
+        TS_TRY((launch_gemm<kEpiF32, kMNMajor, kMNMajor>(dw, st, "flce_gemm_dweight")));
+      } else if (wmode == kEpiAccF32) {
+        TS_TRY((launch_gemm<kEpiAccF32, kMNMajor, kMNMajor>(dw, st, "flce_gemm_dweight")));
       } else {
-        TS_TRY((launch_gemm<kEpiAccBf16, kMNMajor, kMNMajor>(d, st, "flce_gemm_dweight")));
+        TS_TRY((launch_gemm<kEpiAccBf16, kMNMajor, kMNMajor>(dw, st, "flce_gemm_dweight")));
       }
     }
   }

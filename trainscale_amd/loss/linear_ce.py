@@ -8,7 +8,7 @@ temperature, rl_training.py:114-122) this API follows, with the keywords of
 
 Two schedules run on the gfx950 kernels:
 
-* ``"two_pass"`` (the default; any reduction, any upstream gradient): the
+* ``"two_pass"`` (any reduction, any upstream gradient, backward twice): the
   forward (``ts_flce_forward``) runs the logits GEMM once and keeps only
   per-row softmax statistics and the label's logit; no logits are stored. The
   backward (``ts_flce_backward``) recomputes the logits one vocabulary chunk
@@ -18,9 +18,13 @@ Two schedules run on the gfx950 kernels:
   directly. Scratch: N x chunk bf16 dlogits plus N x H fp32.
 * ``"fused"`` (mean/sum, no transforms): one call (``ts_flce_fwd_bwd``) forms
   the loss and both gradients for an upstream gradient of 1, token chunk by
-  token chunk (a chunk's bf16 logits are stored, all N rows when the chunk is
-  not bounded); the backward scales them in place. Three GEMMs instead of
-  four, at the price of the logits scratch.
+  token chunk: a quarter of the tokens by default, whose bf16 logits are the
+  only [rows, V] scratch, with grad_weight summed over the chunks in its bf16
+  output (as autograd sums the reference's per-chunk bf16 gradients); the
+  backward scales the gradients in place. Three GEMMs instead of four.
+* ``"auto"`` (the default): "fused" when gradients are needed for mean/sum
+  without transforms, "two_pass" otherwise (forward only, reduction "none",
+  transforms).
 
 Numerics follow the reference's bf16 path: logits are rounded to bf16 as a
 bf16 matmul rounds them, softmax statistics and the loss are fp32, dlogits are
@@ -38,25 +42,26 @@ from .._lib import check, ptr
 from .sota_losses import SECOND_BACKWARD_MSG
 
 __all__ = ["LinearCrossEntropyFunction", "FusedLinearCrossEntropyFunction",
-           "fused_linear_cross_entropy", "chunked_log_softmax", "DEFAULT_LOGITS_SCRATCH",
+           "fused_linear_cross_entropy", "chunked_log_softmax", "DEFAULT_TOKEN_CHUNKS",
            "linear_ce_forward", "linear_ce_backward", "linear_ce_forward_backward",
            "VocabShardState", "linear_ce_vocab_phase1", "linear_ce_vocab_phase2"]
 
-# Upper bound on the bf16 logits scratch of one token chunk. 4 GiB keeps a
-# batch of up to 16384 tokens at V = 128256 in one chunk (one grad-weight GEMM
-# with a bf16 epilogue instead of an fp32 accumulator read and written per
-# chunk); against 288 GB of HBM the scratch is small.
-DEFAULT_LOGITS_SCRATCH = 4 << 30
+# The one-call schedule's token chunk with chunk_tokens=None: a quarter of the
+# tokens (rounded up to 256 rows), so its bf16 logits scratch stays within a
+# quarter of the [N, V] logits; batches of up to 256 tokens run as one chunk.
+DEFAULT_TOKEN_CHUNKS = 4
 
 _REDUCTIONS = {"mean": 0, "sum": 1}
+TS_FLCE_GRADS, TS_FLCE_ACCUM_BF16 = 1, 2  # include/trainscale_amd.h
 _REDUCTIONS_2P = {"mean": 0, "sum": 1, "none": 2}
 
 
 def _chunk_rows(N: int, V: int, chunk_tokens: Optional[int]) -> int:
+    """Token chunk of the one-call schedule (0: one chunk)."""
     if chunk_tokens is not None:
         return int(chunk_tokens)
-    rows = DEFAULT_LOGITS_SCRATCH // (2 * V)
-    rows = max(256, rows // 256 * 256)
+    rows = -(-N // DEFAULT_TOKEN_CHUNKS)
+    rows = -(-rows // 256) * 256
     return 0 if rows >= N else rows
 
 
@@ -145,9 +150,16 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
 def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
                                ignore_index: int = -100, reduction: str = "mean",
                                need_grad_hidden: bool = True, need_grad_weight: bool = True,
-                               chunk_tokens: Optional[int] = None):
+                               chunk_tokens: Optional[int] = None,
+                               grad_weight_accum: str = "fp32"):
     """Runs ts_flce_fwd_bwd; returns (loss fp32 0-d, loss_rows [N], lse [N],
-    grad_hidden or None, grad_weight or None) for an upstream gradient of 1."""
+    grad_hidden or None, grad_weight or None) for an upstream gradient of 1.
+    chunk_tokens: rows per token chunk (None: a quarter of the tokens, 0: one chunk);
+    grad_weight_accum: "fp32" (a V x H fp32 workspace, rounded once) or "bf16" (summed
+    in the bf16 output, rounded after each chunk)."""
+    if grad_weight_accum not in ("fp32", "bf16"):
+        raise ValueError(f"fused_linear_cross_entropy: grad_weight_accum must be 'fp32' or "
+                         f"'bf16', got {grad_weight_accum!r}")
     dev = _lib.require_gpu("fused_linear_cross_entropy", hidden, weight, labels)
     if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
         raise TypeError("fused_linear_cross_entropy: hidden and weight must be bfloat16")
@@ -174,7 +186,8 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
         hidden = torch.cat([hidden, hidden.new_zeros((pad, H))])
         labels = torch.cat([labels, labels.new_full((pad,), int(ignore_index))])
         out = linear_ce_forward_backward(hidden, weight, labels, ignore_index, reduction,
-                                         need_grad_hidden, need_grad_weight, chunk_tokens)
+                                         need_grad_hidden, need_grad_weight, chunk_tokens,
+                                         grad_weight_accum)
         loss, rows, lse, gh, gw = out
         return loss, rows[:N], lse[:N], gh[:N] if gh is not None else None, gw
     ldh = hidden.stride(0) if N > 1 else H
@@ -187,13 +200,15 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
     chunk = _chunk_rows(N, V, chunk_tokens)
     lib = _lib.load()
     grads = gh is not None or gw is not None
-    ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk, int(grads)))
+    flags = TS_FLCE_ACCUM_BF16 if grad_weight_accum == "bf16" else 0
+    ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk,
+                                              (TS_FLCE_GRADS if grads else 0) | flags))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         check(lib.ts_flce_fwd_bwd(
             ptr(hidden), ldh, ptr(weight), ldw, ptr(labels), N, H, V, int(ignore_index),
             _REDUCTIONS[reduction], ptr(loss), ptr(loss_rows), ptr(lse), ptr(gh), ptr(gw),
-            chunk, ptr(ws), ws_bytes, _lib.stream_handle(dev)), "ts_flce_fwd_bwd")
+            chunk, flags, ptr(ws), ws_bytes, _lib.stream_handle(dev)), "ts_flce_fwd_bwd")
     return loss, loss_rows, lse, gh, gw
 
 
@@ -324,13 +339,14 @@ class FusedLinearCrossEntropyFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
-                reduction: str = "mean", chunk_tokens: Optional[int] = None) -> Tensor:
+                reduction: str = "mean", chunk_tokens: Optional[int] = None,
+                grad_weight_accum: str = "bf16") -> Tensor:
         shape = hidden.shape
         h2 = hidden.reshape(-1, shape[-1])
         loss, _, _, gh, gw = linear_ce_forward_backward(
             h2, weight, labels, ignore_index, reduction,
             need_grad_hidden=ctx.needs_input_grad[0], need_grad_weight=ctx.needs_input_grad[1],
-            chunk_tokens=chunk_tokens)
+            chunk_tokens=chunk_tokens, grad_weight_accum=grad_weight_accum)
         ctx.hidden_shape = shape
         ctx.save_for_backward(gh, gw)
         return loss
@@ -346,7 +362,7 @@ class FusedLinearCrossEntropyFunction(torch.autograd.Function):
         _scale_(gh, scale)
         _scale_(gw, scale)
         gh = gh.view(ctx.hidden_shape) if gh is not None else None
-        return gh, gw, None, None, None, None
+        return gh, gw, None, None, None, None, None
 
 
 def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
@@ -354,10 +370,11 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
                                logit_softcapping: float = 0.0,
                                logit_scaling: float = 0.0,
                                temperature: float = 1.0,
-                               schedule: str = "two_pass",
+                               schedule: str = "auto",
                                vocab_chunk: Optional[int] = None,
-                               chunk_tokens: Optional[int] = None) -> Tensor:
-    """Cross-entropy of hidden @ weight.T against labels, without the logits in memory.
+                               chunk_tokens: Optional[int] = None,
+                               grad_weight_accum: str = "bf16") -> Tensor:
+    """Cross-entropy of hidden @ weight.T against labels, without all logits in memory.
 
     hidden [..., H] and weight [V, H] in bfloat16 (the lm_head layout of
     rl_training.py:156-162); labels [...] int64, ignore_index rows skipped.
@@ -365,10 +382,19 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
     (rl_training.py:114-122): t = softcap * tanh(z / softcap) when
     logit_softcapping > 0, then t * logit_scaling when logit_scaling > 0, then
     t / temperature. reduction "mean" (over non-ignored rows), "sum", or "none"
-    (per-row losses, shaped like labels). schedule "two_pass" (default) or
-    "fused" (mean/sum without transforms; chunk_tokens bounds its logits
-    scratch, None = one chunk up to 4 GiB).
+    (per-row losses, shaped like labels).
+
+    schedule: "auto" (default), "fused" or "two_pass" (module docstring).
+    "fused": chunk_tokens rows per token chunk (None: a quarter of the tokens,
+    0: one chunk, i.e. all [N, V] logits), grad_weight_accum "bf16" (summed in
+    the bf16 output) or "fp32" (a V x H fp32 workspace); a second backward
+    through its graph raises. "two_pass": vocab_chunk columns per recomputed
+    chunk (None: about V/8).
     """
+    if schedule == "auto":
+        grads = torch.is_grad_enabled() and (hidden.requires_grad or weight.requires_grad)
+        plain = logit_softcapping == 0.0 and logit_scaling == 0.0 and temperature == 1.0
+        schedule = "fused" if grads and plain and reduction in _REDUCTIONS else "two_pass"
     if schedule == "fused":
         if reduction not in _REDUCTIONS:
             raise ValueError("fused_linear_cross_entropy: schedule 'fused' takes reduction "
@@ -377,7 +403,7 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
             raise ValueError("fused_linear_cross_entropy: schedule 'fused' takes no logit "
                              "transforms; use schedule 'two_pass'")
         return FusedLinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index,
-                                                     reduction, chunk_tokens)
+                                                     reduction, chunk_tokens, grad_weight_accum)
     if schedule != "two_pass":
         raise ValueError(f"fused_linear_cross_entropy: unknown schedule {schedule!r}")
     out = LinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index, reduction,
@@ -402,5 +428,6 @@ def chunked_log_softmax(hidden_states: Tensor, lm_head: Tensor, input_ids: Tenso
     del num_chunks
     rows = fused_linear_cross_entropy(hidden_states, lm_head, input_ids, ignore_index=-(1 << 62),
                                       reduction="none", logit_softcapping=logit_softcapping,
-                                      logit_scaling=logit_scale, temperature=temperature)
+                                      logit_scaling=logit_scale, temperature=temperature,
+                                      schedule="two_pass")
     return -rows
