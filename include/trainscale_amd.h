@@ -193,7 +193,9 @@ ts_status ts_swiglu_bwd(const void* dout, const void* gate, const void* up,
  *     [0, table_rows) produce NaN outputs for that token instead of a fault.
  *   - in-register: cos_tab == sin_tab == NULL, inv_freq = HOST array of D/2
  *     fp32 values; angle_i = fp32(pos / pos_div) * inv_freq[i] (the fp32
- *     product torch.outer forms), then sin/cos are evaluated on the GPU.
+ *     product torch.outer forms), then multiplied by angle_scale when that is
+ *     not 1 (YaRN's mscale, kernels/rope_kernels.py:181-184: freqs * mscale),
+ *     and sin/cos are evaluated on the GPU. angle_scale is ignored with tables.
  *
  * Replaces _rope_forward_kernel/_rope_backward_kernel (kernels/triton_kernels.py
  * :713-890, Fast_RoPE :893-981), _rope_fwd_kernel/_rope_bwd_kernel,
@@ -212,7 +214,7 @@ ts_status ts_rope_apply(const void* q_in, void* q_out,
                         ts_dtype dtype, int64_t B, int64_t S, int64_t D,
                         const void* cos_tab, const void* sin_tab,
                         ts_dtype tab_dtype, int64_t tab_ld, int64_t table_rows,
-                        const float* inv_freq, float pos_div,
+                        const float* inv_freq, float pos_div, float angle_scale,
                         const int64_t* position_ids, int64_t pos_sb, int64_t pos_ss,
                         int64_t position_offset,
                         int32_t interleaved, int32_t backward,

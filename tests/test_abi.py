@@ -66,16 +66,19 @@ def _rope(lib, **kw):
     a = dict(q_in=FAKE, q_out=FAKE, qs=(4096, 512, 128), qos=(4096, 512, 128), Hq=4,
              k_in=NULL, k_out=NULL, ks=(0, 0, 0), kos=(0, 0, 0), Hk=0, dtype=1, B=2, S=8, D=128,
              cos=FAKE, sin=FAKE, tab_dtype=0, tab_ld=64, rows=8, inv=NULL, pos_div=1.0,
-             pos=NULL, psb=0, pss=0, off=0, il=0, bwd=0)
+             ascale=1.0, pos=NULL, psb=0, pss=0, off=0, il=0, bwd=0)
     a.update(kw)
     return lib.ts_rope_apply(a["q_in"], a["q_out"], *a["qs"], *a["qos"], a["Hq"], a["k_in"],
                              a["k_out"], *a["ks"], *a["kos"], a["Hk"], a["dtype"], a["B"], a["S"],
                              a["D"], a["cos"], a["sin"], a["tab_dtype"], a["tab_ld"], a["rows"],
-                             a["inv"], a["pos_div"], a["pos"], a["psb"], a["pss"], a["off"],
+                             a["inv"], a["pos_div"], a["ascale"], a["pos"], a["psb"], a["pss"],
+                             a["off"],
                              a["il"], a["bwd"], NULL)
 
 
 def test_rope_validation(lib):
+    assert _rope(lib, cos=NULL, sin=NULL, inv=FAKE, ascale=0.0) == INVALID
+    assert _rope(lib, cos=NULL, sin=NULL, inv=FAKE, ascale=float("inf")) == INVALID
     assert _rope(lib, D=127) == SHAPE
     assert _rope(lib, D=1024) == SHAPE
     assert _rope(lib, rows=7) == SHAPE  # positions 0..7 need 8 table rows

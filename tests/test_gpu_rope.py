@@ -201,6 +201,28 @@ def test_bf16_tables_rotary_embedding(gpu):
     assert_rope(y2, x0, cos, sin, oracle.rope_positions(2, 300))
 
 
+@pytest.mark.parametrize("scaling", [("yarn", 4.0, {}), ("yarn", 8.0, {"yarn_mscale_all_dim": 1.3}),
+                                     ("linear", 2.0, {}), ("ntk", 4.0, {})])
+def test_in_register_scalings_match_tables(gpu, scaling):
+    """In-register sin/cos reproduce the module's own fp32 tables for every scaling,
+    YaRN's angle mscale included (freqs * mscale, rope_kernels.py:181-184), forward
+    and backward."""
+    kind, factor, extra = scaling
+    torch.manual_seed(6)
+    rot = RotaryEmbedding(128, max_seq_len=1024, base=10000.0, scaling_type=kind,
+                          scaling_factor=factor, in_register=True, **extra)
+    from trainscale_amd.kernels.rope_kernels import compute_rope_frequencies
+    cos, sin = compute_rope_frequencies(rot.config, 1024, torch.device("cpu"), torch.float32)
+    x = torch.randn(2, 700, 4, 128, device=gpu).to(BF)
+    pos = oracle.rope_positions(2, 700, position_offset=300)
+    xg = x.clone().requires_grad_()
+    y = rot(xg.clone(), position_offset=300)
+    assert_rope(y, x, cos, sin, pos, what=f"{kind} fwd")
+    g = torch.randn_like(x)
+    y.backward(g)
+    assert_rope(xg.grad, g, cos, sin, pos, backward=True, what=f"{kind} bwd")
+
+
 def test_inplace_qk_and_offset(gpu):
     torch.manual_seed(4)
     q = torch.randn(2, 16, 8, 64, device=gpu).to(BF)

@@ -65,7 +65,7 @@ SIGNATURES = {
          P, P, I64, I64, I64, I64, I64, I64, I64,   # k
          I32, I64, I64, I64,                        # dtype, B, S, D
          P, P, I32, I64, I64,                       # tables
-         P, F32,                                    # inv_freq (host), pos_div
+         P, F32, F32,                               # inv_freq (host), pos_div, angle_scale
          P, I64, I64, I64,                          # position_ids, strides, offset
          I32, I32, P],                              # interleaved, backward, stream
         I32),

@@ -10,6 +10,7 @@
 // Each thread issues the loads of its first task, then the workgroup fills
 // LDS with cos/sin for its tokens: gathered from the caller's tables at
 // pos(b, s), or evaluated from the fp32 angle fp32(pos / pos_div) * inv_freq[i]
+// (times angle_scale when that is not 1)
 // (the product torch.outer forms on the host), once per (token, frequency)
 // and shared by all Hq + Hk heads. After one barrier the thread rotates and
 // stores. Backward is the same kernel with sin negated (the transpose
@@ -46,6 +47,7 @@ struct RopeArgs {
   const void* sin_tab;
   int64_t tab_ld, table_rows;
   float pos_div;
+  float angle_scale;         // multiplies the fp32 angle when != 1 (YaRN's mscale)
   const int64_t* position_ids;
   int64_t pos_sb, pos_ss, position_offset;
   int32_t backward;
@@ -80,7 +82,8 @@ __device__ inline void angle_at(const RopeArgs& a, int64_t pos, int f, float& c,
       c = s = __builtin_nanf("");
     }
   } else {
-    const float ang = ((float)pos / a.pos_div) * a.inv_freq[f];
+    float ang = ((float)pos / a.pos_div) * a.inv_freq[f];
+    if (a.angle_scale != 1.f) ang *= a.angle_scale;
     sincosf(ang, &s, &c);
   }
   if (a.backward) s = -s;
@@ -372,7 +375,8 @@ extern "C" ts_status ts_rope_apply(
     void* k_out, int64_t k_in_sb, int64_t k_in_ss, int64_t k_in_sh, int64_t k_out_sb,
     int64_t k_out_ss, int64_t k_out_sh, int64_t Hk, ts_dtype dtype, int64_t B, int64_t S,
     int64_t D, const void* cos_tab, const void* sin_tab, ts_dtype tab_dtype, int64_t tab_ld,
-    int64_t table_rows, const float* inv_freq, float pos_div, const int64_t* position_ids,
+    int64_t table_rows, const float* inv_freq, float pos_div, float angle_scale,
+    const int64_t* position_ids,
     int64_t pos_sb, int64_t pos_ss, int64_t position_offset, int32_t interleaved,
     int32_t backward, ts_stream_t stream) {
   using ts_host::fail;
@@ -414,6 +418,8 @@ extern "C" ts_status ts_rope_apply(
     if (inv_freq == nullptr)
       return fail(TS_ERR_INVALID_ARGUMENT, "rope: need cos/sin tables or inv_freq");
     if (!(pos_div > 0.f)) return fail(TS_ERR_INVALID_ARGUMENT, "rope: pos_div must be > 0");
+    if (!(angle_scale > 0.f) || !__builtin_isfinite(angle_scale))
+      return fail(TS_ERR_INVALID_ARGUMENT, "rope: angle_scale must be finite and > 0");
   }
   const int64_t ntok = B * S;
   if (ntok == 0 || Hq + Hk == 0) return TS_OK;
@@ -430,6 +436,7 @@ extern "C" ts_status ts_rope_apply(
   a.S = S; a.ntok = ntok; a.half = (int32_t)(D / 2);
   a.cos_tab = cos_tab; a.sin_tab = sin_tab; a.tab_ld = tab_ld; a.table_rows = table_rows;
   a.pos_div = pos_div > 0.f ? pos_div : 1.f;
+  a.angle_scale = table ? 1.f : angle_scale;
   a.position_ids = position_ids; a.pos_sb = pos_sb; a.pos_ss = pos_ss;
   a.position_offset = position_offset;
   a.backward = backward;

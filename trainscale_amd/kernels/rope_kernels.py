@@ -289,17 +289,18 @@ class _RoPEThetaFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: Tensor, inv_freq: Tensor, pos_div: float,
                 position_ids: Optional[Tensor], position_offset: int, interleaved: bool,
-                inplace: bool) -> Tensor:
+                inplace: bool, angle_scale: float = 1.0) -> Tensor:
         ctx.save_for_backward(position_ids)
         ctx.inv_freq = inv_freq
         ctx.pos_div = pos_div
+        ctx.angle_scale = angle_scale
         ctx.position_offset = position_offset
         ctx.interleaved = interleaved
         x = ops._bshd(x, "apply_rope_theta x")
         out = x if inplace else torch.empty_like(x, memory_format=torch.contiguous_format)
         ops.rope_apply(x, out, None, None, inv_freq=inv_freq, pos_div=pos_div,
-                       position_ids=position_ids, position_offset=position_offset,
-                       interleaved=interleaved)
+                       angle_scale=angle_scale, position_ids=position_ids,
+                       position_offset=position_offset, interleaved=interleaved)
         return out
 
     @staticmethod
@@ -308,9 +309,10 @@ class _RoPEThetaFunction(torch.autograd.Function):
         g = ops._bshd(grad_output, "apply_rope_theta grad")
         grad_input = torch.empty_like(g, memory_format=torch.contiguous_format)
         ops.rope_apply(g, grad_input, None, None, inv_freq=ctx.inv_freq, pos_div=ctx.pos_div,
-                       position_ids=position_ids, position_offset=ctx.position_offset,
-                       interleaved=ctx.interleaved, backward=True)
-        return grad_input, None, None, None, None, None, None
+                       angle_scale=ctx.angle_scale, position_ids=position_ids,
+                       position_offset=ctx.position_offset, interleaved=ctx.interleaved,
+                       backward=True)
+        return grad_input, None, None, None, None, None, None, None
 
 
 # ---------------------------------------------------------------------------
@@ -347,17 +349,19 @@ def inplace_rope_embedding(Q: Tensor, K: Tensor, cos: Tensor, sin: Tensor,
 
 def apply_rope_theta(x: Tensor, theta: float = 10000.0, position_ids: Optional[Tensor] = None,
                      position_offset: int = 0, interleaved: bool = False, inplace: bool = True,
-                     scaling_factor: float = 1.0, inv_freq: Optional[Tensor] = None) -> Tensor:
+                     scaling_factor: float = 1.0, inv_freq: Optional[Tensor] = None,
+                     angle_scale: float = 1.0) -> Tensor:
     """RoPE with in-register sin/cos: no cos/sin tables are read.
 
     The angle of pair i at position p is fp32(p / scaling_factor) * inv_freq[i],
     the fp32 product ``precompute_freqs_cis`` forms on the host, with
-    inv_freq = 1/theta**(arange(0, D, 2)/D) unless given.
+    inv_freq = 1/theta**(arange(0, D, 2)/D) unless given, then times angle_scale
+    when that is not 1 (YaRN's mscale, rope_kernels.py:181-184).
     """
     if inv_freq is None:
         inv_freq = _base_inv_freq(theta, x.shape[-1], "cpu")
     return _RoPEThetaFunction.apply(x, inv_freq, float(scaling_factor), position_ids,
-                                    position_offset, interleaved, inplace)
+                                    position_offset, interleaved, inplace, float(angle_scale))
 
 
 class _HFTableRoPEFunction(torch.autograd.Function):
@@ -433,8 +437,8 @@ class RotaryEmbedding(nn.Module):
 
     Like the reference, the tables are cast to the activation dtype before use.
     ``in_register=True`` evaluates sin/cos on the GPU in fp32 instead (more
-    accurate than bf16 tables, no table reads); it supports the
-    none/linear/ntk/dynamic_ntk/longrope scalings (YaRN's mscale needs tables).
+    accurate than bf16 tables, no table reads), from the same fp32 angle as
+    the tables, YaRN's mscale included.
     """
 
     def __init__(self, dim: int, max_seq_len: int = 8192, base: float = 10000.0,
@@ -450,8 +454,6 @@ class RotaryEmbedding(nn.Module):
                                  scaling_type=_SCALING_NAMES.get(scaling_type.lower(),
                                                                  RoPEScalingType.NONE),
                                  scaling_factor=scaling_factor, **kwargs)
-        if in_register and self.config.scaling_type == RoPEScalingType.YARN:
-            raise ValueError("RotaryEmbedding: in_register does not support YaRN scaling")
         self.in_register = in_register
         cos, sin = compute_rope_frequencies(self.config, max_seq_len, torch.device("cpu"),
                                             torch.float32)
@@ -476,10 +478,13 @@ class RotaryEmbedding(nn.Module):
     def forward(self, x: Tensor, position_ids: Optional[Tensor] = None,
                 position_offset: int = 0) -> Tensor:
         if self.in_register:
+            mscale = (_yarn_mscale(self.config)
+                      if self.config.scaling_type == RoPEScalingType.YARN else 1.0)
             return apply_rope_theta(x, position_ids=position_ids,
                                     position_offset=position_offset,
                                     interleaved=self.interleaved, inplace=True,
-                                    scaling_factor=self._pos_div(), inv_freq=self._inv_freq)
+                                    scaling_factor=self._pos_div(), inv_freq=self._inv_freq,
+                                    angle_scale=mscale)
         self._update_cache(x.shape[1] + position_offset, x.device, x.dtype)
         return apply_rope(x, self.cos_cached, self.sin_cached, position_ids=position_ids,
                           position_offset=position_offset, interleaved=self.interleaved,

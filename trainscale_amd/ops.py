@@ -140,6 +140,7 @@ def rope_apply(q_in: Optional[Tensor], q_out: Optional[Tensor],
                k_in: Optional[Tensor], k_out: Optional[Tensor], *,
                cos: Optional[Tensor] = None, sin: Optional[Tensor] = None,
                inv_freq: Optional[Tensor] = None, pos_div: float = 1.0,
+               angle_scale: float = 1.0,
                position_ids: Optional[Tensor] = None, position_offset: int = 0,
                interleaved: bool = False, backward: bool = False) -> None:
     """Rotates q_in -> q_out and k_in -> k_out (either pair may be None; in == out is in place).
@@ -225,7 +226,7 @@ def rope_apply(q_in: Optional[Tensor], q_out: Optional[Tensor],
             ptr(k_in), ptr(k_out), *strides(k_in), *strides(k_out), Hk,
             _lib.dtype_code(ref, "rope"), B, S, D,
             ptr(cos), ptr(sin), tab_code, tab_ld, tab_rows,
-            inv_ptr, float(pos_div),
+            inv_ptr, float(pos_div), float(angle_scale),
             ptr(position_ids), pos_sb, pos_ss, int(position_offset),
             int(bool(interleaved)), int(bool(backward)), _lib.stream_handle(dev)),
             "ts_rope_apply")
