@@ -26,6 +26,8 @@
 // chunk size bounds that at Nc x V x 2 bytes.
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "gemm.hpp"
 
@@ -162,50 +164,66 @@ __device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) 
 
   if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32 || kMode == kEpiAccBf16 ||
                 kMode == kEpiAddBf16) {
-    // fp32 C32 rows of 128 columns = 512 B: 32 lanes x 16 B per row, 2 rows per step
+    // fp32 C32 rows of 128 columns = 512 B: 32 lanes x 16 B per row, 2 rows per step.
+    // The modes that add to what C or C32 holds load the old values of a row tile's steps
+    // ahead (all 16 steps' 8-byte bf16 values, or 8 steps' 16-byte fp32 values at a time
+    // to stay within the register budget), the first batch before the tile is staged, so
+    // the loads' latency overlaps the staging instead of stalling step after step.
     const int c4 = lane & 31;
+    const int64_t gc = nb + c4 * 4;
+    constexpr bool kAddOld = kMode == kEpiAccF32 || kMode == kEpiAccBf16 || kMode == kEpiAddBf16;
+    constexpr int kPre = kMode == kEpiAddBf16 ? 16 : (kAddOld ? 8 : 16);
+    using Old = typename std::conditional<kMode == kEpiAddBf16, uint2, float4>::type;
 #pragma unroll
     for (int i = 0; i < kTI; ++i) {
-      stage_f32_tile(acc, i, region, lane);
-#pragma unroll 4
-      for (int it = 0; it < 16; ++it) {
-        const int lrow = it * 2 + (lane >> 5);
-        const int64_t gm = mb + i * 32 + lrow;
-        const int64_t gc = nb + c4 * 4;
-        if (gm < a.M && gc < a.N) {  // N % 8 == 0: 4 columns are all in or all out
-          float4 v = *reinterpret_cast<const float4*>(region + lrow * 512 + c4 * 16);
-          if constexpr (kMode == kEpiAddBf16) {
-            uint2* q = reinterpret_cast<uint2*>(a.C + gm * a.ldc + gc);
-            const uint2 o = *q;
-            v.x += __builtin_bit_cast(float, o.x << 16);
-            v.y += __builtin_bit_cast(float, o.x & 0xffff0000u);
-            v.z += __builtin_bit_cast(float, o.y << 16);
-            v.w += __builtin_bit_cast(float, o.y & 0xffff0000u);
-            bf16x2_t lo = {(__bf16)v.x, (__bf16)v.y};
-            bf16x2_t hi = {(__bf16)v.z, (__bf16)v.w};
-            uint2 pk;
-            pk.x = __builtin_bit_cast(uint32_t, lo);
-            pk.y = __builtin_bit_cast(uint32_t, hi);
-            *q = pk;
-            continue;
+      const int64_t gm0 = mb + i * 32 + (lane >> 5);  // this lane's row at step it: gm0 + 2 it
+#pragma unroll
+      for (int h = 0; h < 16; h += kPre) {
+        Old old[kAddOld ? kPre : 1];
+        if constexpr (kAddOld) {
+#pragma unroll
+          for (int q = 0; q < kPre; ++q) {
+            const int64_t gm = gm0 + 2 * (h + q);
+            const bool in = gm < a.M && gc < a.N;  // N % 8 == 0: 4 columns all in or all out
+            if constexpr (kMode == kEpiAddBf16)
+              old[q] = in ? *reinterpret_cast<const uint2*>(a.C + gm * a.ldc + gc)
+                          : make_uint2(0u, 0u);
+            else
+              old[q] = in ? *reinterpret_cast<const float4*>(a.C32 + gm * a.ldc32 + gc)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
           }
-          float* p = a.C32 + gm * a.ldc32 + gc;
-          if constexpr (kMode != kEpiF32) {
-            const float4 o = *reinterpret_cast<const float4*>(p);
-            v.x += o.x;
-            v.y += o.y;
-            v.z += o.z;
-            v.w += o.w;
-          }
-          if constexpr (kMode == kEpiAccBf16) {
-            bf16x2_t lo = {(__bf16)v.x, (__bf16)v.y};
-            bf16x2_t hi = {(__bf16)v.z, (__bf16)v.w};
-            uint2 pk;
-            pk.x = __builtin_bit_cast(uint32_t, lo);
-            pk.y = __builtin_bit_cast(uint32_t, hi);
-            *reinterpret_cast<uint2*>(a.C + gm * a.ldc + gc) = pk;
-          } else {
-            *reinterpret_cast<float4*>(p) = v;
+        }
+        if (h == 0) stage_f32_tile(acc, i, region, lane);
+#pragma unroll
+        for (int q = 0; q < kPre; ++q) {
+          const int it = h + q;
+          const int lrow = it * 2 + (lane >> 5);
+          const int64_t gm = gm0 + 2 * it;
+          if (gm < a.M && gc < a.N) {
+            float4 v = *reinterpret_cast<const float4*>(region + lrow * 512 + c4 * 16);
+            if constexpr (kMode == kEpiAddBf16) {
+              const uint2 o = old[q];
+              v.x += __builtin_bit_cast(float, o.x << 16);
+              v.y += __builtin_bit_cast(float, o.x & 0xffff0000u);
+              v.z += __builtin_bit_cast(float, o.y << 16);
+              v.w += __builtin_bit_cast(float, o.y & 0xffff0000u);
+            } else if constexpr (kAddOld) {
+              const float4 o = old[q];
+              v.x += o.x;
+              v.y += o.y;
+              v.z += o.z;
+              v.w += o.w;
+            }
+            if constexpr (kMode == kEpiAccBf16 || kMode == kEpiAddBf16) {
+              bf16x2_t lo = {(__bf16)v.x, (__bf16)v.y};
+              bf16x2_t hi = {(__bf16)v.z, (__bf16)v.w};
+              uint2 pk;
+              pk.x = __builtin_bit_cast(uint32_t, lo);
+              pk.y = __builtin_bit_cast(uint32_t, hi);
+              *reinterpret_cast<uint2*>(a.C + gm * a.ldc + gc) = pk;
+            } else {
+              *reinterpret_cast<float4*>(a.C32 + gm * a.ldc32 + gc) = v;
+            }
           }
         }
       }
