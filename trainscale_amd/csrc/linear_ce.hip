@@ -1296,33 +1296,34 @@ extern "C" ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const vo
   const __bf16* Wd = static_cast<const __bf16*>(weight);
   using ts_gemm::kKMajor;
   using ts_gemm::kMNMajor;
-  if (grad_hidden_partial != nullptr) {
-    GemmArgs d{};
-    d.A = L;  // dlogits [N, Vp], K-major
-    d.lda = Vp;
-    d.B = Wd;  // weight shard [Vp, H] as the [H, Vp] operand: MN-major
-    d.ldb = ldw;
-    d.M = N;
-    d.N = H;
-    d.K = Vp;
-    d.C = static_cast<__bf16*>(grad_hidden_partial);
-    d.ldc = H;
-    TS_TRY((launch_gemm<kEpiBf16, kKMajor, kMNMajor>(d, st, "flce_vocab_gemm_dhidden")));
+  GemmArgs dh{};
+  dh.A = L;  // dlogits [N, Vp], K-major
+  dh.lda = Vp;
+  dh.B = Wd;  // weight shard [Vp, H] as the [H, Vp] operand: MN-major
+  dh.ldb = ldw;
+  dh.M = N;
+  dh.N = H;
+  dh.K = Vp;
+  dh.C = static_cast<__bf16*>(grad_hidden_partial);
+  dh.ldc = H;
+  GemmArgs dw{};
+  dw.A = L;  // dlogits [N, Vp] as the [Vp, N] operand: MN-major
+  dw.lda = Vp;
+  dw.B = Hd;  // hidden [N, H] as the [H, N] operand: MN-major
+  dw.ldb = ldh;
+  dw.M = Vp;
+  dw.N = H;
+  dw.K = N;
+  dw.C = static_cast<__bf16*>(grad_weight_shard);
+  dw.ldc = H;
+  if (grad_hidden_partial != nullptr && grad_weight_shard != nullptr) {
+    // both GEMMs read the same dlogits: one grid
+    return launch_gemm_pair<kEpiBf16, kKMajor, kMNMajor, kEpiBf16, kMNMajor, kMNMajor>(
+        dh, dw, st, "flce_vocab_gemm_grads");
   }
-  if (grad_weight_shard != nullptr) {
-    GemmArgs d{};
-    d.A = L;  // dlogits [N, Vp] as the [Vp, N] operand: MN-major
-    d.lda = Vp;
-    d.B = Hd;  // hidden [N, H] as the [H, N] operand: MN-major
-    d.ldb = ldh;
-    d.M = Vp;
-    d.N = H;
-    d.K = N;
-    d.C = static_cast<__bf16*>(grad_weight_shard);
-    d.ldc = H;
-    TS_TRY((launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(d, st, "flce_vocab_gemm_dweight")));
-  }
-  return TS_OK;
+  if (grad_hidden_partial != nullptr)
+    return launch_gemm<kEpiBf16, kKMajor, kMNMajor>(dh, st, "flce_vocab_gemm_dhidden");
+  return launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(dw, st, "flce_vocab_gemm_dweight");
 }
 
 namespace {
