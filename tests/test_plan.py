@@ -7,6 +7,11 @@ indices. A small C++ driver compiled with g++ sweeps many shapes and checks:
 * every backward plan writes at most the partial rows ts_rmsnorm_bwd_workspace_size
   reports (regression: a split-row launch once wrote past a workspace sized
   for the unsplit launch);
+* every 16-byte load the backward kernel issues (ts_plan::rms_bwd_load_offset,
+  the function the kernel computes its addresses with) lies inside the matrix,
+  including the lanes and row slots with nothing to load (regression: those
+  once loaded their own row's start, past the matrix for the slots beyond the
+  last row and for lanes beyond a short row);
 * register plans cover every 16-byte vector of the row and stay within the
   template instantiations the launcher has;
 * the grouped GEMM tile order visits every output tile exactly once;
@@ -75,6 +80,25 @@ int main() {
               CHECK(rows == 0 || (p.grid - 1) * p.steps * r.rpb < rows, "empty workgroup");
               CHECK(p.grid < (1ll << 31), "grid too large");
               if (dw) CHECK(p.nparts == p.grid * r.rpb, "nparts != grid * rpb");
+              // every 16-byte load of the backward kernel lies inside the [rows, ld] matrix
+              // (ld = cols and a wider stride), for every workgroup, slot, step and lane
+              if (rows > 0 && rows <= 2049 && cols <= 8192) {
+                for (long long ld : {cols, cols + V}) {
+                  const long long rstep = p.grid * r.rpb;
+                  for (long long wg = 0; wg < p.grid; wg += (p.grid > 64 ? p.grid / 17 : 1))
+                    for (int sub = 0; sub < r.rpb; ++sub)
+                      for (long long st = 0; st < p.steps + 1; ++st)
+                        for (int t = 0; t < r.tpr; t += (r.tpr > 64 ? 7 : 1))
+                          for (int k = 0; k < r.kv; ++k) {
+                            const long long off = rms_bwd_load_offset(
+                                wg * r.rpb + sub, st, rstep, p.steps, rows, t, k, r.tpr, V, nvec, ld);
+                            CHECK(off >= 0 && off + V <= (rows - 1) * ld + cols,
+                                  "rows=%lld cols=%lld ld=%lld wg=%lld sub=%d st=%lld t=%d k=%d: "
+                                  "load at element %lld past the matrix", rows, cols, ld, wg, sub,
+                                  st, t, k, off);
+                          }
+                }
+              }
             }
           }
         }

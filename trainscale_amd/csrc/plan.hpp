@@ -115,6 +115,21 @@ inline RmsBwdPlan rms_bwd_plan(int64_t rows, int64_t cols, int elt_bytes, bool v
   return p;
 }
 
+// Element offset, from the start of a [rows, ld] matrix, of the k-th 16-byte
+// vector (V elements) that lane t of a backward row slot loads at step st:
+// the slot's first row is row0, consecutive steps are rstep rows apart, and a
+// row has nvec vectors. A lane with nothing to load there (a step past
+// `steps`, a row past the matrix, a vector past the row) gets offset 0, the
+// matrix's first element, so every load of the kernel stays inside the matrix.
+TS_HOST_DEVICE inline int64_t rms_bwd_load_offset(int64_t row0, int64_t st, int64_t rstep,
+                                                  int64_t steps, int64_t rows, int t, int k,
+                                                  int tpr, int V, int64_t nvec, int64_t ld) {
+  const int64_t row = row0 + st * rstep;
+  const int64_t v = (int64_t)t + (int64_t)k * tpr;
+  const bool ok = st < steps && row < rows && v < nvec;
+  return ok ? row * ld + v * V : 0;
+}
+
 // Rows of fp32 dW partials any backward launch for (rows, cols) may write:
 // the maximum over element sizes 2 and 4 and over both paths.
 inline int64_t rms_bwd_workspace_rows(int64_t rows, int64_t cols) {

@@ -231,30 +231,25 @@ __global__ __launch_bounds__(512) void rms_bwd_reg(
 
   // Loads of row group st into `sl` (zeros past the end of this workgroup's
   // range or of the matrix).
-  // This thread's first row and its element t * V there; row group st adds
-  // st * kRpb rows (a uniform offset).
+  // This thread's first row; row group st adds st * rstep rows.
   const int64_t row0 = (int64_t)blockIdx.x * kRpb + sub;
   const int64_t rstep = (int64_t)gridDim.x * kRpb;
-  const T* xb = x + row0 * ldx + (int64_t)t * V;
-  const T* dyb = dy + row0 * lddy + (int64_t)t * V;
-  //
-  //
-  // The loads are unconditional (an address outside the matrix is replaced by
-  // the thread's first element, which exists whenever the kernel runs) and
-  // the data of such lanes is zeroed where it is used, which keeps the loads
-  // free of branches.
+  // The loads are unconditional: a lane with nothing to load (a row past this
+  // workgroup's range or the matrix, or a vector past the row) loads the
+  // matrix's first element instead (ts_plan::rms_bwd_load_offset), which
+  // exists whenever the kernel runs, and the data of such lanes is zeroed
+  // where it is used, which keeps the loads free of branches.
   auto issue = [&](BwdSlot<T, KV>& sl, int64_t st) {
     const int64_t row = row0 + st * rstep;
     const bool valid = st < steps && row < rows;
-    const int64_t sx = valid ? st * (rstep * ldx) : 0;
-    const int64_t sdy = valid ? st * (rstep * lddy) : 0;
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
-      const bool ok = valid && t + k * TPR < nvec;
-      sl.xv[k] = ld16_stream(xb + (ok ? sx + k * TPR * V : 0));
-      sl.dv[k] = ld16_stream(dyb + (ok ? sdy + k * TPR * V : 0));
+      sl.xv[k] = ld16_stream(x + ts_plan::rms_bwd_load_offset(row0, st, rstep, steps, rows, t, k,
+                                                              TPR, V, nvec, ldx));
+      sl.dv[k] = ld16_stream(dy + ts_plan::rms_bwd_load_offset(row0, st, rstep, steps, rows, t,
+                                                               k, TPR, V, nvec, lddy));
     }
-    sl.rstd = rstd_in[valid ? row : row0];
+    sl.rstd = rstd_in[valid ? row : 0];
     sl.valid = valid;
   };
 
