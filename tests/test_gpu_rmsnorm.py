@@ -90,6 +90,22 @@ def test_shapes_bf16(gpu, rows, cols):
     check_against_oracle(x, w, dy, 1e-6)
 
 
+@pytest.mark.parametrize("rows,cols", [(5, 256), (3, 512), (7, 1024), (2, 2048), (9, 200),
+                                       (1, 4096)])
+def test_backward_fewer_rows_than_row_slots(gpu, rows, cols):
+    """Backward launches whose last workgroup has row slots past the last row.
+
+    Up to 256 vectors a row, a backward workgroup holds several rows at a time
+    (8 at 256 columns of bf16); the slots past the matrix must load nothing
+    outside it. Each case is its own allocation of exactly rows x cols.
+    """
+    torch.manual_seed(rows * 31 + cols)
+    x = torch.randn(rows, cols, device=gpu).to(BF)
+    w = (1 + 0.02 * torch.randn(cols, device=gpu)).to(BF)
+    dy = torch.randn(rows, cols, device=gpu).to(BF)
+    check_against_oracle(x, w, dy, 1e-6)
+
+
 @pytest.mark.parametrize("dtype,wdtype", [(torch.float16, torch.float16),
                                           (torch.float32, torch.float32),
                                           (BF, torch.float32), (torch.float16, torch.float32)])
