@@ -16,7 +16,8 @@
 //      place as the MN-major [H, V] operand)
 //   5. grad_weight      += dlogits^T @ hidden  (MFMA; dlogits and hidden are
 //      read in place as MN-major operands); with several chunks the sum is
-//      carried in fp32 and rounded once.
+//      carried in fp32 and rounded once, or (TS_FLCE_ACCUM_BF16) kept in the
+//      bf16 output and rounded after every chunk.
 //   No operand is transposed in memory: gemm.hpp reads MN-major tiles with
 //   transposing LDS loads.
 // Every reduction has a fixed order, so results are bit-reproducible.
@@ -26,7 +27,6 @@
 // chunk size bounds that at Nc x V x 2 bytes.
 #include <math.h>
 
-#include <type_traits>
 
 #include "common.hpp"
 #include "gemm.hpp"
@@ -162,35 +162,70 @@ __device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) 
   __syncthreads();
   uint8_t* region = smem + wid * kRegion;
 
-  if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32 || kMode == kEpiAccBf16 ||
-                kMode == kEpiAddBf16) {
+  if constexpr (kMode == kEpiAddBf16) {
+    // bf16 running sum C = bf16(C + acc): a lane owns 8 consecutive columns (16 bytes of
+    // C) of a 128-column row, 16 lanes a row, 4 rows a step. All 8 steps' old values of a
+    // 32-row tile are loaded before that tile is staged, so their latency overlaps the
+    // staging; the loads and stores are 16 bytes wide (measured on MI355X at the C5
+    // chunk shape: the gradient pair 3.57-3.59 ms against 3.65 ms with 8-byte accesses,
+    // 32 lanes a row).
+    const int c8 = lane & 15;
+    const int64_t gc = nb + c8 * 8;
+#pragma unroll
+    for (int i = 0; i < kTI; ++i) {
+      const int64_t gm0 = mb + i * 32 + (lane >> 4);  // this lane's row at step s: gm0 + 4 s
+      u32x4 old[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int64_t gm = gm0 + 4 * s;
+        // N % 8 == 0: a lane's 8 columns are all in or all out
+        old[s] = gm < a.M && gc < a.N ? ld16(a.C + gm * a.ldc + gc) : u32x4{0u, 0u, 0u, 0u};
+      }
+      stage_f32_tile(acc, i, region, lane);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int lrow = 4 * s + (lane >> 4);
+        const int64_t gm = gm0 + 4 * s;
+        if (gm < a.M && gc < a.N) {
+          const float4 v0 = *reinterpret_cast<const float4*>(region + lrow * 512 + c8 * 32);
+          const float4 v1 = *reinterpret_cast<const float4*>(region + lrow * 512 + c8 * 32 + 16);
+          float f[8];
+          Elt<__bf16>::unpack(old[s], f);
+          f[0] += v0.x;
+          f[1] += v0.y;
+          f[2] += v0.z;
+          f[3] += v0.w;
+          f[4] += v1.x;
+          f[5] += v1.y;
+          f[6] += v1.z;
+          f[7] += v1.w;
+          st16(a.C + gm * a.ldc + gc, Elt<__bf16>::pack(f));
+        }
+      }
+    }
+  } else if constexpr (kMode == kEpiF32 || kMode == kEpiAccF32 || kMode == kEpiAccBf16) {
     // fp32 C32 rows of 128 columns = 512 B: 32 lanes x 16 B per row, 2 rows per step.
-    // The modes that add to what C or C32 holds load the old values of a row tile's steps
-    // ahead (all 16 steps' 8-byte bf16 values, or 8 steps' 16-byte fp32 values at a time
-    // to stay within the register budget), the first batch before the tile is staged, so
-    // the loads' latency overlaps the staging instead of stalling step after step.
+    // The modes that add to what C32 holds load the old values of 8 steps at a time
+    // (16-byte fp32 values; more would exceed the register budget), the first batch
+    // before the tile is staged, so the loads' latency overlaps the staging instead of
+    // stalling step after step.
     const int c4 = lane & 31;
     const int64_t gc = nb + c4 * 4;
-    constexpr bool kAddOld = kMode == kEpiAccF32 || kMode == kEpiAccBf16 || kMode == kEpiAddBf16;
-    constexpr int kPre = kMode == kEpiAddBf16 ? 16 : (kAddOld ? 8 : 16);
-    using Old = typename std::conditional<kMode == kEpiAddBf16, uint2, float4>::type;
+    constexpr bool kAddOld = kMode == kEpiAccF32 || kMode == kEpiAccBf16;
+    constexpr int kPre = kAddOld ? 8 : 16;
 #pragma unroll
     for (int i = 0; i < kTI; ++i) {
       const int64_t gm0 = mb + i * 32 + (lane >> 5);  // this lane's row at step it: gm0 + 2 it
 #pragma unroll
       for (int h = 0; h < 16; h += kPre) {
-        Old old[kAddOld ? kPre : 1];
+        float4 old[kAddOld ? kPre : 1];
         if constexpr (kAddOld) {
 #pragma unroll
           for (int q = 0; q < kPre; ++q) {
             const int64_t gm = gm0 + 2 * (h + q);
             const bool in = gm < a.M && gc < a.N;  // N % 8 == 0: 4 columns all in or all out
-            if constexpr (kMode == kEpiAddBf16)
-              old[q] = in ? *reinterpret_cast<const uint2*>(a.C + gm * a.ldc + gc)
-                          : make_uint2(0u, 0u);
-            else
-              old[q] = in ? *reinterpret_cast<const float4*>(a.C32 + gm * a.ldc32 + gc)
-                          : make_float4(0.f, 0.f, 0.f, 0.f);
+            old[q] = in ? *reinterpret_cast<const float4*>(a.C32 + gm * a.ldc32 + gc)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
           }
         }
         if (h == 0) stage_f32_tile(acc, i, region, lane);
@@ -201,20 +236,14 @@ __device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) 
           const int64_t gm = gm0 + 2 * it;
           if (gm < a.M && gc < a.N) {
             float4 v = *reinterpret_cast<const float4*>(region + lrow * 512 + c4 * 16);
-            if constexpr (kMode == kEpiAddBf16) {
-              const uint2 o = old[q];
-              v.x += __builtin_bit_cast(float, o.x << 16);
-              v.y += __builtin_bit_cast(float, o.x & 0xffff0000u);
-              v.z += __builtin_bit_cast(float, o.y << 16);
-              v.w += __builtin_bit_cast(float, o.y & 0xffff0000u);
-            } else if constexpr (kAddOld) {
+            if constexpr (kAddOld) {
               const float4 o = old[q];
               v.x += o.x;
               v.y += o.y;
               v.z += o.z;
               v.w += o.w;
             }
-            if constexpr (kMode == kEpiAccBf16 || kMode == kEpiAddBf16) {
+            if constexpr (kMode == kEpiAccBf16) {
               bf16x2_t lo = {(__bf16)v.x, (__bf16)v.y};
               bf16x2_t hi = {(__bf16)v.z, (__bf16)v.w};
               uint2 pk;
