@@ -119,6 +119,26 @@ def test_token_chunks_accumulate_grad_weight(gpu, chunk, accum):
         assert rel_fro(gw1.float() * n_valid, sum(p.float() for p in parts)) <= 8e-3
 
 
+@pytest.mark.parametrize("accum", ["fp32", "bf16"])
+def test_token_chunks_partial_tiles(gpu, accum):
+    # grad_weight [V, H] with neither dimension a multiple of the 256 x 256 tile (nor H of
+    # the 128 columns a wave writes): the running-sum epilogues must mask rows and columns
+    torch.manual_seed(9)
+    N, H, V = 1032, 296, 776
+    h = torch.randn(N, H, device=gpu).to(BF)
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[3::11] = -100
+    chunk = 256
+    _, _, gw1 = check_against_oracle(h, w, labels, chunk=chunk, accum=accum)
+    if accum == "bf16":
+        parts = [linear_ce_forward_backward(h[s:s + chunk], w, labels[s:s + chunk],
+                                            reduction="sum", chunk_tokens=0)[4]
+                 for s in range(0, N, chunk)]
+        n_valid = int((labels != -100).sum())
+        assert rel_fro(gw1.float() * n_valid, sum(p.float() for p in parts)) <= 8e-3
+
+
 def test_exact_logits_pin_the_gemms(gpu):
     # entries of hidden in {-1, 0, 1}, of weight in {0, +-0.5, +-1}, H = 64: every logit is
     # a multiple of 0.5 of magnitude <= 64, exact in bf16 however the sum is ordered
