@@ -521,7 +521,41 @@ def bench_linear_ce(dev, steps: int, warmup: int):
     out["rl_form"] = line(time_ms(rl, reps, warm),
                           what="two-pass, reduction none, temperature 0.9, per-row upstream "
                                "gradients (chunked_log_softmax's use by GRPOCompute)")
-    del wsf, wsb
+    del wsb
+    torch.cuda.empty_cache()
+
+    # the two-pass schedule with the forward's bf16 logits kept for the backward
+    ws_k = int(lib.ts_flce_backward_kept_workspace_size(N))
+    wsk = torch.empty((ws_k,), dtype=torch.uint8, device=dev)
+    kept = torch.empty((N, V), dtype=torch.bfloat16, device=dev)
+
+    def fwd_keep(red=0, temp=1.0):
+        _lib.check(lib.ts_flce_forward_keep(
+            P(h), H, P(w), H, P(labels), N, H, V, -100, red, 0.0, 0.0, temp, P(loss), P(rows),
+            P(lse), P(kept), P(wsf), ws_f, stream), "ts_flce_forward_keep")
+
+    def bwd_kept(red=0, temp=1.0, up=one, stride=0):
+        _lib.check(lib.ts_flce_backward_kept(
+            P(h), H, P(w), H, P(labels), N, H, V, -100, red, 0.0, 0.0, temp, P(lse), P(up),
+            stride, P(kept), P(gh), P(gw), P(wsk), ws_k, stream), "ts_flce_backward_kept")
+
+    def stored():
+        fwd_keep()
+        bwd_kept()
+
+    def rl_stored():
+        fwd_keep(red=2, temp=0.9)
+        bwd_kept(red=2, temp=0.9, up=up_rows, stride=1)
+
+    kept_what = (f"the forward also keeps the bf16 logits ({N * V * 2} bytes, as the "
+                 f"reference's chunked_log_softmax keeps its chunks' logits for autograd); the "
+                 f"backward forms dlogits over them and runs the two gradient GEMMs: three "
+                 f"GEMMs instead of four (opt-in)")
+    out["stored_logits"] = line(time_ms(stored, reps, warm), workspace_bytes=ws_f + ws_k,
+                                kept_logits_bytes=N * V * 2, what=kept_what)
+    out["rl_form_stored_logits"] = line(time_ms(rl_stored, reps, warm),
+                                        what="the RL form through the stored-logits schedule")
+    del wsf, wsk, kept
     torch.cuda.empty_cache()
     ms1, ws1 = one_call_timer(0, 0)
     out["one_chunk_schedule"] = line(

@@ -486,6 +486,42 @@ ts_status ts_flce_backward(const void* hidden, int64_t ldh, const void* weight, 
                            void* workspace, size_t workspace_bytes, ts_stream_t stream);
 
 /*
+ * ts_flce_forward that also writes the bf16 logits z = bf16(hidden @ weight^T)
+ * to `logits` ([N, V], row stride V, 16-byte aligned, N * V * 2 bytes of
+ * caller memory: 2.1 GB at N = 8192, V = 128256), for ts_flce_backward_kept.
+ * Everything else is bit-identical to ts_flce_forward's, and its workspace is
+ * the same. The reference's chunked_log_softmax keeps each chunk's
+ * [B, chunk, V] logits alive for autograd's backward (rl_training.py:175-189);
+ * this keeps one bf16 copy, so the backward need not recompute them.
+ */
+ts_status ts_flce_forward_keep(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                               const int64_t* labels, int64_t N, int64_t H, int64_t V,
+                               int64_t ignore_index, int32_t reduction,
+                               float softcap, float scale, float temperature,
+                               float* loss, float* loss_rows, float* lse, void* logits,
+                               void* workspace, size_t workspace_bytes, ts_stream_t stream);
+
+/*
+ * ts_flce_backward from the logits ts_flce_forward_keep kept, which it
+ * overwrites with dz (they are consumed: another backward needs
+ * ts_flce_backward). dz is bit-identical to what ts_flce_backward forms, and
+ * so is grad_weight; grad_hidden sums over all of V in one fp32 accumulation
+ * instead of one per vocabulary chunk (the order of the fp32 sums differs).
+ * Three GEMMs in all instead of four. Workspace:
+ * ts_flce_backward_kept_workspace_size(N) bytes. Replaces autograd's backward
+ * through chunked_log_softmax / selective_log_softmax (rl_training.py:95-191)
+ * and the lm_head matmul, as ts_flce_backward does.
+ */
+size_t ts_flce_backward_kept_workspace_size(int64_t N);
+ts_status ts_flce_backward_kept(const void* hidden, int64_t ldh, const void* weight, int64_t ldw,
+                                const int64_t* labels, int64_t N, int64_t H, int64_t V,
+                                int64_t ignore_index, int32_t reduction,
+                                float softcap, float scale, float temperature,
+                                const float* lse, const float* dloss, int64_t dloss_stride,
+                                void* logits, void* grad_hidden, void* grad_weight,
+                                void* workspace, size_t workspace_bytes, ts_stream_t stream);
+
+/*
  * x[i] *= *scale for n contiguous values of `dtype` (any n >= 0; 16-byte
  * vectors where x is 16-byte aligned, single elements for the rest); scale
  * is a device pointer, and when *scale == 1 nothing is written. Applies an upstream gradient other than 1

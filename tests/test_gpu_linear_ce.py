@@ -468,6 +468,86 @@ def test_chunked_log_softmax_drop_in(gpu):
     assert rel_fro(lm_head.grad, ref_gw.float()) <= 1e-2
 
 
+@pytest.mark.parametrize("xf,reduction", [({}, "mean"), ({}, "none"),
+                                          (dict(logit_softcapping=20.0, logit_scaling=0.5,
+                                                temperature=0.9), "none"),
+                                          (dict(temperature=0.7), "sum")])
+def test_stored_logits_equal_the_recompute(gpu, xf, reduction):
+    # ts_flce_forward_keep + ts_flce_backward_kept against the recomputing two-pass: the
+    # same statistics, the logits bf16(hidden @ weight.T), and the same dz; with one
+    # vocabulary chunk the recompute sums grad_hidden over all of V in one GEMM too, so
+    # both gradients are bit-identical
+    torch.manual_seed(31)
+    N, H, V = 1035, 296, 776
+    h = torch.randn(N, H, device=gpu).to(BF)
+    w = (0.1 * torch.randn(V, H, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::9] = -100
+    up = torch.randn(N, device=gpu) if reduction == "none" else torch.full((), 1.5, device=gpu)
+    loss0, rows0, lse0 = linear_ce_forward(h, w, labels, reduction=reduction, **xf)
+    loss1, rows1, lse1, logits = linear_ce_forward(h, w, labels, reduction=reduction,
+                                                   keep_logits=True, **xf)
+    assert torch.equal(rows0, rows1) and torch.equal(lse0, lse1)
+    if reduction != "none":
+        assert torch.equal(loss0, loss1)
+    # the kept logits: bf16(hidden @ weight.T) to a bf16 ulp (the fp32 sums are ordered
+    # differently from the CPU's; near 0 an absolute 1e-3 stands for that difference)
+    z = (h.float().cpu() @ w.float().cpu().t()).to(BF)
+    torch.testing.assert_close(logits.float().cpu(), z.float(), rtol=2 ** -7, atol=1e-3)
+    gh0, gw0 = linear_ce_backward(h, w, labels, lse0, up, reduction=reduction, vocab_chunk=V,
+                                  **xf)
+    gh1, gw1 = linear_ce_backward(h, w, labels, lse1, up, reduction=reduction, logits=logits,
+                                  **xf)
+    assert torch.equal(gh0, gh1) and torch.equal(gw0, gw1)
+    gh2, gw2 = linear_ce_backward(h, w, labels, lse0, up, reduction=reduction, vocab_chunk=256,
+                                  **xf)
+    assert torch.equal(gw2, gw1) and rel_fro(gh2, gh1) <= 4e-3
+    # and against the oracle (the recompute is pinned there already; this pins the pair)
+    _, ref_gh, ref_gw = oracle.linear_ce(h, w, labels, reduction=reduction, bf16_logits=True,
+                                         dloss=up.cpu(), **xf)
+    assert rel_fro(gh1, ref_gh.float()) <= 1e-2 and rel_fro(gw1, ref_gw.float()) <= 1e-2
+
+
+def test_stored_logits_module_and_rl(gpu):
+    torch.manual_seed(32)
+    B, L, H, V = 2, 67, 128, 1024
+    h = torch.randn(B, L, H, device=gpu).to(BF).requires_grad_()
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF).requires_grad_()
+    labels = torch.randint(0, V, (B, L), device=gpu)
+    labels[0, :5] = -100
+    grads = []
+    for schedule in ("two_pass", "stored_logits"):
+        h.grad = None
+        w.grad = None
+        rows = fused_linear_cross_entropy(h, w, labels, reduction="none", temperature=0.8,
+                                          schedule=schedule, vocab_chunk=V)
+        up = torch.linspace(-1.0, 1.0, B * L, device=gpu).reshape(B, L)
+        (rows * up).sum().backward(retain_graph=True)
+        g1 = (h.grad.clone(), w.grad.clone())
+        # a second backward through the same graph: the kept logits were consumed, so it
+        # recomputes (vocab_chunk=V: one chunk, bit-identical gradients); they accumulate
+        (rows * up).sum().backward()
+        grads.append((rows.detach(), g1, (h.grad.clone(), w.grad.clone())))
+    (r0, g0, a0), (r1, g1, a1) = grads
+    assert torch.equal(r0, r1)
+    assert torch.equal(g0[0], g1[0]) and torch.equal(g0[1], g1[1])
+    assert torch.equal(a0[0], a1[0]) and torch.equal(a0[1], a1[1])
+    # chunked_log_softmax with and without the kept logits
+    hs = torch.randn(B, L, H, device=gpu).to(BF).requires_grad_()
+    ids = torch.randint(0, V, (B, L), device=gpu)
+    out = []
+    for store in (False, True):
+        hs.grad = None
+        w.grad = None
+        lp = chunked_log_softmax(hs[:, :-1, :], w, ids[:, 1:], temperature=0.9,
+                                 store_logits=store)
+        (lp * torch.ones_like(lp)).sum().backward()
+        out.append((lp.detach(), hs.grad.clone(), w.grad.clone()))
+    assert torch.equal(out[0][0], out[1][0])
+    assert torch.equal(out[0][2], out[1][2])  # grad_weight: the same sums over tokens
+    assert rel_fro(out[1][1], out[0][1]) <= 4e-3  # grad_hidden: chunked vs one fp32 sum
+
+
 def test_two_pass_strided_rows(gpu):
     torch.manual_seed(25)
     N, H, V = 519, 72, 1032

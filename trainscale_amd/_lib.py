@@ -91,6 +91,11 @@ SIGNATURES = {
     "ts_flce_backward_workspace_size": ([I64, I64, I64, I64], SZ),
     "ts_flce_backward": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, F32, F32, F32, P, P, I64,
                           P, P, I64, P, SZ, P], I32),
+    "ts_flce_forward_keep": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, F32, F32, F32, P, P, P,
+                              P, P, SZ, P], I32),
+    "ts_flce_backward_kept_workspace_size": ([I64], SZ),
+    "ts_flce_backward_kept": ([P, I64, P, I64, P, I64, I64, I64, I64, I32, F32, F32, F32, P, P,
+                               I64, P, P, P, P, SZ, P], I32),
     "ts_scale_inplace": ([P, I64, I32, P, P], I32),
     "ts_swiglu_fwd": ([P, P, P, I64, I32, P], I32),
     "ts_swiglu_bwd": ([P, P, P, P, P, I64, I32, P], I32),

@@ -46,7 +46,8 @@ enum EpiMode : int {
   kEpiF32 = 2,        // fp32 C32 = acc
   kEpiAccF32 = 3,     // fp32 C32 += acc
   kEpiAccBf16 = 4,    // bf16 C = C32 + acc
-  kEpiStats = 5,      // row statistics of the transformed logits + the label's value; no C
+  kEpiStats = 5,      // row statistics of the transformed logits + the label's value (and,
+                      // when C is not NULL, the bf16 logits in C)
   kEpiDlogits = 6,    // bf16 C = dlogits of the transformed logits (lse known)
   kEpiAddBf16 = 7     // bf16 C = bf16(C + acc): a running sum kept in the bf16 output
 };
@@ -85,7 +86,7 @@ struct GemmArgs {
   const __bf16* B;
   int64_t ldb;
   int64_t M, N, K;
-  __bf16* C;      // bf16 output (modes 0, 1, 4)
+  __bf16* C;      // bf16 output (modes 0, 1, 4, 6, 7; optional in 5)
   int64_t ldc;
   float* C32;     // fp32 accumulator (modes 2, 3, 4)
   int64_t ldc32;
@@ -290,7 +291,9 @@ __device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) 
         if (in) st16(a.C + gm * a.ldc + gc, v);
       }
       if constexpr (kMode == kEpiStats) {
-        // statistics of t over the row's 128-column slice, and t at the label
+        // statistics of t over the row's 128-column slice, and t at the label; the
+        // logits themselves when the caller keeps them for the backward
+        if (in && a.C != nullptr) st16(a.C + gm * a.ldc + gc, v);
         float f[8];
         Elt<__bf16>::unpack(v, f);
         if (xf_on) {
@@ -611,6 +614,46 @@ __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int6
       st16_stream(row + v * 8, Elt<__bf16>::pack(g));
     }
   }
+}
+
+// dz of the logits a forward kept, in place over them: for row r and column j,
+//   dz = bf16(dscale[r] * (exp(t - lse[r]) - [j == labels[r]]) * dt/dz),  t = xf(z),
+// the arithmetic of the dlogits epilogue (kEpiDlogits) on the same bf16 z, so
+// the result is bit-identical to what the recomputing backward forms (ignored
+// rows have dscale 0 and give zeros of the same signs). Grid as flce_dlogits:
+// blockIdx.x = row * chunks + chunk, one 16-byte vector a thread.
+__global__ __launch_bounds__(256) void flce_dlogits_kept(__bf16* __restrict__ L, int64_t ldl,
+                                                         const float* __restrict__ lse,
+                                                         const int64_t* __restrict__ labels,
+                                                         int64_t V, int64_t chunks,
+                                                         const float* __restrict__ dscale,
+                                                         LogitXform xf) {
+  const int64_t r = (int64_t)blockIdx.x / chunks;
+  const int64_t v = ((int64_t)blockIdx.x % chunks) * 256 + threadIdx.x;
+  if (v >= V / 8) return;
+  __bf16* p = L + r * ldl + v * 8;
+  const float ds = dscale[r];
+  const u32x4 q = ld16_stream(p);
+  const float l2 = lse[r] * kLog2e;
+  const int64_t d = labels[r] - v * 8;  // the label's position in this vector, if in [0, 8)
+  float f[8], g[8];
+  Elt<__bf16>::unpack(q, f);
+  if (!xf.on()) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pr = fast_exp2(__builtin_fmaf(f[e], kLog2e, -l2));
+      g[e] = ds * (e == d ? pr - 1.f : pr);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float dt;
+      const float t = xf.apply_d(f[e], dt);
+      const float pr = fast_exp2(__builtin_fmaf(t, kLog2e, -l2));
+      g[e] = ds * (e == d ? pr - 1.f : pr) * dt;
+    }
+  }
+  st16_stream(p, Elt<__bf16>::pack(g));
 }
 
 __global__ __launch_bounds__(256) void fill_zero_u32(uint32_t* __restrict__ p, int64_t n,
@@ -1008,19 +1051,21 @@ extern "C" size_t ts_flce_forward_workspace_size(int64_t N, int64_t V) {
   return fwd_layout(N, V).total;
 }
 
-extern "C" ts_status ts_flce_forward(const void* hidden, int64_t ldh, const void* weight,
-                                     int64_t ldw, const int64_t* labels, int64_t N, int64_t H,
-                                     int64_t V, int64_t ignore_index, int32_t reduction,
-                                     float softcap, float scale, float temperature, float* loss,
-                                     float* loss_rows, float* lse, void* workspace,
-                                     size_t workspace_bytes, ts_stream_t stream) {
+namespace {
+
+// ts_flce_forward, and ts_flce_forward_keep when `logits` is not NULL.
+ts_status flce_forward_impl(const char* who, const void* hidden, int64_t ldh, const void* weight,
+                            int64_t ldw, const int64_t* labels, int64_t N, int64_t H, int64_t V,
+                            int64_t ignore_index, int32_t reduction, float softcap, float scale,
+                            float temperature, float* loss, float* loss_rows, float* lse,
+                            void* logits, void* workspace, size_t workspace_bytes,
+                            hipStream_t st) {
   using ts_host::fail;
   LogitXform xf{};
-  TS_TRY(check_two_pass("flce_forward", hidden, ldh, weight, ldw, labels, N, H, V, reduction,
-                        softcap, scale, temperature, &xf));
+  TS_TRY(check_two_pass(who, hidden, ldh, weight, ldw, labels, N, H, V, reduction, softcap, scale,
+                        temperature, &xf));
   if (reduction != 2 && loss == nullptr)
-    return fail(TS_ERR_INVALID_ARGUMENT, "flce_forward: loss is NULL");
-  hipStream_t st = static_cast<hipStream_t>(stream);
+    return fail(TS_ERR_INVALID_ARGUMENT, "%s: loss is NULL", who);
   if (N == 0) {
     if (loss == nullptr) return TS_OK;
     hipLaunchKernelGGL(fill_zero_u32, dim3(1), dim3(256), 0, st, nullptr, (int64_t)0, loss);
@@ -1028,8 +1073,8 @@ extern "C" ts_status ts_flce_forward(const void* hidden, int64_t ldh, const void
   }
   const FwdLayout lay = fwd_layout(N, V);
   if (workspace == nullptr || workspace_bytes < lay.total || !ts_host::aligned16(workspace))
-    return fail(TS_ERR_WORKSPACE, "flce_forward: workspace needs %zu bytes (16-byte aligned), "
-                "got %zu", lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
+    return fail(TS_ERR_WORKSPACE, "%s: workspace needs %zu bytes (16-byte aligned), got %zu", who,
+                lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   float2* stats = reinterpret_cast<float2*>(ws + lay.off_stats);
   float* zlab = reinterpret_cast<float*>(ws + lay.off_zlab);
@@ -1050,6 +1095,8 @@ extern "C" ts_status ts_flce_forward(const void* hidden, int64_t ldh, const void
   g.label_offset = 0;
   g.zlab = zlab;
   g.xf = xf;
+  g.C = static_cast<__bf16*>(logits);  // NULL: the statistics only
+  g.ldc = V;
   TS_TRY(launch_gemm<kEpiStats>(g, st, "flce_gemm_stats"));
   hipLaunchKernelGGL(flce_rows_t, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, stats,
                      lay.nparts, zlab, labels, N, V, ignore_index, lse_ws, rows_ws);
@@ -1060,6 +1107,35 @@ extern "C" ts_status ts_flce_forward(const void* hidden, int64_t ldh, const void
   hipLaunchKernelGGL(flce_loss, dim3(1), dim3(256), 0, st, rows_ws, N, n_valid,
                      reduction == 0 ? 1 : 0, loss, sc);
   return ts_host::check_launch("flce_loss");
+}
+
+}  // namespace
+
+extern "C" ts_status ts_flce_forward(const void* hidden, int64_t ldh, const void* weight,
+                                     int64_t ldw, const int64_t* labels, int64_t N, int64_t H,
+                                     int64_t V, int64_t ignore_index, int32_t reduction,
+                                     float softcap, float scale, float temperature, float* loss,
+                                     float* loss_rows, float* lse, void* workspace,
+                                     size_t workspace_bytes, ts_stream_t stream) {
+  return flce_forward_impl("flce_forward", hidden, ldh, weight, ldw, labels, N, H, V,
+                           ignore_index, reduction, softcap, scale, temperature, loss, loss_rows,
+                           lse, nullptr, workspace, workspace_bytes,
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" ts_status ts_flce_forward_keep(const void* hidden, int64_t ldh, const void* weight,
+                                          int64_t ldw, const int64_t* labels, int64_t N,
+                                          int64_t H, int64_t V, int64_t ignore_index,
+                                          int32_t reduction, float softcap, float scale,
+                                          float temperature, float* loss, float* loss_rows,
+                                          float* lse, void* logits, void* workspace,
+                                          size_t workspace_bytes, ts_stream_t stream) {
+  if (N > 0 && (logits == nullptr || !ts_host::aligned16(logits)))
+    return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "flce_forward_keep: logits NULL or unaligned");
+  return flce_forward_impl("flce_forward_keep", hidden, ldh, weight, ldw, labels, N, H, V,
+                           ignore_index, reduction, softcap, scale, temperature, loss, loss_rows,
+                           lse, logits, workspace, workspace_bytes,
+                           static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t ts_flce_backward_workspace_size(int64_t N, int64_t H, int64_t V,
@@ -1178,6 +1254,119 @@ extern "C" ts_status ts_flce_backward(const void* hidden, int64_t ldh, const voi
     }
   }
   return TS_OK;
+}
+
+// The backward from logits the forward kept (ts_flce_forward_keep): dz in place
+// over them, then the two gradient GEMMs in one grid, as the one-call schedule
+// runs them. Workspace: the per-row upstream gradients and the valid count.
+namespace {
+
+struct KeptLayout {
+  size_t off_dscale, off_misc, total;
+};
+
+KeptLayout kept_layout(int64_t N) {
+  KeptLayout l{};
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += (bytes + 255) / 256 * 256;
+    return o;
+  };
+  l.off_dscale = take((size_t)N * 4);
+  l.off_misc = take(64);
+  l.total = off;
+  return l;
+}
+
+}  // namespace
+
+extern "C" size_t ts_flce_backward_kept_workspace_size(int64_t N) {
+  if (N <= 0) return 0;
+  return kept_layout(N).total;
+}
+
+extern "C" ts_status ts_flce_backward_kept(const void* hidden, int64_t ldh, const void* weight,
+                                           int64_t ldw, const int64_t* labels, int64_t N,
+                                           int64_t H, int64_t V, int64_t ignore_index,
+                                           int32_t reduction, float softcap, float scale,
+                                           float temperature, const float* lse,
+                                           const float* dloss, int64_t dloss_stride,
+                                           void* logits, void* grad_hidden, void* grad_weight,
+                                           void* workspace, size_t workspace_bytes,
+                                           ts_stream_t stream) {
+  using ts_host::fail;
+  LogitXform xf{};
+  TS_TRY(check_two_pass("flce_backward_kept", hidden, ldh, weight, ldw, labels, N, H, V,
+                        reduction, softcap, scale, temperature, &xf));
+  if (dloss_stride < 0)
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_backward_kept: dloss_stride must be >= 0");
+  if (N > 0 && (lse == nullptr || dloss == nullptr || logits == nullptr))
+    return fail(TS_ERR_INVALID_ARGUMENT, "flce_backward_kept: lse, dloss or logits is NULL");
+  if ((logits != nullptr && !ts_host::aligned16(logits)) ||
+      (grad_hidden != nullptr && !ts_host::aligned16(grad_hidden)) ||
+      (grad_weight != nullptr && !ts_host::aligned16(grad_weight)))
+    return fail(TS_ERR_INVALID_ARGUMENT,
+                "flce_backward_kept: logits and gradients must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (N == 0) {
+    // no rows: grad_weight is 0 (grad_hidden is empty)
+    if (grad_weight == nullptr) return TS_OK;
+    const int64_t words = V * H / 2;
+    hipLaunchKernelGGL(fill_zero_u32, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st,
+                       static_cast<uint32_t*>(grad_weight), words, nullptr);
+    return ts_host::check_launch("fill_zero_u32");
+  }
+  if (grad_hidden == nullptr && grad_weight == nullptr) return TS_OK;
+  const int64_t dchunks = (V / 8 + 255) / 256;
+  if (N * dchunks > 0x7fffffffLL)
+    return fail(TS_ERR_SHAPE, "flce_backward_kept: too many rows for the dz grid");
+  const KeptLayout lay = kept_layout(N);
+  if (workspace == nullptr || workspace_bytes < lay.total || !ts_host::aligned16(workspace))
+    return fail(TS_ERR_WORKSPACE,
+                "flce_backward_kept: workspace needs %zu bytes (16-byte aligned), got %zu",
+                lay.total, workspace == nullptr ? (size_t)0 : workspace_bytes);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float* dscale = reinterpret_cast<float*>(ws + lay.off_dscale);
+  int* n_valid = reinterpret_cast<int*>(ws + lay.off_misc);
+  __bf16* L = static_cast<__bf16*>(logits);
+
+  hipLaunchKernelGGL(flce_count, dim3(1), dim3(256), 0, st, labels, N, ignore_index, n_valid);
+  TS_TRY(ts_host::check_launch("flce_count"));
+  hipLaunchKernelGGL(flce_dscale, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, labels, N,
+                     ignore_index, dloss, dloss_stride, n_valid, reduction == 0 ? 1 : 0, dscale);
+  TS_TRY(ts_host::check_launch("flce_dscale"));
+  hipLaunchKernelGGL(flce_dlogits_kept, dim3((unsigned)(N * dchunks)), dim3(256), 0, st, L, V,
+                     lse, labels, V, dchunks, dscale, xf);
+  TS_TRY(ts_host::check_launch("flce_dlogits_kept"));
+  using ts_gemm::kKMajor;
+  using ts_gemm::kMNMajor;
+  GemmArgs dh{};
+  dh.A = L;  // dz [N, V], K-major
+  dh.lda = V;
+  dh.B = static_cast<const __bf16*>(weight);  // weight [V, H] as the [H, V] operand: MN-major
+  dh.ldb = ldw;
+  dh.M = N;
+  dh.N = H;
+  dh.K = V;
+  dh.C = static_cast<__bf16*>(grad_hidden);
+  dh.ldc = H;
+  GemmArgs dw{};
+  dw.A = L;  // dz [N, V] as the [V, N] operand: MN-major
+  dw.lda = V;
+  dw.B = static_cast<const __bf16*>(hidden);  // hidden [N, H] as the [H, N] operand: MN-major
+  dw.ldb = ldh;
+  dw.M = V;
+  dw.N = H;
+  dw.K = N;
+  dw.C = static_cast<__bf16*>(grad_weight);
+  dw.ldc = H;
+  if (grad_hidden != nullptr && grad_weight != nullptr)
+    return launch_gemm_pair<kEpiBf16, kKMajor, kMNMajor, kEpiBf16, kMNMajor, kMNMajor>(
+        dh, dw, st, "flce_gemm_grads_kept");
+  if (grad_hidden != nullptr)
+    return launch_gemm<kEpiBf16, kKMajor, kMNMajor>(dh, st, "flce_gemm_dhidden_kept");
+  return launch_gemm<kEpiBf16, kMNMajor, kMNMajor>(dw, st, "flce_gemm_dweight_kept");
 }
 
 // ---------------------------------------------------------------------------

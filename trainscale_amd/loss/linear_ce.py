@@ -22,6 +22,12 @@ Two schedules run on the gfx950 kernels:
   only [rows, V] scratch, with grad_weight summed over the chunks in its bf16
   output (as autograd sums the reference's per-chunk bf16 gradients); the
   backward scales the gradients in place. Three GEMMs instead of four.
+* ``"stored_logits"`` (opt-in; any reduction and transform): the two-pass
+  forward also keeps the bf16 logits ([N, V], N * V * 2 bytes, as the
+  reference's chunked_log_softmax keeps each chunk's logits for autograd);
+  the backward forms dlogits over them in place and runs the two gradient
+  GEMMs, three GEMMs in all instead of four. The kept logits are consumed: a
+  second backward recomputes, as "two_pass" does.
 * ``"auto"`` (the default): "fused" when gradients are needed for mean/sum
   without transforms, "two_pass" otherwise (forward only, reduction "none",
   transforms).
@@ -87,10 +93,12 @@ def _ld(t: Tensor) -> int:
 
 def linear_ce_forward(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
                       reduction: str = "mean", logit_softcapping: float = 0.0,
-                      logit_scaling: float = 0.0, temperature: float = 1.0):
+                      logit_scaling: float = 0.0, temperature: float = 1.0,
+                      keep_logits: bool = False):
     """ts_flce_forward: returns (loss fp32 0-d or None for reduction "none",
     loss_rows fp32 [N], lse fp32 [N]). lse is that of the transformed logits and
-    is what linear_ce_backward needs."""
+    is what linear_ce_backward needs. With keep_logits (ts_flce_forward_keep) a
+    fourth value, the bf16 logits [N, V], for linear_ce_backward(logits=...)."""
     if reduction not in _REDUCTIONS_2P:
         raise ValueError(f"fused_linear_cross_entropy: reduction must be 'mean', 'sum' or "
                          f"'none', got {reduction!r}")
@@ -103,24 +111,33 @@ def linear_ce_forward(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_ind
     lib = _lib.load()
     ws_bytes = int(lib.ts_flce_forward_workspace_size(N, V))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
-        check(lib.ts_flce_forward(
-            ptr(hidden), _ld(hidden), ptr(weight), _ld(weight), ptr(labels), N, H, V,
+    args = (ptr(hidden), _ld(hidden), ptr(weight), _ld(weight), ptr(labels), N, H, V,
             int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
-            float(logit_scaling), float(temperature), ptr(loss), ptr(rows), ptr(lse), ptr(ws),
-            ws_bytes, _lib.stream_handle(dev)), "ts_flce_forward")
-    return loss, rows, lse
+            float(logit_scaling), float(temperature), ptr(loss), ptr(rows), ptr(lse))
+    if not keep_logits:
+        with torch.cuda.device(dev):
+            check(lib.ts_flce_forward(*args, ptr(ws), ws_bytes, _lib.stream_handle(dev)),
+                  "ts_flce_forward")
+        return loss, rows, lse
+    logits = torch.empty((N, V), dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        check(lib.ts_flce_forward_keep(*args, ptr(logits), ptr(ws), ws_bytes,
+                                       _lib.stream_handle(dev)), "ts_flce_forward_keep")
+    return loss, rows, lse, logits
 
 
 def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tensor,
                        dloss: Tensor, ignore_index: int = -100, reduction: str = "mean",
                        logit_softcapping: float = 0.0, logit_scaling: float = 0.0,
                        temperature: float = 1.0, need_grad_hidden: bool = True,
-                       need_grad_weight: bool = True, vocab_chunk: Optional[int] = None):
+                       need_grad_weight: bool = True, vocab_chunk: Optional[int] = None,
+                       logits: Optional[Tensor] = None):
     """ts_flce_backward: (grad_hidden [N, H] or None, grad_weight [V, H] or None) for the
     upstream gradient dloss (one value for mean/sum, or [N] per-row values for "none";
     a single value broadcasts). vocab_chunk: columns per recomputed chunk (default
-    about V/8)."""
+    about V/8). With `logits`, the [N, V] bf16 logits linear_ce_forward kept
+    (keep_logits), ts_flce_backward_kept forms the gradients from them instead of
+    recomputing, and overwrites them."""
     if reduction not in _REDUCTIONS_2P:
         raise ValueError(f"fused_linear_cross_entropy: bad reduction {reduction!r}")
     dev, hidden, weight, labels = _operands("fused_linear_cross_entropy", hidden, weight, labels)
@@ -134,8 +151,23 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
     lse = lse.detach().to(torch.float32).reshape(-1).contiguous()
     gh = torch.empty((N, H), dtype=torch.bfloat16, device=dev) if need_grad_hidden else None
     gw = torch.empty((V, H), dtype=torch.bfloat16, device=dev) if need_grad_weight else None
-    chunk = int(vocab_chunk) if vocab_chunk else 0
     lib = _lib.load()
+    if logits is not None:
+        if (logits.shape != (N, V) or logits.dtype != torch.bfloat16 or logits.device != dev or
+                not logits.is_contiguous()):
+            raise ValueError(f"fused_linear_cross_entropy: kept logits must be contiguous bf16 "
+                             f"[{N}, {V}] on {dev}")
+        ws_bytes = int(lib.ts_flce_backward_kept_workspace_size(N))
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            check(lib.ts_flce_backward_kept(
+                ptr(hidden), _ld(hidden), ptr(weight), _ld(weight), ptr(labels), N, H, V,
+                int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
+                float(logit_scaling), float(temperature), ptr(lse), ptr(dloss), stride,
+                ptr(logits), ptr(gh), ptr(gw), ptr(ws), ws_bytes, _lib.stream_handle(dev)),
+                "ts_flce_backward_kept")
+        return gh, gw
+    chunk = int(vocab_chunk) if vocab_chunk else 0
     ws_bytes = int(lib.ts_flce_backward_workspace_size(N, H, V, chunk))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
@@ -304,18 +336,26 @@ def _scale_(t: Optional[Tensor], scale: Tensor) -> None:
 class LinearCrossEntropyFunction(torch.autograd.Function):
     """loss = CE(t(hidden @ weight.T), labels), two-pass schedule: the forward keeps
     per-row statistics only, the backward recomputes the logits by vocabulary chunk.
-    Returns the reduced loss, or the per-row losses [N] for reduction "none" (0 on
-    ignore_index rows). Calling backward twice (retain_graph) recomputes again."""
+    With keep_logits the forward also keeps the bf16 logits and the first backward
+    forms the gradients from them (consuming them). Returns the reduced loss, or the
+    per-row losses [N] for reduction "none" (0 on ignore_index rows). Calling
+    backward again (retain_graph) recomputes."""
 
     @staticmethod
     def forward(ctx, hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,
                 reduction: str = "mean", logit_softcapping: float = 0.0,
                 logit_scaling: float = 0.0, temperature: float = 1.0,
-                vocab_chunk: Optional[int] = None) -> Tensor:
+                vocab_chunk: Optional[int] = None, keep_logits: bool = False) -> Tensor:
         shape = hidden.shape
         h2 = hidden.reshape(-1, shape[-1])
-        loss, rows, lse = linear_ce_forward(h2, weight, labels, ignore_index, reduction,
-                                            logit_softcapping, logit_scaling, temperature)
+        # kept only when a backward can consume them (forward runs without grad mode,
+        # so needs_input_grad says whether this call is recorded for one)
+        keep = keep_logits and (ctx.needs_input_grad[0] or ctx.needs_input_grad[1])
+        out = linear_ce_forward(h2, weight, labels, ignore_index, reduction, logit_softcapping,
+                                logit_scaling, temperature, keep_logits=keep)
+        loss, rows, lse = out[:3]
+        # the kept logits are not a saved tensor: the first backward overwrites them
+        ctx.logits = out[3] if keep else None
         ctx.cfg = (ignore_index, reduction, logit_softcapping, logit_scaling, temperature,
                    vocab_chunk)
         ctx.hidden_shape = shape
@@ -326,11 +366,13 @@ class LinearCrossEntropyFunction(torch.autograd.Function):
     def backward(ctx, grad_output: Tensor):
         h2, weight, labels, lse = ctx.saved_tensors
         ignore_index, reduction, cap, sc, temp, chunk = ctx.cfg
+        logits, ctx.logits = ctx.logits, None
         gh, gw = linear_ce_backward(h2, weight, labels, lse, grad_output, ignore_index, reduction,
                                     cap, sc, temp, need_grad_hidden=ctx.needs_input_grad[0],
-                                    need_grad_weight=ctx.needs_input_grad[1], vocab_chunk=chunk)
+                                    need_grad_weight=ctx.needs_input_grad[1], vocab_chunk=chunk,
+                                    logits=logits)
         gh = gh.view(ctx.hidden_shape) if gh is not None else None
-        return gh, gw, None, None, None, None, None, None, None
+        return gh, gw, None, None, None, None, None, None, None, None
 
 
 class FusedLinearCrossEntropyFunction(torch.autograd.Function):
@@ -384,12 +426,13 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
     t / temperature. reduction "mean" (over non-ignored rows), "sum", or "none"
     (per-row losses, shaped like labels).
 
-    schedule: "auto" (default), "fused" or "two_pass" (module docstring).
-    "fused": chunk_tokens rows per token chunk (None: a quarter of the tokens,
-    0: one chunk, i.e. all [N, V] logits), grad_weight_accum "bf16" (summed in
-    the bf16 output) or "fp32" (a V x H fp32 workspace); a second backward
-    through its graph raises. "two_pass": vocab_chunk columns per recomputed
-    chunk (None: about V/8).
+    schedule: "auto" (default), "fused", "two_pass" or "stored_logits" (module
+    docstring). "fused": chunk_tokens rows per token chunk (None: a quarter of
+    the tokens, 0: one chunk, i.e. all [N, V] logits), grad_weight_accum "bf16"
+    (summed in the bf16 output) or "fp32" (a V x H fp32 workspace); a second
+    backward through its graph raises. "two_pass": vocab_chunk columns per
+    recomputed chunk (None: about V/8). "stored_logits": the two-pass schedule
+    with the bf16 logits kept from the forward to the backward (N * V * 2 bytes).
     """
     if schedule == "auto":
         grads = torch.is_grad_enabled() and (hidden.requires_grad or weight.requires_grad)
@@ -404,11 +447,12 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
                              "transforms; use schedule 'two_pass'")
         return FusedLinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index,
                                                      reduction, chunk_tokens, grad_weight_accum)
-    if schedule != "two_pass":
+    if schedule not in ("two_pass", "stored_logits"):
         raise ValueError(f"fused_linear_cross_entropy: unknown schedule {schedule!r}")
     out = LinearCrossEntropyFunction.apply(hidden, weight, labels, ignore_index, reduction,
                                            float(logit_softcapping), float(logit_scaling),
-                                           float(temperature), vocab_chunk)
+                                           float(temperature), vocab_chunk,
+                                           schedule == "stored_logits")
     if reduction == "none":
         out = out.view(labels.shape)
     return out
@@ -416,18 +460,21 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
 
 def chunked_log_softmax(hidden_states: Tensor, lm_head: Tensor, input_ids: Tensor,
                         num_chunks: int = 4, temperature: float = 1.0,
-                        logit_softcapping: float = 0.0, logit_scale: float = 0.0) -> Tensor:
+                        logit_softcapping: float = 0.0, logit_scale: float = 0.0,
+                        store_logits: bool = False) -> Tensor:
     """Drop-in for chunked_log_softmax (rl_training.py:138-191): log-probabilities
     [B, L] of input_ids under the transformed logits of hidden_states [B, L, H] @
     lm_head[V, H].T, differentiable in hidden_states and lm_head.
 
     The reference splits the sequence into num_chunks and materialises each
-    chunk's [B, chunk, V] logits; here the logits are never stored (the two-pass
-    schedule), so num_chunks is accepted for the signature and unused.
+    chunk's [B, chunk, V] logits, which autograd keeps for the backward. Here
+    the logits are never stored (the two-pass schedule), so num_chunks is
+    accepted for the signature and unused; store_logits=True keeps one bf16
+    copy of them ([B * L, V]) so the backward skips their recompute.
     """
     del num_chunks
     rows = fused_linear_cross_entropy(hidden_states, lm_head, input_ids, ignore_index=-(1 << 62),
                                       reduction="none", logit_softcapping=logit_softcapping,
                                       logit_scaling=logit_scale, temperature=temperature,
-                                      schedule="two_pass")
+                                      schedule="stored_logits" if store_logits else "two_pass")
     return -rows
