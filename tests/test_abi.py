@@ -286,3 +286,30 @@ def test_flce_two_pass_validation(lib):
     assert bwd(gh=ctypes.c_void_p(0x1008)) == INVALID   # unaligned
     assert bwd(wsb=wb - 256) == WORKSPACE
     assert bwd(gh=NULL, gw=NULL) == TS_OK   # no gradient requested: nothing launched
+
+    # the stored-logits pair: the forward's checks plus the logits buffer
+    def fwd_keep(logits=FAKE, red=0, temp=1.0, wsb=wf, n=N):
+        return lib.ts_flce_forward_keep(FAKE, H, FAKE, H, FAKE, n, H, V, -100, red, 0.0, 0.0,
+                                        temp, FAKE, NULL, NULL, logits, FAKE, wsb, st)
+
+    assert fwd_keep(logits=NULL) == INVALID
+    assert fwd_keep(logits=ctypes.c_void_p(0x1008)) == INVALID  # unaligned
+    assert fwd_keep(red=3) == INVALID
+    assert fwd_keep(temp=0.0) == INVALID
+    assert fwd_keep(wsb=wf - 256) == WORKSPACE
+    wk = lib.ts_flce_backward_kept_workspace_size(N)
+    assert wk >= N * 4 and lib.ts_flce_backward_kept_workspace_size(0) == 0
+
+    def bwd_kept(logits=FAKE, lse=FAKE, dloss=FAKE, dl_stride=0, wsb=wk, gh=FAKE, gw=FAKE):
+        return lib.ts_flce_backward_kept(FAKE, H, FAKE, H, FAKE, N, H, V, -100, 2, 0.0, 0.0,
+                                         1.0, lse, dloss, dl_stride, logits, gh, gw, FAKE, wsb,
+                                         st)
+
+    assert bwd_kept(logits=NULL) == INVALID
+    assert bwd_kept(logits=ctypes.c_void_p(0x1008)) == INVALID
+    assert bwd_kept(lse=NULL) == INVALID
+    assert bwd_kept(dloss=NULL) == INVALID
+    assert bwd_kept(dl_stride=-1) == INVALID
+    assert bwd_kept(gw=ctypes.c_void_p(0x1008)) == INVALID
+    assert bwd_kept(wsb=wk - 256) == WORKSPACE
+    assert bwd_kept(gh=NULL, gw=NULL) == TS_OK
