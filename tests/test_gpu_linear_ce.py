@@ -255,10 +255,21 @@ def _check_c5(h, w, labels, loss, rows, gh, gw):
 
 
 def test_c5_full(gpu):
-    """C5 at full size through the default (two-pass, vocabulary-chunked) schedule:
+    """C5 at full size through the schedule fused_linear_cross_entropy picks for it by
+    default (auto: the one-call schedule in token chunks of a quarter of the tokens,
+    grad_weight summed in its bf16 output), the configuration of bench.py's C5 line:
     sampled rows against the CPU oracle, the loss, grad_hidden and 64 grad_weight rows
     spread over the vocabulary against an independent composition on the GPU (torch
     bf16 matmul + fp32 softmax)."""
+    wl = workloads.linear_ce_workload(gpu)
+    h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
+    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels, chunk_tokens=None,
+                                                         grad_weight_accum="bf16")
+    _check_c5(h, w, labels, loss, rows, gh, gw)
+
+
+def test_c5_full_two_pass(gpu):
+    """C5 through the two-pass schedule (vocabulary-chunked recompute)."""
     wl = workloads.linear_ce_workload(gpu)
     h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
     loss, rows, lse = linear_ce_forward(h, w, labels)
@@ -268,12 +279,27 @@ def test_c5_full(gpu):
 
 @pytest.mark.parametrize("chunk", [None, 0])
 def test_c5_full_fused_schedule(gpu, chunk):
-    """C5 through the one-call schedule: its default token chunk (a quarter of the
-    tokens, grad_weight summed in fp32 over the chunks) and one chunk (opt-in)."""
+    """C5 through the one-call schedule with grad_weight summed in fp32 (opt-in), at the
+    default token chunk (a quarter of the tokens) and in one chunk (opt-in)."""
     wl = workloads.linear_ce_workload(gpu)
     h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
-    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels, chunk_tokens=chunk)
+    loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels, chunk_tokens=chunk,
+                                                         grad_weight_accum="fp32")
     _check_c5(h, w, labels, loss, rows, gh, gw)
+
+
+def test_c5_full_stored_logits(gpu):
+    """C5 through the stored-logits schedule, and bit for bit against the recomputing
+    backward in one vocabulary chunk (the same dz and the same two GEMMs)."""
+    wl = workloads.linear_ce_workload(gpu)
+    h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
+    loss, rows, lse, logits = linear_ce_forward(h, w, labels, keep_logits=True)
+    one = torch.ones((), device=gpu)
+    gh, gw = linear_ce_backward(h, w, labels, lse, one, logits=logits)
+    del logits
+    _check_c5(h, w, labels, loss, rows, gh, gw)
+    gh0, gw0 = linear_ce_backward(h, w, labels, lse, one, vocab_chunk=w.shape[0])
+    assert torch.equal(gh0, gh) and torch.equal(gw0, gw)
 
 
 # ---------------------------------------------------------------------------
