@@ -133,7 +133,10 @@ ts_status ts_rmsnorm_bwd(const void* dy, int64_t lddy,
  * TS_ERR_WORKSPACE before launching anything. Every call on one device
  * shares that device's scratch, so calls that overlap on one device (two
  * streams, or two threads) race; calls in one stream are ordered. The
- * device of `stream` must be the current device.
+ * device of `stream` must be the current device. The first call on a device
+ * looks the scratch array's address up there (hipGetSymbolAddress); a caller
+ * that captures the call in a graph makes one call on that device outside the
+ * capture first (torch.cuda.graph's warm-up is such a call).
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).
@@ -410,7 +413,9 @@ size_t ts_flce_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk,
  * chunk's bf16 logits are the only [rows, V] scratch. Per chunk the two
  * gradient GEMMs run as one grid. grad_weight sums over the chunks in fp32 in
  * the workspace (rounded once), or with flags & TS_FLCE_ACCUM_BF16 in the
- * bf16 output (no V x H workspace). flags: 0 or TS_FLCE_ACCUM_BF16.
+ * bf16 output (no V x H workspace). flags: the value given to
+ * ts_flce_workspace_size (TS_FLCE_GRADS is accepted and ignored here: the
+ * gradient pointers decide whether gradients are formed).
  * Has no counterpart in the reference, which has no fused linear-CE; it
  * replaces the composition logits = hidden @ lm_head.t() (rl_training.py:177,
  * chunked_log_softmax :138-191) followed by cross-entropy

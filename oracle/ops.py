@@ -25,6 +25,7 @@ __all__ = [
     "ce_bwd",
     "linear_ce",
     "rl_logit_xform",
+    "selective_log_softmax",
     "vocab_parallel_ce",
     "swiglu_fwd",
     "swiglu_bwd",
@@ -312,6 +313,23 @@ def rl_logit_xform(z32: Tensor, logit_softcapping: float = 0.0, logit_scale: flo
         t = t / temperature
         d = d / temperature
     return t, d
+
+
+def selective_log_softmax(logits: Tensor, input_ids: Tensor, temperature: float = 1.0,
+                          logit_softcapping: float = 0.0, logit_scale: float = 0.0) -> Tensor:
+    """fp32 log-probabilities of input_ids [...] under logits [..., V].
+
+    Restates selective_log_softmax (rl_training.py:95-135): softcapping, then
+    scaling, then temperature (:114-122), a max-shifted log-softmax (:127-130) and
+    a gather at input_ids (:133-134). The reference computes in the logits'
+    dtype; this restatement computes in fp32.
+    """
+    logits, ids = _cpu(logits), _cpu(input_ids).to(torch.int64)
+    t, _ = rl_logit_xform(logits.float(), logit_softcapping, logit_scale, temperature)
+    m = t.max(dim=-1, keepdim=True).values
+    shifted = t - m
+    lp = shifted - torch.log(torch.exp(shifted).sum(dim=-1, keepdim=True))
+    return torch.gather(lp, -1, ids.unsqueeze(-1)).squeeze(-1)
 
 
 def linear_ce(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_index: int = -100,

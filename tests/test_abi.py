@@ -243,6 +243,11 @@ def test_flce_validation(lib):
     assert call(hidden=NULL) == INVALID
     assert call(wsb=ws - 256) == WORKSPACE
     assert call(flags=4) == INVALID
+    # the flags given to ts_flce_workspace_size are accepted (TS_FLCE_GRADS is ignored
+    # here): these calls pass the flag check and stop at the missing workspace
+    for flags in (1, 2, 3):
+        assert call(flags=flags, wsb=0) == WORKSPACE, flags
+    assert call(flags=5, wsb=0) == INVALID
     # bf16 accumulation needs no V x H fp32 sum: smaller than fp32 accumulation over chunks
     assert lib.ts_flce_workspace_size(1024, 256, 4096, 256, 3) + 4096 * 256 * 4 == \
         lib.ts_flce_workspace_size(1024, 256, 4096, 256, 1)
@@ -313,3 +318,16 @@ def test_flce_two_pass_validation(lib):
     assert bwd_kept(gw=ctypes.c_void_p(0x1008)) == INVALID
     assert bwd_kept(wsb=wk - 256) == WORKSPACE
     assert bwd_kept(gh=NULL, gw=NULL) == TS_OK
+
+
+def test_noalloc_rejects_shapes_beyond_the_scratch(lib):
+    """ts_rmsnorm_bwd_noalloc refuses partials above its 16 MiB device scratch before any
+    HIP call (so these made-up pointers are never used)."""
+    cap = int(lib.ts_rmsnorm_bwd_noalloc_max_bytes())
+    assert cap == 16 << 20
+    rows, cols = 65536, 65536  # the generic path's partials: rows / 64 x cols x 4 bytes
+    assert int(lib.ts_rmsnorm_bwd_workspace_size(rows, cols)) > cap
+    status = lib.ts_rmsnorm_bwd_noalloc(FAKE, cols, FAKE, cols, _lib.TS_BF16, FAKE, _lib.TS_BF16,
+                                        FAKE, FAKE, cols, FAKE, rows, cols, NULL)
+    assert status == WORKSPACE
+    assert b"device scratch" in lib.ts_last_error()

@@ -505,3 +505,41 @@ def test_c3_full_schedule_b_equals_schedule_a_on_every_row(gpu):
         rs = gv.sum(-1).abs()
         bound = gv.abs().sum(-1) * 2.0 ** -8
         assert bool((rs <= bound).all()), float((rs / bound).max())
+
+
+def test_c3_full_gradient_every_row_against_fp32_softmax(gpu):
+    """Both schedules' gradients on all 16384 rows of C3 against the oracle's arithmetic
+    (oracle.ce_bwd: fp32 softmax of the bf16 logits minus the one-hot, times the upstream
+    gradient, rounded once to bf16) evaluated with torch on the GPU, 1024 rows at a time:
+    within 1 bf16 ulp on every element. Both roundings start from fp32 values a few fp32
+    ulps apart, so they land at most one bf16 ulp apart."""
+    wl = workloads.ce_workload(gpu)
+    logits, labels = wl.tensors["logits"], wl.tensors["labels"]
+    N, V = logits.shape
+    valid = labels != -100
+    n_valid = int(valid.sum())
+    dl = torch.tensor([1.0 / n_valid], device=gpu)
+    _, _, grad_b = ops.ce_forward_backward(logits, V, labels, dl)
+    _, lse_a = ops.ce_forward(logits, V, labels)
+    grad_a = torch.empty_like(logits)
+    ops.ce_backward(logits, V, labels, lse_a, dl, grad_a, V)
+
+    def ordered(t):
+        u = t.contiguous().view(torch.int16).int() & 0xFFFF
+        return torch.where(u < 0x8000, u, 0x8000 - u)
+
+    worst = {"B": 0, "A": 0}
+    for s in range(0, N, 1024):
+        e = min(s + 1024, N)
+        p = torch.softmax(logits[s:e].float(), dim=1)
+        vc = valid[s:e]
+        rows = torch.arange(e - s, device=gpu)
+        p[rows[vc], labels[s:e][vc]] -= 1.0
+        p[~vc] = 0.0
+        ref = (p * dl).to(BF)
+        for name, g in (("B", grad_b), ("A", grad_a)):
+            d = (ordered(g[s:e]) - ordered(ref)).abs()
+            tiny = (g[s:e].float() - ref.float()).abs() <= TINY
+            d = torch.where(tiny, torch.zeros_like(d), d)
+            worst[name] = max(worst[name], int(d.max()))
+    assert worst["B"] <= 1 and worst["A"] <= 1, worst

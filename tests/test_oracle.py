@@ -325,6 +325,46 @@ def test_linear_ce_rl_mutations_fail_golden():
     assert np.abs(gh_bad.double().numpy() - g["grad_hidden"]).max() > 1e-3
 
 
+def test_selective_log_softmax_matches_golden():
+    """selective_log_softmax on the golden RL case's logits (float64 h @ w.T handed over
+    in fp32): the log-probs are minus the golden per-token losses."""
+    g, h, w, labels, dloss, kw = _rl_case()
+    z = torch.from_numpy(g["hidden"]).double() @ torch.from_numpy(g["weight"]).double().t()
+    valid = labels != -100
+    lp = oracle.selective_log_softmax(z.float(), labels.clamp(min=0),
+                                      temperature=kw["temperature"],
+                                      logit_softcapping=kw["logit_softcapping"],
+                                      logit_scale=kw["logit_scaling"])
+    np.testing.assert_allclose(lp[valid].double().numpy(), -g["loss_rows"][valid.numpy()],
+                               rtol=2e-6, atol=2e-6)
+    # mutation: scale before the softcap misses the golden values
+    bad = oracle.selective_log_softmax(z.float() * kw["logit_scaling"], labels.clamp(min=0),
+                                       temperature=kw["temperature"],
+                                       logit_softcapping=kw["logit_softcapping"])
+    assert np.abs(bad[valid].double().numpy() + g["loss_rows"][valid.numpy()]).max() > 1e-3
+
+
+def test_selective_log_softmax_matches_autograd_float64():
+    """The log-probs and their gradient against torch's float64 log_softmax of the
+    transformed logits (a separate formulation: F.log_softmax, autograd)."""
+    torch.manual_seed(3)
+    z = 3 * torch.randn(5, 7, 300)
+    ids = torch.randint(0, 300, (5, 7))
+    kw = dict(temperature=0.8, logit_softcapping=4.0, logit_scale=1.3)
+    lp = oracle.selective_log_softmax(z, ids, **kw)
+    z64 = z.double().requires_grad_()
+    t = 4.0 * torch.tanh(z64 / 4.0) * 1.3 / 0.8
+    ref = torch.gather(F.log_softmax(t, -1), -1, ids.unsqueeze(-1)).squeeze(-1)
+    torch.testing.assert_close(lp.double(), ref.detach(), rtol=2e-6, atol=2e-6)
+    # the gradient the kernels form: -dout * (softmax - onehot) * dt/dz
+    up = torch.randn(5, 7).double()
+    (ref * up).sum().backward()
+    t32, dt = oracle.rl_logit_xform(z, 4.0, 1.3, 0.8)
+    g = oracle.ce_bwd(t32.reshape(-1, 300), ids.reshape(-1), -up.reshape(-1).float(),
+                      out_dtype=torch.float32) * dt.reshape(-1, 300)
+    torch.testing.assert_close(g.double(), z64.grad.reshape(-1, 300), rtol=1e-4, atol=1e-6)
+
+
 def test_linear_ce_reductions_agree():
     """mean = sum(rows) / n_valid with gradients equal to those of "none" under a
     constant upstream gradient 1 / n_valid; sum likewise with 1."""

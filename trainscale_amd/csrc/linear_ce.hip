@@ -799,7 +799,8 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   if (N < 0 || H <= 0 || V <= 0)
     return fail(TS_ERR_SHAPE, "flce: bad shape N=%lld H=%lld V=%lld", (long long)N, (long long)H,
                 (long long)V);
-  if ((flags & ~TS_FLCE_ACCUM_BF16) != 0)
+  // TS_FLCE_GRADS sizes the workspace; here the gradient pointers decide
+  if ((flags & ~(TS_FLCE_ACCUM_BF16 | TS_FLCE_GRADS)) != 0)
     return fail(TS_ERR_INVALID_ARGUMENT, "flce: unknown flags 0x%x", (unsigned)flags);
   const bool acc_bf16 = (flags & TS_FLCE_ACCUM_BF16) != 0;
   if (N % 8 != 0 || H % 8 != 0 || V % 8 != 0)

@@ -11,7 +11,8 @@ import torch.nn as nn
 from torch import Tensor
 
 from .linear_ce import (FusedLinearCrossEntropyFunction, LinearCrossEntropyFunction,
-                        chunked_log_softmax, fused_linear_cross_entropy)
+                        SelectiveLogSoftmaxFunction, chunked_log_softmax,
+                        fused_linear_cross_entropy, selective_log_softmax)
 from .sota_losses import (
     ChunkedCrossEntropyLoss,
     CrossEntropyRowsFunction,
@@ -32,6 +33,8 @@ __all__ = [
     "FusedLinearCrossEntropyFunction",
     "fused_linear_cross_entropy",
     "chunked_log_softmax",
+    "selective_log_softmax",
+    "SelectiveLogSoftmaxFunction",
 ]
 
 

@@ -38,6 +38,7 @@ bf16, and the gradient GEMMs accumulate in fp32.
 """
 from __future__ import annotations
 
+import math
 from typing import Optional
 
 import torch
@@ -48,7 +49,8 @@ from .._lib import check, ptr
 from .sota_losses import SECOND_BACKWARD_MSG
 
 __all__ = ["LinearCrossEntropyFunction", "FusedLinearCrossEntropyFunction",
-           "fused_linear_cross_entropy", "chunked_log_softmax", "DEFAULT_TOKEN_CHUNKS",
+           "fused_linear_cross_entropy", "chunked_log_softmax", "selective_log_softmax",
+           "SelectiveLogSoftmaxFunction", "DEFAULT_TOKEN_CHUNKS",
            "linear_ce_forward", "linear_ce_backward", "linear_ce_forward_backward",
            "VocabShardState", "linear_ce_vocab_phase1", "linear_ce_vocab_phase2"]
 
@@ -458,10 +460,16 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
     return out
 
 
+# A label value no token id takes: every position of the RL drop-ins counts (the
+# reference gathers at every position, rl_training.py:131-134).
+_NO_IGNORE = -(1 << 62)
+
+
 def chunked_log_softmax(hidden_states: Tensor, lm_head: Tensor, input_ids: Tensor,
                         num_chunks: int = 4, temperature: float = 1.0,
                         logit_softcapping: float = 0.0, logit_scale: float = 0.0,
-                        store_logits: bool = False) -> Tensor:
+                        store_logits: bool = False,
+                        out_dtype: Optional[torch.dtype] = None) -> Tensor:
     """Drop-in for chunked_log_softmax (rl_training.py:138-191): log-probabilities
     [B, L] of input_ids under the transformed logits of hidden_states [B, L, H] @
     lm_head[V, H].T, differentiable in hidden_states and lm_head.
@@ -471,10 +479,72 @@ def chunked_log_softmax(hidden_states: Tensor, lm_head: Tensor, input_ids: Tenso
     the logits are never stored (the two-pass schedule), so num_chunks is
     accepted for the signature and unused; store_logits=True keeps one bf16
     copy of them ([B * L, V]) so the backward skips their recompute.
+
+    The log-probs come back in the logits' dtype, as the reference's do (its
+    selective_log_softmax computes in the dtype of hidden_states @ lm_head.T):
+    formed in fp32 and rounded once. out_dtype=torch.float32 keeps them unrounded.
     """
     del num_chunks
-    rows = fused_linear_cross_entropy(hidden_states, lm_head, input_ids, ignore_index=-(1 << 62),
+    rows = fused_linear_cross_entropy(hidden_states, lm_head, input_ids, ignore_index=_NO_IGNORE,
                                       reduction="none", logit_softcapping=logit_softcapping,
                                       logit_scaling=logit_scale, temperature=temperature,
                                       schedule="stored_logits" if store_logits else "two_pass")
-    return -rows
+    return (-rows).to(out_dtype or hidden_states.dtype)
+
+
+def _rl_as_ce_xform(temperature: float, logit_softcapping: float, logit_scale: float):
+    """selective_log_softmax's transform t = (c tanh(z / c) or z) * (s or 1) / T
+    (rl_training.py:114-122) as the CE kernels' scale-then-softcap form
+    t = c' tanh(s' z / c') (or s' z): with m = (s or 1) / T, s' = m and c' = c m give
+    c m tanh(m z / (c m)) = c m tanh(z / c). Returns (logit_scale, softcap) for the
+    CE kernels, 0 meaning off."""
+    if not temperature > 0 or not math.isfinite(temperature):
+        raise ValueError(f"selective_log_softmax: temperature must be > 0, got {temperature}")
+    if logit_softcapping < 0 or logit_scale < 0:
+        raise ValueError("selective_log_softmax: logit_softcapping and logit_scale must be >= 0")
+    m = (logit_scale if logit_scale > 0 else 1.0) / temperature
+    return (m if m != 1.0 else 0.0), (logit_softcapping * m if logit_softcapping > 0 else 0.0)
+
+
+class SelectiveLogSoftmaxFunction(torch.autograd.Function):
+    """log_softmax(t(logits))[input_ids] over explicit logits [..., V] on the CE kernels
+    (ts_ce_fwd, ts_ce_bwd): forward returns the log-probs shaped like input_ids; the
+    backward writes the gradient of the logits into a new tensor."""
+
+    @staticmethod
+    def forward(ctx, logits: Tensor, input_ids: Tensor, temperature: float,
+                logit_softcapping: float, logit_scale: float,
+                out_dtype: Optional[torch.dtype]) -> Tensor:
+        if logits.shape[:-1] != input_ids.shape:
+            raise ValueError(f"selective_log_softmax: logits {tuple(logits.shape)} and input_ids "
+                             f"{tuple(input_ids.shape)} do not match")
+        scale, cap = _rl_as_ce_xform(temperature, logit_softcapping, logit_scale)
+        l2d, ld = ops.as_rows(logits)
+        ids = input_ids.reshape(-1)
+        rows, lse = ops.ce_forward(l2d, ld, ids, _NO_IGNORE, scale, cap)
+        ctx.save_for_backward(l2d, ids, lse)
+        ctx.cfg = (ld, scale, cap, logits.shape)
+        return (-rows).to(out_dtype or logits.dtype).view(input_ids.shape)
+
+    @staticmethod
+    def backward(ctx, grad_out: Tensor):
+        l2d, ids, lse = ctx.saved_tensors
+        ld, scale, cap, shape = ctx.cfg
+        grad = torch.empty((l2d.shape[0], l2d.shape[1]), dtype=l2d.dtype, device=l2d.device)
+        # d(log-prob)/d(row loss) = -1
+        dl = -grad_out.detach().float().reshape(-1)
+        ops.ce_backward(l2d, ld, ids, lse, dl, grad, grad.shape[1], 1.0, _NO_IGNORE, scale, cap)
+        return grad.view(shape), None, None, None, None, None
+
+
+def selective_log_softmax(logits: Tensor, input_ids: Tensor, temperature: float = 1.0,
+                          logit_softcapping: float = 0.0, logit_scale: float = 0.0,
+                          out_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """Drop-in for selective_log_softmax (rl_training.py:95-135): the log-probability
+    of input_ids [...] under logits [..., V] after softcapping, then scaling, then
+    temperature, without a [..., V] log-softmax in memory; differentiable in logits.
+    Returns the logits' dtype as the reference does (formed in fp32, rounded once;
+    out_dtype=torch.float32 keeps them unrounded). temperature must be > 0."""
+    return SelectiveLogSoftmaxFunction.apply(logits, input_ids, float(temperature),
+                                             float(logit_softcapping), float(logit_scale),
+                                             out_dtype)
