@@ -20,8 +20,8 @@ streaming copy of the same bytes (ts_stream_copy).
 
 Also reported, outside the timed step: C4 (packed varlen RMSNorm + RoPE with
 position_ids at 70B shapes, GB/s) and C5 (fused linear cross-entropy, TFLOP/s
-against the bf16 MFMA peak: the default schedule for the call, token chunks of a
-quarter of the tokens; the two-pass schedule, the RL form and the one-call
+against the bf16 MFMA peak: the default schedule for the call, token chunks of
+half the tokens; the two-pass schedule, the RL form and the one-call
 schedule with all logits in one chunk as separate lines), each with its own
 timing, and the reference's eager CPU path per config.
 
@@ -413,9 +413,9 @@ def bench_next_rows(dev, steps: int, warmup: int):
 
 def bench_linear_ce(dev, steps: int, warmup: int):
     """C5: fused linear CE fwd+bwd (loss, grad_hidden, grad_weight). The default schedule
-    for this call (mean, gradients needed) is the one-call schedule in token chunks of a
-    quarter of the tokens, grad_weight summed in its bf16 output: no more than a quarter
-    of the [N, V] logits exists at a time, three GEMMs. Also timed: the two-pass schedule
+    for this call (mean, gradients needed) is the one-call schedule in token chunks of
+    half the tokens, grad_weight summed in its bf16 output: no more than half of the
+    [N, V] logits exists at a time, three GEMMs. Also timed: the two-pass schedule
     (no logits stored, four GEMMs), the RL form through it (per-token losses,
     temperature, per-row upstream gradients), and the one-call schedule with all logits
     in one chunk (opt-in, not the C5 configuration)."""
@@ -460,16 +460,16 @@ def bench_linear_ce(dev, steps: int, warmup: int):
         torch.cuda.empty_cache()
         return ms, ws_bytes
 
-    # the default: token chunks of a quarter of the tokens, grad_weight summed in bf16
+    # the default: token chunks of half the tokens, grad_weight summed in bf16
     chunk = _chunk_rows(N, V, None)
     ms, ws_bytes = one_call_timer(chunk, TS_FLCE_ACCUM_BF16)
     tf = flops / (ms * 1e-3) / 1e12
     out = {"workload": (f"C5 fused linear CE: hidden [{N},{H}] bf16, lm_head [{V},{H}] bf16, "
                         f"5% ignored, mean; loss + grad_hidden + grad_weight; default schedule: "
                         f"one call in token chunks of {chunk} rows (at most {chunk}x{V} bf16 "
-                        f"logits at a time, a quarter of the full logits), grad_weight summed "
+                        f"logits at a time, half of the full logits), grad_weight summed "
                         f"over the chunks in its bf16 output"),
-           "schedule": "fused, token chunk N/4, bf16 grad_weight sum",
+           "schedule": "fused, token chunk N/2, bf16 grad_weight sum",
            "ms": round(ms, 4), "algorithmic_flop": flops, "executed_flop": flops,
            "TFLOP_s": round(tf, 1), "workspace_bytes": ws_bytes,
            "full_logits_bytes": N * V * 2,

@@ -267,13 +267,13 @@ def test_strided_rows(gpu):
 # C5 at full size: every element of both gradients, for each schedule
 # ---------------------------------------------------------------------------
 
-C5_TOKEN_CHUNK = 2048  # the default schedule's token chunk at N = 8192
+C5_TOKEN_CHUNK = 4096  # the default schedule's token chunk at N = 8192
 
 
 @pytest.fixture(scope="module")
 def c5(gpu):
     """C5's inputs, the stored-logits schedule's outputs and the reference with its bound
-    terms, in token chunks of the default schedule's 2048 rows (torch on the GPU: the
+    terms, in token chunks of the default schedule's 4096 rows (torch on the GPU: the
     oracle's arithmetic with fp32 logits GEMMs and float64 gradient GEMMs)."""
     wl = workloads.linear_ce_workload(gpu)
     h, w, labels = wl.tensors["hidden"], wl.tensors["weight"], wl.tensors["labels"]
@@ -315,10 +315,10 @@ def test_c5_dlogits(c5):
 
 def test_c5_full(c5):
     """C5 through the schedule fused_linear_cross_entropy picks for it by default (auto:
-    the one-call schedule in token chunks of a quarter of the tokens, grad_weight summed
-    in its bf16 output), the configuration of bench.py's C5 line: the loss, every row's
-    loss, and every element of grad_hidden and grad_weight within the bounds of that
-    accumulation (a bf16 running sum over 4 chunks for grad_weight)."""
+    the one-call schedule in token chunks of half the tokens, grad_weight summed in its
+    bf16 output), the configuration of bench.py's C5 line: the loss, every row's loss,
+    and every element of grad_hidden and grad_weight within the bounds of that
+    accumulation (a bf16 running sum over 2 chunks for grad_weight)."""
     loss, rows, lse, gh, gw = linear_ce_forward_backward(c5.h, c5.w, c5.labels,
                                                          chunk_tokens=None,
                                                          grad_weight_accum="bf16")
@@ -343,7 +343,7 @@ def test_c5_full_stored_logits(c5):
 @pytest.mark.parametrize("chunk", [None, 0])
 def test_c5_full_fused_schedule(c5, chunk):
     """C5 through the one-call schedule with grad_weight summed in fp32 (opt-in), at the
-    default token chunk (a quarter of the tokens) and in one chunk (opt-in)."""
+    default token chunk (half the tokens) and in one chunk (opt-in)."""
     loss, rows, lse, gh, gw = linear_ce_forward_backward(c5.h, c5.w, c5.labels,
                                                          chunk_tokens=chunk,
                                                          grad_weight_accum="fp32")

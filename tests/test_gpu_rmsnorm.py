@@ -106,6 +106,21 @@ def test_backward_fewer_rows_than_row_slots(gpu, rows, cols):
     check_against_oracle(x, w, dy, 1e-6)
 
 
+@pytest.mark.parametrize("rows,cols,dtype,wdtype", [(5000, 2048, BF, BF), (4099, 1024, BF, BF),
+                                                    (3001, 1536, BF, torch.float32),
+                                                    (2049, 1024, torch.float32, torch.float32),
+                                                    (1027, 520, torch.float16, torch.float16)])
+def test_backward_one_wave_per_row(gpu, rows, cols, dtype, wdtype):
+    """Rows of 65-256 16-byte vectors take the one-wave-per-row backward (rms_bwd_wave):
+    enough rows that every wave walks several steps, and a last step with rows past
+    the matrix."""
+    torch.manual_seed(rows + cols)
+    x = torch.randn(rows, cols, device=gpu).to(dtype)
+    w = (1 + 0.1 * torch.randn(cols, device=gpu)).to(wdtype)
+    dy = torch.randn(rows, cols, device=gpu).to(dtype)
+    check_against_oracle(x, w, dy, 1e-5)
+
+
 @pytest.mark.parametrize("dtype,wdtype", [(torch.float16, torch.float16),
                                           (torch.float32, torch.float32),
                                           (BF, torch.float32), (torch.float16, torch.float32)])

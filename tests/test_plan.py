@@ -68,23 +68,51 @@ int main() {
               CHECK(cols % V == 0 && vec, "reg path for unaligned row");
               CHECK((long long)r.tpr * r.kv >= nvec, "rows=%lld cols=%lld: plan covers %d of %lld vectors",
                     rows, cols, r.tpr * r.kv, nvec);
-              const bool inst = (r.kv == 1 && (r.tpr == 64 || r.tpr == 128 || r.tpr == 256 ||
-                                                r.tpr == 512)) ||
-                                (r.tpr == 512 && (r.kv == 2 || r.kv == 4));
-              CHECK(inst, "no bwd instantiation for tpr=%d kv=%d", r.tpr, r.kv);
-              CHECK(r.block == 512 && r.rpb * r.tpr == 512, "bwd block shape");
+              if (p.wave) {
+                CHECK(r.tpr == 64 && (r.kv == 2 || r.kv == 4),
+                      "no wave instantiation for tpr=%d kv=%d", r.tpr, r.kv);
+                CHECK(r.block == 64 * kWaveRowsPerBlock && r.rpb == kWaveRowsPerBlock,
+                      "wave block shape");
+                CHECK(nvec <= kWaveRowMaxVec, "wave dW staging exceeds its LDS array");
+              } else {
+                const bool inst = (r.kv == 1 && (r.tpr == 64 || r.tpr == 128 || r.tpr == 256 ||
+                                                  r.tpr == 512)) ||
+                                  (r.tpr == 512 && (r.kv == 2 || r.kv == 4));
+                CHECK(inst, "no bwd instantiation for tpr=%d kv=%d", r.tpr, r.kv);
+                CHECK(r.block == 512 && r.rpb * r.tpr == 512, "bwd block shape");
+              }
               CHECK(p.steps >= 1 && p.grid >= (rows > 0 ? 1 : 0), "grid %lld steps %lld",
                     (long long)p.grid, (long long)p.steps);
               // every row is covered by exactly one (workgroup, step, slot)
               CHECK(p.grid * p.steps * r.rpb >= rows, "rows=%lld not covered", rows);
               CHECK(rows == 0 || (p.grid - 1) * p.steps * r.rpb < rows, "empty workgroup");
               CHECK(p.grid < (1ll << 31), "grid too large");
-              if (dw) CHECK(p.nparts == p.grid * r.rpb, "nparts != grid * rpb");
+              if (dw) CHECK(p.nparts == (p.wave ? p.grid : p.grid * r.rpb), "nparts");
               // every 16-byte load of the backward kernel lies inside the [rows, ld] matrix
               // (ld = cols and a wider stride), for every workgroup, slot, step and lane
               if (rows > 0 && rows <= 2049 && cols <= 8192) {
                 for (long long ld : {cols, cols + V}) {
                   const long long rstep = p.grid * r.rpb;
+                  if (p.wave) {
+                    // the buffer span of every (workgroup, slot, step) lies inside the matrix;
+                    // lane offsets (v * 16 for v < nvec) lie inside a span of nvec * 16 bytes
+                    const uint32_t rb = (uint32_t)(nvec * 16);
+                    for (long long wg = 0; wg < p.grid; ++wg)
+                      for (int sub = 0; sub < r.rpb; ++sub)
+                        for (long long st = 0; st < p.steps + 1; ++st) {
+                          const RowSpan sp = rms_bwd_wave_row(wg * r.rpb + sub, st, rstep,
+                                                              p.steps, rows, ld, rb);
+                          const long long row = wg * r.rpb + sub + st * rstep;
+                          CHECK(sp.bytes == 0 || (sp.offset >= 0 && sp.offset * (16 / V) + sp.bytes <=
+                                                  ((rows - 1) * ld + cols) * (16 / V)),
+                                "rows=%lld cols=%lld ld=%lld wg=%lld sub=%d st=%lld: span past the "
+                                "matrix", rows, cols, ld, wg, sub, st);
+                          CHECK((sp.bytes != 0) == (st < p.steps && row < rows),
+                                "span of a row that %s", sp.bytes ? "does not exist" : "exists");
+                          CHECK(sp.bytes == 0 || sp.offset == row * ld, "span of another row");
+                        }
+                    continue;
+                  }
                   for (long long wg = 0; wg < p.grid; wg += (p.grid > 64 ? p.grid / 17 : 1))
                     for (int sub = 0; sub < r.rpb; ++sub)
                       for (long long st = 0; st < p.steps + 1; ++st)

@@ -85,8 +85,33 @@ inline RmsRowPlan rms_bwd_row_plan(int64_t nvec) {
   return p;
 }
 
+// Backward, one wave per row (rms_bwd_wave): rows of 65..256 vectors, kv = 2
+// or 4 vectors per lane, kWaveRowsPerBlock waves (rows) per workgroup step.
+// The row's sum is a wave reduction (no LDS, no barrier), and each lane has
+// 2 kv loads in flight; the workgroup sums its waves' dW in LDS once at the
+// end and writes one partial row. Measured on MI355X against the workgroup-
+// per-row kernel (rms_bwd_reg): [16384, 2048] bf16 42.0 against 48.1 us,
+// [16384, 1024] 35.5 against 36.6 us; at [16384, 4096] (8 vectors per lane,
+// 233 VGPRs) it was slower, 80.4 against 74.7 us, so longer rows keep
+// rms_bwd_reg.
+constexpr int64_t kWaveRowMinVec = 65;
+constexpr int64_t kWaveRowMaxVec = 256;
+constexpr int kWaveRowsPerBlock = 4;
+
+inline RmsRowPlan rms_bwd_wave_plan(int64_t nvec) {
+  RmsRowPlan p{false, 0, 0, 0, 0};
+  if (nvec < kWaveRowMinVec || nvec > kWaveRowMaxVec) return p;
+  p.tpr = 64;
+  p.kv = nvec <= 128 ? 2 : 4;
+  p.reg = true;
+  p.block = 64 * kWaveRowsPerBlock;
+  p.rpb = kWaveRowsPerBlock;
+  return p;
+}
+
 struct RmsBwdPlan {
   bool reg;        // register path (else the generic element-wise kernels)
+  bool wave;       // register path with one wave per row (rms_bwd_wave)
   RmsRowPlan row;  // register-path shape
   int64_t steps;   // row groups (of rpb rows) per workgroup
   int64_t grid;    // workgroups of the dx kernel
@@ -96,9 +121,13 @@ struct RmsBwdPlan {
 // `vec_ok` says whether pointers and strides allow 16-byte access.
 inline RmsBwdPlan rms_bwd_plan(int64_t rows, int64_t cols, int elt_bytes, bool vec_ok,
                                bool need_dw) {
-  RmsBwdPlan p{false, RmsRowPlan{false, 0, 0, 0, 0}, 0, 0, 0};
+  RmsBwdPlan p{false, false, RmsRowPlan{false, 0, 0, 0, 0}, 0, 0, 0};
   const int V = vec_elems(elt_bytes);
-  if (vec_ok && cols % V == 0) p.row = rms_bwd_row_plan(cols / V);
+  if (vec_ok && cols % V == 0) {
+    p.row = rms_bwd_wave_plan(cols / V);
+    p.wave = p.row.reg;
+    if (!p.wave) p.row = rms_bwd_row_plan(cols / V);
+  }
   p.reg = p.row.reg;
   if (p.reg) {
     const int64_t groups = (rows + p.row.rpb - 1) / p.row.rpb;
@@ -106,7 +135,8 @@ inline RmsBwdPlan rms_bwd_plan(int64_t rows, int64_t cols, int elt_bytes, bool v
     if (steps < 1) steps = 1;
     p.steps = steps;
     p.grid = (groups + steps - 1) / steps;
-    p.nparts = need_dw ? p.grid * p.row.rpb : 0;
+    // the wave kernel sums its rows' dW in LDS: one partial row per workgroup
+    p.nparts = need_dw ? (p.wave ? p.grid : p.grid * p.row.rpb) : 0;
   } else {
     p.steps = 0;
     p.grid = rows;
@@ -128,6 +158,23 @@ TS_HOST_DEVICE inline int64_t rms_bwd_load_offset(int64_t row0, int64_t st, int6
   const int64_t v = (int64_t)t + (int64_t)k * tpr;
   const bool ok = st < steps && row < rows && v < nvec;
   return ok ? row * ld + v * V : 0;
+}
+
+// The row that a wave-per-row backward slot (rms_bwd_wave) touches at step
+// st, for a [rows, ld] matrix: the element offset of the row and its bytes
+// (row_bytes), or {0, 0} for a step past `steps` or a row past the matrix. The
+// kernel builds a buffer resource on it, so its accesses can only reach that
+// row, or nothing (the hardware drops stores and zero-fills loads outside).
+struct RowSpan {
+  int64_t offset;
+  uint32_t bytes;
+};
+TS_HOST_DEVICE inline RowSpan rms_bwd_wave_row(int64_t row0, int64_t st, int64_t rstep,
+                                               int64_t steps, int64_t rows, int64_t ld,
+                                               uint32_t row_bytes) {
+  const int64_t row = row0 + st * rstep;
+  const bool ok = st < steps && row < rows;
+  return ok ? RowSpan{row * ld, row_bytes} : RowSpan{0, 0u};
 }
 
 // Rows of fp32 dW partials any backward launch for (rows, cols) may write:

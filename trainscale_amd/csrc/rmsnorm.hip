@@ -325,6 +325,167 @@ __global__ __launch_bounds__(512) void rms_bwd_reg(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Backward, one wave per row (ts_plan::rms_bwd_wave_plan): lane l holds the
+// row's 16-byte vectors l, l + 64, ... (KV of them), so sum(dy * w * xhat) is
+// a wave reduction (DPP and lane reads: no LDS, no barrier). Wave j of
+// workgroup b takes rows (b * kR + j) + s * gridDim.x * kR, s < steps: as in
+// rms_bwd_reg, the running workgroups stay on a compact window of rows.
+//
+// Rows are addressed through buffer resources (ts_plan::rms_bwd_wave_row):
+// a row's resource spans that row, or nothing for a row past the matrix, so
+// loads past it read zeros and stores past it are dropped by the hardware,
+// and the loop has no branches around memory operations. The next row's
+// loads are issued before this row's dx stores: vmcnt counts loads and
+// stores in issue order, so the wait for those loads at the top of the next
+// step does not wait for the stores.
+//
+// dW: each lane keeps dy * xhat of its columns over its wave's rows in fp32;
+// at the end the kR waves' sums are added in LDS in a fixed order and the
+// workgroup writes one fp32 partial row (rms_dw_reduce4 sums those).
+// ---------------------------------------------------------------------------
+template <typename T, typename W, int KV>
+__global__ __launch_bounds__(64 * ts_plan::kWaveRowsPerBlock)
+__attribute__((amdgpu_waves_per_eu(2, 2))) void rms_bwd_wave(
+    const T* __restrict__ dy, int64_t lddy, const T* __restrict__ x, int64_t ldx,
+    const W* __restrict__ w, const float* __restrict__ rstd_in, T* __restrict__ dx,
+    int64_t lddx, float* __restrict__ partial, int64_t rows, int64_t steps, int nvec,
+    float fcols) {
+  constexpr int V = Elt<T>::kVec;
+  constexpr int kR = ts_plan::kWaveRowsPerBlock;
+  constexpr int kWv = Elt<W>::kVec;
+  constexpr int kWq = V / kWv;  // 16-byte weight vectors per data vector (1 or 2)
+  // dW of the kR waves before they are combined: up to kWaveRowMaxVec vectors each
+  __shared__ float4 dw_lds[kR * ts_plan::kWaveRowMaxVec * V / 4];
+  const int lane = threadIdx.x & (kWave - 1);
+  // uniform over the wave: keeps the row's buffer resources in SGPRs
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+
+  // lane-invariant byte offsets of this lane's vectors within a row
+  int voff[KV];
+  u32x4 wq[KV][kWq];
+  float acc[KV][V];
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const int v = lane + k * kWave;
+    voff[k] = v < nvec ? v * 16 : kBufOob;
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[k][i] = 0.f;
+#pragma unroll
+    for (int h = 0; h < kWq; ++h) {
+      if (w != nullptr && v < nvec) {
+        wq[k][h] = ld16(w + (int64_t)v * V + h * kWv);
+      } else {
+        float one[kWv];
+#pragma unroll
+        for (int i = 0; i < kWv; ++i) one[i] = 1.f;
+        wq[k][h] = Elt<W>::pack(one);
+      }
+    }
+  }
+
+  const int64_t row0 = (int64_t)blockIdx.x * kR + wid;
+  const int64_t rstep = (int64_t)gridDim.x * kR;
+  const uint32_t row_bytes = (uint32_t)nvec * 16u;
+  u32x4 xv[KV], dv[KV];
+  auto issue = [&](int64_t st) {
+    const ts_plan::RowSpan sx = ts_plan::rms_bwd_wave_row(row0, st, rstep, steps, rows, ldx,
+                                                          row_bytes);
+    const ts_plan::RowSpan sd = ts_plan::rms_bwd_wave_row(row0, st, rstep, steps, rows, lddy,
+                                                          row_bytes);
+    const Rsrc rx = buf_rsrc(x + sx.offset, sx.bytes);
+    const Rsrc rd = buf_rsrc(dy + sd.offset, sd.bytes);
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      xv[k] = buf_ld16_stream(rx, voff[k]);
+      dv[k] = buf_ld16_stream(rd, voff[k]);
+    }
+  };
+
+  issue(0);
+  {  // as in rms_bwd_reg: enter the loop with the back edge's loads-then-stores pattern
+    const Rsrc none = buf_rsrc(dx, 0u);
+#pragma unroll
+    for (int k = 0; k < KV; ++k) buf_st16_stream(u32x4{0u, 0u, 0u, 0u}, none, voff[k]);
+  }
+  for (int64_t st = 0; st < steps; ++st) {
+    const int64_t row = row0 + st * rstep;
+    const bool valid = row < rows;
+    const float rstd = valid ? rstd_in[row] : 0.f;
+    // c1 = mean(dy * w * xhat); lanes and rows outside the matrix loaded zeros
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      float xf[V], df[V], wf[V];
+      Elt<T>::unpack(xv[k], xf);
+      Elt<T>::unpack(dv[k], df);
+#pragma unroll
+      for (int h = 0; h < kWq; ++h) Elt<W>::unpack(wq[k][h], wf + h * kWv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        const float xh = xf[i] * rstd;
+        s = __builtin_fmaf(df[i] * wf[i], xh, s);
+        acc[k][i] = __builtin_fmaf(df[i], xh, acc[k][i]);
+      }
+    }
+    const float c1 = wave_sum(s) / fcols;
+    // dx unpacks the raw vectors again: carrying the unpacked floats across the
+    // reduction would triple their registers
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      asm volatile("" : "+v"(xv[k]), "+v"(dv[k]));
+#pragma unroll
+      for (int h = 0; h < kWq; ++h) asm volatile("" : "+v"(wq[k][h]));
+    }
+    u32x4 o[KV];
+#pragma unroll
+    for (int k = 0; k < KV; ++k) {
+      float xf[V], df[V], wf[V], of[V];
+      Elt<T>::unpack(xv[k], xf);
+      Elt<T>::unpack(dv[k], df);
+#pragma unroll
+      for (int h = 0; h < kWq; ++h) Elt<W>::unpack(wq[k][h], wf + h * kWv);
+#pragma unroll
+      for (int i = 0; i < V; ++i) of[i] = rstd * (df[i] * wf[i] - (xf[i] * rstd) * c1);
+      o[k] = Elt<T>::pack(of);
+    }
+    issue(st + 1);  // a step past `steps` spans nothing: its loads read zeros
+    const ts_plan::RowSpan so = ts_plan::rms_bwd_wave_row(row0, st, rstep, steps, rows, lddx,
+                                                          row_bytes);
+    const Rsrc ro = buf_rsrc(dx + so.offset, so.bytes);
+#pragma unroll
+    for (int k = 0; k < KV; ++k) buf_st16_stream(o[k], ro, voff[k]);
+  }
+
+  if (partial == nullptr) return;  // dW not requested
+  const int nq = nvec * V / 4;     // float4 quads of a row
+  float4* mine = dw_lds + wid * nq;
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const int v = lane + k * kWave;
+    if (v < nvec) {
+#pragma unroll
+      for (int h = 0; h < V / 4; ++h)
+        mine[v * (V / 4) + h] =
+            make_float4(acc[k][4 * h], acc[k][4 * h + 1], acc[k][4 * h + 2], acc[k][4 * h + 3]);
+    }
+  }
+  __syncthreads();
+  float4* prow = reinterpret_cast<float4*>(partial + (int64_t)blockIdx.x * nvec * V);
+  for (int q = threadIdx.x; q < nq; q += kR * kWave) {
+    float4 t = dw_lds[q];
+#pragma unroll
+    for (int j = 1; j < kR; ++j) {
+      const float4 u = dw_lds[j * nq + q];
+      t.x += u.x;
+      t.y += u.y;
+      t.z += u.z;
+      t.w += u.w;
+    }
+    prow[q] = t;
+  }
+}
+
 // Clears n bytes (a kernel rather than hipMemsetAsync, so a captured graph
 // replays it like any other node).
 __global__ __launch_bounds__(256) void zero_bytes(uint8_t* __restrict__ p, size_t n) {
@@ -551,7 +712,25 @@ ts_status bwd_typed(const void* dy, int64_t lddy, const void* x, int64_t ldx, co
   if (dw != nullptr && (size_t)plan.nparts * (size_t)cols * sizeof(float) > ws_bytes)
     return ts_host::fail(TS_ERR_WORKSPACE, "rmsnorm_bwd: plan needs %lld partial rows",
                          (long long)plan.nparts);
-  if (plan.reg) {
+  if (plan.wave) {
+    float* part = dw != nullptr ? ws : nullptr;
+    bool launched = false;
+#define TS_LAUNCH_WAVE(KV)                                                                     \
+  if (plan.row.kv == KV) {                                                                     \
+    hipLaunchKernelGGL((rms_bwd_wave<T, W, KV>), dim3((unsigned)plan.grid),                    \
+                       dim3(plan.row.block), 0, st, dyp, lddy, xp, ldx, wp, rstd, dxp, lddx,   \
+                       part, rows, plan.steps, (int)nvec, (float)cols);                        \
+    launched = true;                                                                           \
+  }
+    TS_LAUNCH_WAVE(2)
+    TS_LAUNCH_WAVE(4)
+#undef TS_LAUNCH_WAVE
+    if (!launched)
+      return ts_host::fail(TS_ERR_INVALID_ARGUMENT, "rmsnorm_bwd: bad wave plan (kv=%d)",
+                           plan.row.kv);
+    ts_status s = ts_host::check_launch("rms_bwd_wave");
+    if (s != TS_OK) return s;
+  } else if (plan.reg) {
     float* part = dw != nullptr ? ws : nullptr;
     bool launched = false;
 #define TS_LAUNCH_BWD(TPR, KV)                                                                  \

@@ -18,10 +18,11 @@ Two schedules run on the gfx950 kernels:
   directly. Scratch: N x chunk bf16 dlogits plus N x H fp32.
 * ``"fused"`` (mean/sum, no transforms): one call (``ts_flce_fwd_bwd``) forms
   the loss and both gradients for an upstream gradient of 1, token chunk by
-  token chunk: a quarter of the tokens by default, whose bf16 logits are the
-  only [rows, V] scratch, with grad_weight summed over the chunks in its bf16
-  output (as autograd sums the reference's per-chunk bf16 gradients); the
-  backward scales the gradients in place. Three GEMMs instead of four.
+  token chunk: half the tokens by default, whose bf16 logits are the only
+  [rows, V] scratch (half the [N, V] logits), with grad_weight summed over the
+  chunks in its bf16 output (one bf16 rounding of the partial sum between the
+  chunks; fp32 accumulation is opt-in); the backward scales the gradients in
+  place. Three GEMMs instead of four.
 * ``"stored_logits"`` (opt-in; any reduction and transform): the two-pass
   forward also keeps the bf16 logits ([N, V], N * V * 2 bytes, as the
   reference's chunked_log_softmax keeps each chunk's logits for autograd);
@@ -54,10 +55,13 @@ __all__ = ["LinearCrossEntropyFunction", "FusedLinearCrossEntropyFunction",
            "linear_ce_forward", "linear_ce_backward", "linear_ce_forward_backward",
            "VocabShardState", "linear_ce_vocab_phase1", "linear_ce_vocab_phase2"]
 
-# The one-call schedule's token chunk with chunk_tokens=None: a quarter of the
-# tokens (rounded up to 256 rows), so its bf16 logits scratch stays within a
-# quarter of the [N, V] logits; batches of up to 256 tokens run as one chunk.
-DEFAULT_TOKEN_CHUNKS = 4
+# The one-call schedule's token chunk with chunk_tokens=None: half the tokens
+# (rounded up to 256 rows), so its bf16 logits scratch stays within half of the
+# [N, V] logits; batches of up to 256 tokens run as one chunk. Measured on MI355X
+# at C5 (N = 8192): 21.5 ms with two chunks of 4096 tokens, 22.5 ms with four of
+# 2048 (two more bf16 read-modify-write passes over grad_weight), 21.4 ms with all
+# the logits in one chunk.
+DEFAULT_TOKEN_CHUNKS = 2
 
 _REDUCTIONS = {"mean": 0, "sum": 1}
 TS_FLCE_GRADS, TS_FLCE_ACCUM_BF16 = 1, 2  # include/trainscale_amd.h
@@ -188,7 +192,7 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
                                grad_weight_accum: str = "fp32"):
     """Runs ts_flce_fwd_bwd; returns (loss fp32 0-d, loss_rows [N], lse [N],
     grad_hidden or None, grad_weight or None) for an upstream gradient of 1.
-    chunk_tokens: rows per token chunk (None: a quarter of the tokens, 0: one chunk);
+    chunk_tokens: rows per token chunk (None: half the tokens, 0: one chunk);
     grad_weight_accum: "fp32" (a V x H fp32 workspace, rounded once) or "bf16" (summed
     in the bf16 output, rounded after each chunk)."""
     if grad_weight_accum not in ("fp32", "bf16"):
@@ -429,7 +433,7 @@ def fused_linear_cross_entropy(hidden: Tensor, weight: Tensor, labels: Tensor,
     (per-row losses, shaped like labels).
 
     schedule: "auto" (default), "fused", "two_pass" or "stored_logits" (module
-    docstring). "fused": chunk_tokens rows per token chunk (None: a quarter of
+    docstring). "fused": chunk_tokens rows per token chunk (None: half of
     the tokens, 0: one chunk, i.e. all [N, V] logits), grad_weight_accum "bf16"
     (summed in the bf16 output) or "fp32" (a V x H fp32 workspace); a second
     backward through its graph raises. "two_pass": vocab_chunk columns per
