@@ -404,7 +404,9 @@ size_t ts_flce_workspace_size(int64_t N, int64_t H, int64_t V, int64_t chunk,
  * i.e. the gradients of *loss for an upstream gradient of 1.
  * hidden, weight, grad_hidden, grad_weight: bf16, row-major, 16-byte aligned,
  * row strides ldh/ldw (elements, multiples of 8; the gradients are dense).
- * N, H, V multiples of 8. Logits are formed in fp32 by MFMA and rounded to
+ * N and H multiples of 8 (the Python wrapper pads other N and H); any V >= 1
+ * (the library's logits rows are padded to whole 16-byte vectors and the
+ * columns past V masked). Logits are formed in fp32 by MFMA and rounded to
  * bf16 (the rounding a bf16 matmul applies); softmax statistics, lse and loss
  * are fp32. loss_rows, lse ([N] fp32) may be NULL. grad_hidden and
  * grad_weight may be NULL (then their GEMM is skipped; both NULL: forward
@@ -445,7 +447,8 @@ ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void* weight, i
  *   reduction 0 (mean): *loss = sum(loss_rows) / max(n_valid, 1); 1 (sum):
  *   *loss = sum(loss_rows); 2 (none): loss may be NULL.
  * hidden [N, H], weight [V, H]: bf16, 16-byte aligned, row strides ldh/ldw
- * (multiples of 8); H and V multiples of 8; any N >= 0.
+ * (multiples of 8); H a multiple of 8 (the Python wrapper pads other H); any
+ * V >= 1; any N >= 0.
  *
  * Forward: one logits GEMM whose epilogue keeps per-(row, 128-column slice)
  * max and sum of exp and the label's t; workspace of
@@ -492,8 +495,10 @@ ts_status ts_flce_backward(const void* hidden, int64_t ldh, const void* weight, 
 
 /*
  * ts_flce_forward that also writes the bf16 logits z = bf16(hidden @ weight^T)
- * to `logits` ([N, V], row stride V, 16-byte aligned, N * V * 2 bytes of
- * caller memory: 2.1 GB at N = 8192, V = 128256), for ts_flce_backward_kept.
+ * to `logits` ([N, V] with row stride round_up(V, 8), 16-byte aligned:
+ * N * round_up(V, 8) * 2 bytes of caller memory, 2.1 GB at N = 8192,
+ * V = 128256; the columns from V to the row's end are written too), for
+ * ts_flce_backward_kept.
  * Everything else is bit-identical to ts_flce_forward's, and its workspace is
  * the same. The reference's chunked_log_softmax keeps each chunk's
  * [B, chunk, V] logits alive for autograd's backward (rl_training.py:175-189);

@@ -263,6 +263,66 @@ def test_strided_rows(gpu):
     assert torch.equal(gh, gh_c) and torch.equal(gw, gw_c)
 
 
+@pytest.mark.parametrize("N,H,V", [(520, 256, 50257), (264, 72, 1001), (136, 100, 777),
+                                   (64, 37, 512), (1032, 768, 50257)])
+def test_vocab_and_hidden_not_multiples_of_8(gpu, N, H, V):
+    """V not a multiple of 8 (GPT-2's 50257): the library pads its logits rows to whole
+    16-byte vectors and masks the columns past V; H not a multiple of 8: the wrapper
+    zero-pads hidden and weight. Every schedule against the oracle: the one-call schedule
+    (default token chunks with an fp32 and a bf16 grad_weight sum, one chunk), the
+    two-pass schedule (default and 256-column vocabulary chunks) and, through make_ref,
+    the stored-logits schedule."""
+    torch.manual_seed(N + H + V)
+    h = torch.randn(N, H, device=gpu).to(BF)
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu)
+    labels[::13] = -100
+    labels[1] = V - 1  # the last column, in the partial last vector when V % 8 != 0
+    for chunk, accum in ((None, "fp32"), (None, "bf16"), (0, "bf16")):
+        _, gh, gw = check_against_oracle(h, w, labels, chunk=chunk, accum=accum)
+        assert gh.shape == (N, H) and gw.shape == (V, H)
+    for chunk in (None, 256):
+        check_two_pass(h, w, labels, "mean", chunk=chunk)
+    # the kept logits: [N, V] over rows padded to whole vectors
+    _, _, _, logits = linear_ce_forward(h, w, labels, keep_logits=True)
+    assert logits.shape == (N, V) and logits.stride(0) == -(-V // 8) * 8
+    z = (h.float().cpu() @ w.float().cpu().t()).to(BF)
+    torch.testing.assert_close(logits.float().cpu(), z.float(), rtol=2 ** -7, atol=1e-3)
+
+
+def test_odd_vocab_through_autograd_and_rl(gpu):
+    """fused_linear_cross_entropy (autograd, each schedule) and chunked_log_softmax at
+    V = 50257, H = 72 with a non-contiguous hidden view."""
+    torch.manual_seed(50257)
+    B, L, H, V = 2, 70, 72, 50257
+    hb = torch.randn(B, L, H + 8, device=gpu).to(BF)
+    w = (0.05 * torch.randn(V, H, device=gpu)).to(BF).requires_grad_()
+    labels = torch.randint(0, V, (B, L), device=gpu)
+    labels[0, :3] = -100
+    hd = hb[..., :H]
+    for schedule in ("fused", "two_pass", "stored_logits"):
+        h = hd.detach().clone().requires_grad_()
+        w.grad = None
+        loss = fused_linear_cross_entropy(h, w, labels, schedule=schedule)
+        loss.backward()
+        ref_loss, _, _ = oracle.linear_ce(h.detach().reshape(-1, H), w.detach(),
+                                          labels.reshape(-1), bf16_logits=True)
+        assert abs(loss.item() - float(ref_loss)) <= 1e-5 * abs(float(ref_loss)), schedule
+        ref = make_ref(h.detach(), w.detach(), labels,
+                       token_chunk=_token_chunk(B * L, V, None) or B * L)
+        mode = "one" if schedule != "fused" or not _token_chunk(B * L, V, None) else "bf16_run"
+        check_grads(h.grad, w.grad, ref, gw_mode=mode, what=f"odd V {schedule}")
+    hs = hd.detach().clone().requires_grad_()
+    w.grad = None
+    ids = torch.randint(0, V, (B, L), device=gpu)
+    lp = chunked_log_softmax(hs[:, :-1, :], w, ids[:, 1:], temperature=0.8,
+                             out_dtype=torch.float32)
+    rows, _, _ = oracle.linear_ce(hs.detach()[:, :-1, :].reshape(-1, H), w.detach(),
+                                  ids[:, 1:].reshape(-1), reduction="none", bf16_logits=True,
+                                  temperature=0.8)
+    torch.testing.assert_close(lp.reshape(-1).cpu(), -rows, rtol=1e-5, atol=2e-5)
+
+
 # ---------------------------------------------------------------------------
 # C5 at full size: every element of both gradients, for each schedule
 # ---------------------------------------------------------------------------

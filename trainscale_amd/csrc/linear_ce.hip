@@ -286,7 +286,11 @@ __device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) 
       const int64_t gm = mb + lrow;
       const int64_t gc = nb + c16 * 8;
       const u32x4 v = *reinterpret_cast<const u32x4*>(region + lrow * kStagePitch + c16 * 16);
-      const bool in = gm < a.M && gc < a.N;  // N % 8 == 0: a chunk is all in or all out
+      // a chunk of 8 columns is stored whole when it starts inside C (rows of C are
+      // padded to whole chunks: ldc >= round_up(N, 8)); nin of its columns are < N,
+      // fewer than 8 only in the last chunk when N % 8 != 0
+      const bool in = gm < a.M && gc < a.N;
+      const int nin = in ? (a.N - gc < 8 ? (int)(a.N - gc) : 8) : 0;
       if constexpr (kMode == kEpiLogits || kMode == kEpiBf16) {
         if (in) st16(a.C + gm * a.ldc + gc, v);
       }
@@ -299,6 +303,10 @@ __device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) 
         if (xf_on) {
 #pragma unroll
           for (int q = 0; q < 8; ++q) f[q] = a.xf.apply(f[q]);
+        }
+        if (nin < 8) {  // columns past N take no part in the statistics
+#pragma unroll
+          for (int q = 0; q < 8; ++q) f[q] = q < nin ? f[q] : -INFINITY;
         }
         float lm = f[0];
 #pragma unroll
@@ -342,11 +350,19 @@ __device__ inline void gemm_tile(const GemmArgs& a, int64_t bid, uint8_t* smem) 
             g[e] = ds * (e == d ? pr - 1.f : pr) * dt;
           }
         }
+        if (nin < 8) {  // columns past N: zero, the gradient GEMMs read them
+#pragma unroll
+          for (int e = 0; e < 8; ++e) g[e] = e < nin ? g[e] : 0.f;
+        }
         if (in) st16(a.C + gm * a.ldc + gc, Elt<__bf16>::pack(g));
       }
       if constexpr (kMode == kEpiLogits) {
         float f[8];
         Elt<__bf16>::unpack(v, f);
+        if (nin < 8) {  // columns past N take no part in the statistics
+#pragma unroll
+          for (int q = 0; q < 8; ++q) f[q] = q < nin ? f[q] : -INFINITY;
+        }
         float lm = f[0];
 #pragma unroll
         for (int q = 1; q < 8; ++q) lm = fmaxf(lm, f[q]);
@@ -566,9 +582,11 @@ __global__ __launch_bounds__(256) void flce_loss(const float* __restrict__ loss_
 }
 
 // dlogits of a chunk in place: D = (exp(z - lse) - onehot) * scale in bf16
-// over the logits [M, V] (0 on ignored rows, which are not read). One-shot
-// grid: a thread owns kDlKv 16-byte vectors of a row, spaced one workgroup
-// apart; blockIdx.x = row * chunks + chunk.
+// over the logits [M, V] with rows of ldl >= round_up(V, 8) elements (0 on
+// ignored rows, which are not read, and in the columns from V up to the end
+// of the last 16-byte vector, which the gradient GEMMs read). One-shot grid: a
+// thread owns kDlKv 16-byte vectors of a row, spaced one workgroup apart;
+// blockIdx.x = row * chunks + chunk.
 constexpr int kDlKv = 1;
 __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int64_t ldl,
                                                     const float* __restrict__ lse,
@@ -579,7 +597,7 @@ __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int6
                                                     int64_t label_offset) {
   const int64_t r = (int64_t)blockIdx.x / chunks;
   const int64_t c0 = ((int64_t)blockIdx.x % chunks) * (256 * kDlKv) + threadIdx.x;
-  const int64_t nvec = V / 8;
+  const int64_t nvec = (V + 7) / 8;
   const int64_t raw = labels[r];
   const int64_t lab = raw - label_offset;  // the label's column in these logits
   __bf16* row = L + r * ldl;
@@ -606,17 +624,19 @@ __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int6
     if (v < nvec) {
       float z[8], g[8];
       Elt<__bf16>::unpack(q[u], z);
+      const int64_t lim = V - v * 8;  // columns of this vector inside the row
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float pr = fast_exp2(__builtin_fmaf(z[e], kLog2e, -l2));
-        g[e] = scale * (v * 8 + e == lab ? pr - 1.f : pr);
+        g[e] = e < lim ? scale * (v * 8 + e == lab ? pr - 1.f : pr) : 0.f;
       }
       st16_stream(row + v * 8, Elt<__bf16>::pack(g));
     }
   }
 }
 
-// dz of the logits a forward kept, in place over them: for row r and column j,
+// dz of the logits a forward kept ([N, V] with rows of ldl >= round_up(V, 8)
+// elements), in place over them: for row r and column j < V (0 from V on),
 //   dz = bf16(dscale[r] * (exp(t - lse[r]) - [j == labels[r]]) * dt/dz),  t = xf(z),
 // the arithmetic of the dlogits epilogue (kEpiDlogits) on the same bf16 z, so
 // the result is bit-identical to what the recomputing backward forms (ignored
@@ -630,7 +650,7 @@ __global__ __launch_bounds__(256) void flce_dlogits_kept(__bf16* __restrict__ L,
                                                          LogitXform xf) {
   const int64_t r = (int64_t)blockIdx.x / chunks;
   const int64_t v = ((int64_t)blockIdx.x % chunks) * 256 + threadIdx.x;
-  if (v >= V / 8) return;
+  if (v >= (V + 7) / 8) return;
   __bf16* p = L + r * ldl + v * 8;
   const float ds = dscale[r];
   const u32x4 q = ld16_stream(p);
@@ -652,6 +672,11 @@ __global__ __launch_bounds__(256) void flce_dlogits_kept(__bf16* __restrict__ L,
       const float pr = fast_exp2(__builtin_fmaf(t, kLog2e, -l2));
       g[e] = ds * (e == d ? pr - 1.f : pr) * dt;
     }
+  }
+  const int64_t lim = V - v * 8;  // the columns from V on are zero for the GEMMs
+  if (lim < 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = e < lim ? g[e] : 0.f;
   }
   st16_stream(p, Elt<__bf16>::pack(g));
 }
@@ -716,6 +741,10 @@ __global__ __launch_bounds__(256) void scale_inplace(T* __restrict__ x, int64_t 
 // ---------------------------------------------------------------------------
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Row stride of the library's [rows, V] bf16 logits: whole 16-byte vectors, so any
+// V (GPT-2's 50257 included) keeps every row 16-byte aligned.
+inline int64_t logits_ld(int64_t V) { return round_up(V, 8); }
+
 struct Layout {
   int64_t chunk, nchunks, nparts;
   size_t off_logits, off_stats, off_lse, off_rows, off_misc, off_acc, total;
@@ -733,7 +762,7 @@ Layout layout(int64_t N, int64_t H, int64_t V, int64_t chunk, bool grads, bool a
     off += (bytes + 255) / 256 * 256;
     return o;
   };
-  l.off_logits = take((size_t)l.chunk * V * 2);
+  l.off_logits = take((size_t)l.chunk * logits_ld(V) * 2);
   l.off_stats = take((size_t)l.nparts * l.chunk * sizeof(float2));
   l.off_lse = take((size_t)N * 4);
   l.off_rows = take((size_t)N * 4);
@@ -803,9 +832,9 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   if ((flags & ~(TS_FLCE_ACCUM_BF16 | TS_FLCE_GRADS)) != 0)
     return fail(TS_ERR_INVALID_ARGUMENT, "flce: unknown flags 0x%x", (unsigned)flags);
   const bool acc_bf16 = (flags & TS_FLCE_ACCUM_BF16) != 0;
-  if (N % 8 != 0 || H % 8 != 0 || V % 8 != 0)
-    return fail(TS_ERR_SHAPE, "flce: N, H and V must be multiples of 8 (N=%lld H=%lld V=%lld)",
-                (long long)N, (long long)H, (long long)V);
+  if (N % 8 != 0 || H % 8 != 0)
+    return fail(TS_ERR_SHAPE, "flce: N and H must be multiples of 8 (N=%lld H=%lld)",
+                (long long)N, (long long)H);
   if (ldh < H || ldw < H || ldh % 8 != 0 || ldw % 8 != 0)
     return fail(TS_ERR_SHAPE, "flce: row strides must be >= H and multiples of 8");
   // Buffer offsets are 32-bit and must stay below 2^31: within a 256-row K-major tile
@@ -849,6 +878,7 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
   float* acc32 = reinterpret_cast<float*>(ws + lay.off_acc);
   const __bf16* Hd = static_cast<const __bf16*>(hidden);
   const __bf16* Wd = static_cast<const __bf16*>(weight);
+  const int64_t ldl = logits_ld(V);
 
   hipLaunchKernelGGL(flce_count, dim3(1), dim3(256), 0, st, labels, N, ignore_index, n_valid);
   TS_TRY(ts_host::check_launch("flce_count"));
@@ -872,23 +902,23 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
     g.N = V;
     g.K = H;
     g.C = Lc;
-    g.ldc = V;
+    g.ldc = ldl;
     g.stats = stats;
     TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_gemm_logits"));
     hipLaunchKernelGGL(flce_rows, dim3((unsigned)((Mc + 3) / 4)), dim3(256), 0, st, stats,
-                       lay.nparts, Lc, V, labels + r0, Mc, V, ignore_index, lse_ws + r0,
+                       lay.nparts, Lc, ldl, labels + r0, Mc, V, ignore_index, lse_ws + r0,
                        rows_ws + r0);
     TS_TRY(ts_host::check_launch("flce_rows"));
     if (!grads) continue;
-    const int64_t dchunks = (V / 8 + 256 * kDlKv - 1) / (256 * kDlKv);
-    hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(Mc * dchunks)), dim3(256), 0, st, Lc, V,
+    const int64_t dchunks = ((V + 7) / 8 + 256 * kDlKv - 1) / (256 * kDlKv);
+    hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(Mc * dchunks)), dim3(256), 0, st, Lc, ldl,
                        lse_ws + r0, labels + r0, V, dchunks, ignore_index, scale, (int64_t)0);
     TS_TRY(ts_host::check_launch("flce_dlogits"));
     using ts_gemm::kKMajor;
     using ts_gemm::kMNMajor;
     GemmArgs dh{};
-    dh.A = Lc;  // dlogits [Mc, V], K-major
-    dh.lda = V;
+    dh.A = Lc;  // dlogits [Mc, V], K-major (zero from V to the end of the row's last vector)
+    dh.lda = ldl;
     dh.B = Wd;  // weight [V, H] as the [H, V] operand: MN-major, k = v
     dh.ldb = ldw;
     dh.M = Mc;
@@ -898,7 +928,7 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
     dh.ldc = H;
     GemmArgs dw{};
     dw.A = Lc;             // dlogits [Mc, V] as the [V, Mc] operand: MN-major, k = token
-    dw.lda = V;
+    dw.lda = ldl;
     dw.B = Hd + r0 * ldh;  // hidden rows r0 .. r0 + Mc as the [H, Mc] operand: MN-major
     dw.ldb = ldh;
     dw.M = V;
@@ -1018,9 +1048,8 @@ ts_status check_two_pass(const char* who, const void* hidden, int64_t ldh, const
   if (N < 0 || H <= 0 || V <= 0)
     return fail(TS_ERR_SHAPE, "%s: bad shape N=%lld H=%lld V=%lld", who, (long long)N,
                 (long long)H, (long long)V);
-  if (H % 8 != 0 || V % 8 != 0)
-    return fail(TS_ERR_SHAPE, "%s: H and V must be multiples of 8 (H=%lld V=%lld)", who,
-                (long long)H, (long long)V);
+  if (H % 8 != 0)
+    return fail(TS_ERR_SHAPE, "%s: H must be a multiple of 8 (H=%lld)", who, (long long)H);
   if (ldh < H || ldw < H || ldh % 8 != 0 || ldw % 8 != 0)
     return fail(TS_ERR_SHAPE, "%s: row strides must be >= H and multiples of 8", who);
   // 32-bit buffer offsets within a 256-row K-major tile and a 32-row MN-major k-block
@@ -1097,7 +1126,7 @@ ts_status flce_forward_impl(const char* who, const void* hidden, int64_t ldh, co
   g.zlab = zlab;
   g.xf = xf;
   g.C = static_cast<__bf16*>(logits);  // NULL: the statistics only
-  g.ldc = V;
+  g.ldc = logits_ld(V);
   TS_TRY(launch_gemm<kEpiStats>(g, st, "flce_gemm_stats"));
   hipLaunchKernelGGL(flce_rows_t, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, stats,
                      lay.nparts, zlab, labels, N, V, ignore_index, lse_ws, rows_ws);
@@ -1319,7 +1348,8 @@ extern "C" ts_status ts_flce_backward_kept(const void* hidden, int64_t ldh, cons
     return ts_host::check_launch("fill_zero_u32");
   }
   if (grad_hidden == nullptr && grad_weight == nullptr) return TS_OK;
-  const int64_t dchunks = (V / 8 + 255) / 256;
+  const int64_t ldl = logits_ld(V);
+  const int64_t dchunks = ((V + 7) / 8 + 255) / 256;
   if (N * dchunks > 0x7fffffffLL)
     return fail(TS_ERR_SHAPE, "flce_backward_kept: too many rows for the dz grid");
   const KeptLayout lay = kept_layout(N);
@@ -1337,14 +1367,14 @@ extern "C" ts_status ts_flce_backward_kept(const void* hidden, int64_t ldh, cons
   hipLaunchKernelGGL(flce_dscale, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, labels, N,
                      ignore_index, dloss, dloss_stride, n_valid, reduction == 0 ? 1 : 0, dscale);
   TS_TRY(ts_host::check_launch("flce_dscale"));
-  hipLaunchKernelGGL(flce_dlogits_kept, dim3((unsigned)(N * dchunks)), dim3(256), 0, st, L, V,
+  hipLaunchKernelGGL(flce_dlogits_kept, dim3((unsigned)(N * dchunks)), dim3(256), 0, st, L, ldl,
                      lse, labels, V, dchunks, dscale, xf);
   TS_TRY(ts_host::check_launch("flce_dlogits_kept"));
   using ts_gemm::kKMajor;
   using ts_gemm::kMNMajor;
   GemmArgs dh{};
-  dh.A = L;  // dz [N, V], K-major
-  dh.lda = V;
+  dh.A = L;  // dz [N, V], K-major (rows of ldl, zero from V on)
+  dh.lda = ldl;
   dh.B = static_cast<const __bf16*>(weight);  // weight [V, H] as the [H, V] operand: MN-major
   dh.ldb = ldw;
   dh.M = N;
@@ -1354,7 +1384,7 @@ extern "C" ts_status ts_flce_backward_kept(const void* hidden, int64_t ldh, cons
   dh.ldc = H;
   GemmArgs dw{};
   dw.A = L;  // dz [N, V] as the [V, N] operand: MN-major
-  dw.lda = V;
+  dw.lda = ldl;
   dw.B = static_cast<const __bf16*>(hidden);  // hidden [N, H] as the [H, N] operand: MN-major
   dw.ldb = ldh;
   dw.M = V;

@@ -77,6 +77,28 @@ def _chunk_rows(N: int, V: int, chunk_tokens: Optional[int]) -> int:
     return 0 if rows >= N else rows
 
 
+def _pad_h(hidden: Tensor, weight: Tensor):
+    """The kernels take H in whole 16-byte vectors (8 bf16): for other H, hidden and
+    weight are copied into zero-padded [.., round_up(H, 8)] tensors. The zero columns
+    leave the logits unchanged and receive zero gradients, which the callers slice
+    off. Returns (hidden, weight, H of the caller)."""
+    H = hidden.shape[1]
+    if H % 8 == 0:
+        return hidden, weight, H
+    pad = 8 - H % 8
+    return (torch.nn.functional.pad(hidden, (0, pad)), torch.nn.functional.pad(weight, (0, pad)),
+            H)
+
+
+def _unpad(g: Optional[Tensor], H: int) -> Optional[Tensor]:
+    return g if g is None or g.shape[1] == H else g[:, :H].contiguous()
+
+
+def _logits_ld(V: int) -> int:
+    """Row stride of the bf16 logits the kernels keep: whole 16-byte vectors."""
+    return -(-V // 8) * 8
+
+
 def _operands(what: str, hidden: Tensor, weight: Tensor, labels: Tensor):
     dev = _lib.require_gpu(what, hidden, weight, labels)
     if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
@@ -85,6 +107,7 @@ def _operands(what: str, hidden: Tensor, weight: Tensor, labels: Tensor):
     if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
         raise ValueError(f"{what}: hidden {tuple(hidden.shape)} and weight "
                          f"{tuple(weight.shape)} must be [N, H] and [V, H]")
+    hidden, weight, _ = _pad_h(hidden, weight)
     hidden, weight = _rows_operand(hidden), _rows_operand(weight)
     labels = labels.reshape(-1)
     if labels.shape[0] != hidden.shape[0]:
@@ -104,7 +127,8 @@ def linear_ce_forward(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_ind
     """ts_flce_forward: returns (loss fp32 0-d or None for reduction "none",
     loss_rows fp32 [N], lse fp32 [N]). lse is that of the transformed logits and
     is what linear_ce_backward needs. With keep_logits (ts_flce_forward_keep) a
-    fourth value, the bf16 logits [N, V], for linear_ce_backward(logits=...)."""
+    fourth value, the bf16 logits [N, V] (a view of rows padded to whole 16-byte
+    vectors, row stride round_up(V, 8)), for linear_ce_backward(logits=...)."""
     if reduction not in _REDUCTIONS_2P:
         raise ValueError(f"fused_linear_cross_entropy: reduction must be 'mean', 'sum' or "
                          f"'none', got {reduction!r}")
@@ -125,11 +149,11 @@ def linear_ce_forward(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_ind
             check(lib.ts_flce_forward(*args, ptr(ws), ws_bytes, _lib.stream_handle(dev)),
                   "ts_flce_forward")
         return loss, rows, lse
-    logits = torch.empty((N, V), dtype=torch.bfloat16, device=dev)
+    logits = torch.empty((N, _logits_ld(V)), dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
         check(lib.ts_flce_forward_keep(*args, ptr(logits), ptr(ws), ws_bytes,
                                        _lib.stream_handle(dev)), "ts_flce_forward_keep")
-    return loss, rows, lse, logits
+    return loss, rows, lse, logits[:, :V]
 
 
 def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tensor,
@@ -146,6 +170,7 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
     recomputing, and overwrites them."""
     if reduction not in _REDUCTIONS_2P:
         raise ValueError(f"fused_linear_cross_entropy: bad reduction {reduction!r}")
+    H0 = hidden.shape[-1]
     dev, hidden, weight, labels = _operands("fused_linear_cross_entropy", hidden, weight, labels)
     N, H = hidden.shape
     V = weight.shape[0]
@@ -160,9 +185,10 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
     lib = _lib.load()
     if logits is not None:
         if (logits.shape != (N, V) or logits.dtype != torch.bfloat16 or logits.device != dev or
-                not logits.is_contiguous()):
-            raise ValueError(f"fused_linear_cross_entropy: kept logits must be contiguous bf16 "
-                             f"[{N}, {V}] on {dev}")
+                (N > 0 and (logits.stride(1) != 1 or logits.stride(0) != _logits_ld(V)))):
+            raise ValueError(f"fused_linear_cross_entropy: kept logits must be bf16 [{N}, {V}] "
+                             f"on {dev} with row stride {_logits_ld(V)} (as linear_ce_forward "
+                             f"returns them)")
         ws_bytes = int(lib.ts_flce_backward_kept_workspace_size(N))
         ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
@@ -172,7 +198,7 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
                 float(logit_scaling), float(temperature), ptr(lse), ptr(dloss), stride,
                 ptr(logits), ptr(gh), ptr(gw), ptr(ws), ws_bytes, _lib.stream_handle(dev)),
                 "ts_flce_backward_kept")
-        return gh, gw
+        return _unpad(gh, H0), _unpad(gw, H0)
     chunk = int(vocab_chunk) if vocab_chunk else 0
     ws_bytes = int(lib.ts_flce_backward_workspace_size(N, H, V, chunk))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
@@ -182,7 +208,7 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
             int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
             float(logit_scaling), float(temperature), ptr(lse), ptr(dloss), stride, ptr(gh),
             ptr(gw), chunk, ptr(ws), ws_bytes, _lib.stream_handle(dev)), "ts_flce_backward")
-    return gh, gw
+    return _unpad(gh, H0), _unpad(gw, H0)
 
 
 def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
@@ -207,6 +233,13 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
     if reduction not in _REDUCTIONS:
         raise ValueError(f"fused_linear_cross_entropy: reduction must be 'mean' or 'sum', "
                          f"got {reduction!r}")
+    if hidden.shape[1] % 8 != 0:
+        H0 = hidden.shape[1]
+        hp, wp, _ = _pad_h(hidden, weight)
+        loss, rows, lse, gh, gw = linear_ce_forward_backward(
+            hp, wp, labels, ignore_index, reduction, need_grad_hidden, need_grad_weight,
+            chunk_tokens, grad_weight_accum)
+        return loss, rows, lse, _unpad(gh, H0), _unpad(gw, H0)
     if hidden.stride(1) != 1 or (hidden.shape[0] > 1 and hidden.stride(0) % 8 != 0):
         hidden = hidden.contiguous()
     if weight.stride(1) != 1 or (weight.shape[0] > 1 and weight.stride(0) % 8 != 0):
