@@ -15,6 +15,16 @@ indices. A small C++ driver compiled with g++ sweeps many shapes and checks:
 * register plans cover every 16-byte vector of the row and stay within the
   template instantiations the launcher has;
 * the grouped GEMM tile order visits every output tile exactly once;
+* the streaming kernels' vector index (ts_plan::chunk_vec over the grid chunks_for
+  gives; SwiGLU, the CE and vocabulary-shard backward, dlogits, dz, scale) and the
+  CE forward's chunk-then-tail row loop visit every vector of a row exactly once,
+  buffer offsets of register rows (vec_boffset) stay inside their resource or use
+  the offset no resource covers, and row kernels' row_vec_in admits only vectors
+  inside the matrix;
+* every RoPE task of a workgroup (rope_task, and the token kernel's rope_head_task)
+  maps to one (token slot, head, index) in range, each once, and its elements
+  (rope_elems) lie inside the head, for the vector and generic paths and both
+  layouts;
 * RoPE workgroups are whole waves within 256..1024 threads and their cos/sin
   staging fits the LDS bound;
 * umulhi(n, ceil(2^32/d)) == n / d wherever magic_exact(n_max, d) admits it,
@@ -198,6 +208,107 @@ int main() {
         if (nn >= nmax) break;
         const unsigned long long n = (unsigned long long)nn;
         CHECK(magic64_div(n, mg) == q && magic64_div(n - 1, mg) == q - 1, "magic64 edge %llu*%llu", q, d);
+      }
+    }
+  }
+  // Streaming kernels: chunk_vec over the grid chunks_for gives (SwiGLU, CE and
+  // vocabulary-shard backward, dlogits, dz, scale sweeps) visits every vector of
+  // [0, nvec) exactly once; accesses are guarded by v < nvec
+  for (int threads : {64, 256, 1024}) {
+    for (int kv : {1, 2, 4, 16}) {
+      for (long long nvec : {1ll, 7ll, 63ll, 64ll, 255ll, 256ll, 257ll, 1000ll, 1024ll, 4097ll,
+                             16032ll, 16033ll}) {
+        std::vector<int> seen(nvec, 0);
+        const long long chunks = chunks_for(nvec, threads, kv);
+        CHECK(chunks * threads * kv >= nvec && (chunks - 1) * threads * kv < nvec,
+              "chunks_for(%lld, %d, %d) = %lld", nvec, threads, kv, chunks);
+        for (long long c = 0; c < chunks; ++c)
+          for (int k = 0; k < kv; ++k)
+            for (int t = 0; t < threads; ++t) {
+              const long long v = chunk_vec(c, k, t, threads, kv);
+              CHECK(v >= 0, "negative vector index");
+              if (v < nvec) seen[v]++;
+            }
+        for (long long v = 0; v < nvec; ++v)
+          CHECK(seen[v] == 1, "nvec=%lld threads=%d kv=%d: vector %lld visited %d times", nvec,
+                threads, kv, v, seen[v]);
+        // the row loop of ce_fwd_vec: whole chunks, then the tail of chunk `full`
+        // stepping by `threads` from chunk_vec(full, 0, t, ...)
+        std::vector<int> seen2(nvec, 0);
+        const long long full = nvec / ((long long)threads * kv);
+        for (long long c = 0; c < full; ++c)
+          for (int k = 0; k < kv; ++k)
+            for (int t = 0; t < threads; ++t) seen2[chunk_vec(c, k, t, threads, kv)]++;
+        for (int t = 0; t < threads; ++t)
+          for (long long v = chunk_vec(full, 0, t, threads, kv); v < nvec; v += threads) seen2[v]++;
+        for (long long v = 0; v < nvec; ++v) CHECK(seen2[v] == 1, "row loop visits %lld %d times", v, seen2[v]);
+        // buffer offsets of register rows (ce_fused_vec, shard stats): inside a
+        // resource of nvec vectors, or an offset no such resource covers
+        for (int vb : {16, 32}) {
+          if ((long long)nvec * vb >= (1ll << 31)) continue;
+          for (long long v = 0; v < nvec + 3 * threads; ++v) {
+            const int32_t o = vec_boffset(v, nvec, vb);
+            if (v < nvec) CHECK(o == v * vb && o + vb <= nvec * vb, "boffset in range");
+            else CHECK(o == kNoAccess && (uint32_t)o >= (uint64_t)nvec * vb, "boffset past the row");
+          }
+        }
+      }
+    }
+  }
+  // Row kernels (RMSNorm forward and add): row_vec_in admits exactly the vectors of
+  // the matrix, whose element ranges lie inside [rows, ld]
+  for (long long rows : {1ll, 3ll, 37ll}) {
+    for (long long nvec : {1ll, 5ll, 64ll, 513ll}) {
+      for (int V : {4, 8}) {
+        for (long long ld : {nvec * V, nvec * V + V}) {
+          const long long extent = (rows - 1) * ld + nvec * V;
+          for (long long row = 0; row < rows + 2; ++row)
+            for (long long v = 0; v < nvec + 70; ++v) {
+              const bool in = row_vec_in(row, rows, v, nvec);
+              CHECK(in == (row < rows && v < nvec), "row_vec_in");
+              if (in) CHECK(row * ld + v * V + V <= extent, "row vector past the matrix");
+            }
+        }
+      }
+    }
+  }
+  // RoPE: every task f < tpb * tasks_per_token of a workgroup maps to one
+  // (token slot, head, index) in range, each exactly once, and its elements lie
+  // inside the head; the token kernel's per-token split likewise
+  for (int heads : {1, 2, 3, 8, 9, 40, 72}) {
+    for (int D : {2, 8, 16, 64, 128, 256, 512}) {
+      const int half = D / 2;
+      for (int W : {1, 4, 8}) {           // element width: 1 = generic path
+        for (int il = 0; il < 2; ++il) {  // NeoX or interleaved
+          const bool inter = il == 1;
+          if (W > 1 && (inter ? D % W != 0 : half % W != 0)) continue;
+          const int tph = W == 1 ? half : (inter ? 2 * half / W : half / W);
+          const long long tpt = (long long)tph * heads;
+          if (tpt >= (1 << 20)) continue;
+          const RopeBlock blk = rope_block(tpt, half, 1024, 4096);
+          const long long total = (long long)blk.tpb * tpt;
+          if (!magic_exact((uint64_t)total, (uint64_t)tpt) || !magic_exact((uint64_t)tpt, (uint64_t)tph)) continue;
+          const uint32_t mt = magic_for((uint32_t)tpt), mh = magic_for((uint32_t)tph);
+          std::vector<char> hit(total, 0);
+          for (long long f = 0; f < total; ++f) {
+            const RopeTask t = rope_task((int)f, (int)tpt, mt, tph, mh);
+            const bool ok = t.i >= 0 && t.i < blk.tpb && t.hh >= 0 && t.hh < heads && t.j >= 0 && t.j < tph;
+            CHECK(ok, "rope task %lld of %d heads D=%d W=%d: (%d, %d, %d)", f, heads, D, W, t.i, t.hh, t.j);
+            if (!ok) continue;
+            const long long id = ((long long)t.i * heads + t.hh) * tph + t.j;
+            CHECK(!hit[id], "rope task visited twice");
+            hit[id] = 1;
+            const RopeElems e = rope_elems(t.j, W, half, inter);
+            const int w1 = W == 1 ? 1 : W;
+            CHECK(e.e1 >= 0 && e.e1 + w1 <= D, "rope e1 %d (D=%d W=%d)", e.e1, D, W);
+            if (W == 1 || !inter) CHECK(e.e2 >= 0 && e.e2 + w1 <= D, "rope e2 %d (D=%d W=%d)", e.e2, D, W);
+            if (!inter) CHECK(e.e2 == e.e1 + half || (W == 1 && e.e2 == e.e1 + half), "NeoX pair");
+            if (t.i == 0 && f < tpt) {
+              const RopeTask u = rope_head_task((int)f, tph, mh);
+              CHECK(u.hh == t.hh && u.j == t.j, "token-kernel task split");
+            }
+          }
+        }
       }
     }
   }

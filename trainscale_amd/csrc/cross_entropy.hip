@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include "common.hpp"
+#include "plan.hpp"
 
 namespace {
 
@@ -100,12 +101,14 @@ __global__ __launch_bounds__(kThreads) void ce_fwd_vec(const T* __restrict__ log
   }
   const T* xr = logits + row * ld;
   float m = -INFINITY, s = 0.f, sz = 0.f;
-  const int64_t step = (int64_t)kThreads * kUnroll;
-  int64_t base = 0;
-  for (; base + step <= nvec; base += step) {
+  // whole chunks of kThreads * kUnroll vectors (ts_plan::chunk_vec), then the rest
+  const int64_t full = nvec / ((int64_t)kThreads * kUnroll);
+  int64_t c = 0;
+  for (; c < full; ++c) {
     u32x4 buf[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) buf[u] = ld16_stream(xr + (base + u * kThreads + threadIdx.x) * VE);
+    for (int u = 0; u < kUnroll; ++u)
+      buf[u] = ld16_stream(xr + ts_plan::chunk_vec(c, u, threadIdx.x, kThreads, kUnroll) * VE);
     float z[kUnroll][VE];
     float lm = -INFINITY;
 #pragma unroll
@@ -130,7 +133,8 @@ __global__ __launch_bounds__(kThreads) void ce_fwd_vec(const T* __restrict__ log
       for (int i = 0; i < VE; ++i) s += fast_exp2(__builtin_fmaf(z[u][i], kLog2e, -mb));
   }
   // Tail: fewer than kThreads*kUnroll vectors remain.
-  for (int64_t v = base + threadIdx.x; v < nvec; v += kThreads) {
+  for (int64_t v = ts_plan::chunk_vec(c, 0, threadIdx.x, kThreads, kUnroll); v < nvec;
+       v += kThreads) {  // chunk_vec(c, u, ...) for u = 0, 1, ...
     float z[VE];
     Elt<T>::unpack(ld16_stream(xr + v * VE), z);
     float lm = -INFINITY;
@@ -264,13 +268,15 @@ __global__ __launch_bounds__(kThreads) void ce_bwd_vec(
   const int64_t row = row0 + blockIdx.y;
   const int64_t label = labels[row];
   G* gr = grad + row * ld_grad;
-  const int64_t base = (int64_t)blockIdx.x * kThreads * kBwdKv + threadIdx.x;
+  int64_t vk[kBwdKv];  // this thread's vectors of the row (ts_plan::chunk_vec)
+#pragma unroll
+  for (int k = 0; k < kBwdKv; ++k)
+    vk[k] = ts_plan::chunk_vec(blockIdx.x, k, threadIdx.x, kThreads, kBwdKv);
   if (label == ignore_index) {
     const float zero[VE] = {};
 #pragma unroll
     for (int k = 0; k < kBwdKv; ++k) {
-      const int64_t v = base + (int64_t)k * kThreads;
-      if (v < nvec) store_grad<G, VE>(gr + v * VE, zero);
+      if (vk[k] < nvec) store_grad<G, VE>(gr + vk[k] * VE, zero);
     }
     return;
   }
@@ -283,12 +289,12 @@ __global__ __launch_bounds__(kThreads) void ce_bwd_vec(
   u32x4 buf[kBwdKv];
 #pragma unroll
   for (int k = 0; k < kBwdKv; ++k) {
-    const int64_t v = base + (int64_t)k * kThreads;
+    const int64_t v = vk[k];
     buf[k] = v < nvec ? ld16_stream(xr + v * VE) : u32x4{0, 0, 0, 0};
   }
 #pragma unroll
   for (int k = 0; k < kBwdKv; ++k) {
-    const int64_t v = base + (int64_t)k * kThreads;
+    const int64_t v = vk[k];
     if (v < nvec) {
       float x[VE], g[VE];
       Elt<T>::unpack(buf[k], x);
@@ -346,10 +352,11 @@ constexpr int kFusedThreads = 1024;
 constexpr int kFusedWaves = kFusedThreads / kWave;
 constexpr int kFusedKv = 16;
 
-// Byte offset of this thread's k-th vector, kBufOob past the row end.
+// Byte offset of this thread's k-th vector, past the row end one no row resource
+// covers (ts_plan::vec_boffset: the hardware drops such stores, loads read 0).
 __device__ inline int fused_voff(int k, int nvec, int vec_bytes) {
-  const int v = threadIdx.x + k * kFusedThreads;
-  return v < nvec ? v * vec_bytes : kBufOob;
+  return ts_plan::vec_boffset(ts_plan::chunk_vec(0, k, threadIdx.x, kFusedThreads, kFusedKv),
+                              nvec, vec_bytes);
 }
 
 // Row lse (and, with kSmooth, the row sum of z) from every thread's online
@@ -646,7 +653,7 @@ ts_status bwd_typed(const void* logits, int64_t ld, const int64_t* labels, const
   if (xform_on == X && smooth == S) {                                                          \
     if (vec) {                                                                                 \
       const int64_t nvec = V / VE;                                                             \
-      const unsigned gx = (unsigned)((nvec + kThreads * kBwdKv - 1) / (kThreads * kBwdKv));    \
+      const unsigned gx = (unsigned)ts_plan::chunks_for(nvec, kThreads, kBwdKv);    \
       for (int64_t r0 = 0; r0 < N; r0 += kMaxGridY) {                                          \
         const unsigned gy = (unsigned)(N - r0 < kMaxGridY ? N - r0 : kMaxGridY);               \
         hipLaunchKernelGGL((ce_bwd_vec<T, G, X, S>), dim3(gx, gy), block, 0, st, lp, ld,       \

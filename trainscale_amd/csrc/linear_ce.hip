@@ -596,7 +596,10 @@ __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int6
                                                     const float* __restrict__ scale_p,
                                                     int64_t label_offset) {
   const int64_t r = (int64_t)blockIdx.x / chunks;
-  const int64_t c0 = ((int64_t)blockIdx.x % chunks) * (256 * kDlKv) + threadIdx.x;
+  const int64_t c = (int64_t)blockIdx.x % chunks;
+  int64_t vk[kDlKv];  // this thread's vectors of row r (ts_plan::chunk_vec)
+#pragma unroll
+  for (int u = 0; u < kDlKv; ++u) vk[u] = ts_plan::chunk_vec(c, u, threadIdx.x, 256, kDlKv);
   const int64_t nvec = (V + 7) / 8;
   const int64_t raw = labels[r];
   const int64_t lab = raw - label_offset;  // the label's column in these logits
@@ -605,7 +608,7 @@ __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int6
     const u32x4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < kDlKv; ++u) {
-      const int64_t v = c0 + u * 256;
+      const int64_t v = vk[u];
       if (v < nvec) st16_stream(row + v * 8, zero);
     }
     return;
@@ -613,14 +616,14 @@ __global__ __launch_bounds__(256) void flce_dlogits(__bf16* __restrict__ L, int6
   u32x4 q[kDlKv];
 #pragma unroll
   for (int u = 0; u < kDlKv; ++u) {
-    const int64_t v = c0 + u * 256;
+    const int64_t v = vk[u];
     if (v < nvec) q[u] = ld16_stream(row + v * 8);
   }
   const float scale = *scale_p;
   const float l2 = lse[r] * kLog2e;
 #pragma unroll
   for (int u = 0; u < kDlKv; ++u) {
-    const int64_t v = c0 + u * 256;
+    const int64_t v = vk[u];
     if (v < nvec) {
       float z[8], g[8];
       Elt<__bf16>::unpack(q[u], z);
@@ -649,7 +652,7 @@ __global__ __launch_bounds__(256) void flce_dlogits_kept(__bf16* __restrict__ L,
                                                          const float* __restrict__ dscale,
                                                          LogitXform xf) {
   const int64_t r = (int64_t)blockIdx.x / chunks;
-  const int64_t v = ((int64_t)blockIdx.x % chunks) * 256 + threadIdx.x;
+  const int64_t v = ts_plan::chunk_vec((int64_t)blockIdx.x % chunks, 0, threadIdx.x, 256, 1);
   if (v >= (V + 7) / 8) return;
   __bf16* p = L + r * ldl + v * 8;
   const float ds = dscale[r];
@@ -709,8 +712,10 @@ __global__ __launch_bounds__(256) void scale_inplace(T* __restrict__ x, int64_t 
     *hint_out = (__builtin_isfinite(g) && g != 0.f) ? g : 1.f;
   const float s = den != nullptr ? g / *den : g;
   if (s == 1.f) return;
+  // sweep n takes chunk blockIdx.x + n * gridDim.x: v0 + u * 256 is
+  // ts_plan::chunk_vec(chunk, u, threadIdx.x, 256, kScaleUnroll)
   const int64_t stride = (int64_t)gridDim.x * 256 * kScaleUnroll;
-  for (int64_t v0 = (int64_t)blockIdx.x * 256 * kScaleUnroll + threadIdx.x; v0 < nvec;
+  for (int64_t v0 = ts_plan::chunk_vec(blockIdx.x, 0, threadIdx.x, 256, kScaleUnroll); v0 < nvec;
        v0 += stride) {
     u32x4 q[kScaleUnroll];
 #pragma unroll
@@ -910,7 +915,7 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
                        rows_ws + r0);
     TS_TRY(ts_host::check_launch("flce_rows"));
     if (!grads) continue;
-    const int64_t dchunks = ((V + 7) / 8 + 256 * kDlKv - 1) / (256 * kDlKv);
+    const int64_t dchunks = ts_plan::chunks_for((V + 7) / 8, 256, kDlKv);
     hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(Mc * dchunks)), dim3(256), 0, st, Lc, ldl,
                        lse_ws + r0, labels + r0, V, dchunks, ignore_index, scale, (int64_t)0);
     TS_TRY(ts_host::check_launch("flce_dlogits"));
@@ -1349,7 +1354,7 @@ extern "C" ts_status ts_flce_backward_kept(const void* hidden, int64_t ldh, cons
   }
   if (grad_hidden == nullptr && grad_weight == nullptr) return TS_OK;
   const int64_t ldl = logits_ld(V);
-  const int64_t dchunks = ((V + 7) / 8 + 255) / 256;
+  const int64_t dchunks = ts_plan::chunks_for((V + 7) / 8, 256, 1);
   if (N * dchunks > 0x7fffffffLL)
     return fail(TS_ERR_SHAPE, "flce_backward_kept: too many rows for the dz grid");
   const KeptLayout lay = kept_layout(N);
@@ -1537,7 +1542,7 @@ extern "C" ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const vo
                      reduction == 0 ? 1 : 0, loss, scale);
   TS_TRY(ts_host::check_launch("flce_loss"));
   if (grad_hidden_partial == nullptr && grad_weight_shard == nullptr) return TS_OK;
-  const int64_t dchunks = (Vp / 8 + 256 * kDlKv - 1) / (256 * kDlKv);
+  const int64_t dchunks = ts_plan::chunks_for(Vp / 8, 256, kDlKv);
   hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(N * dchunks)), dim3(256), 0, st, L, Vp,
                      lse_ws, labels, Vp, dchunks, ignore_index, scale, vocab_start);
   TS_TRY(ts_host::check_launch("flce_dlogits"));

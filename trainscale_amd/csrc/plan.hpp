@@ -219,13 +219,17 @@ inline RopeBlock rope_block(int64_t tasks_per_token, int half, int max_threads, 
 // Magic-number division used by the RoPE task decomposition:
 // q = umulhi(n, ceil(2^32 / d)) equals n / d whenever n * d < 2^32 and d > 1.
 // ceil(2^32 / 1) does not fit 32 bits, so d == 1 is encoded as magic 0 and
-// divides by returning n (the device code makes the same choice).
+// divides by returning n. The kernels divide with magic_div too.
 // ---------------------------------------------------------------------------
 inline uint32_t magic_for(uint32_t d) {
   return d <= 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + d - 1) / d);
 }
-inline uint32_t magic_div(uint32_t n, uint32_t magic) {
+TS_HOST_DEVICE inline uint32_t magic_div(uint32_t n, uint32_t magic) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return magic == 0 ? n : __umulhi(n, magic);
+#else
   return magic == 0 ? n : (uint32_t)(((uint64_t)n * magic) >> 32);
+#endif
 }
 inline bool magic_exact(uint64_t n_max, uint64_t d) { return n_max * d < ((uint64_t)1 << 32); }
 
@@ -268,6 +272,78 @@ TS_HOST_DEVICE inline void gemm_tile_of(int64_t bid, int64_t MT, int64_t NT, int
   const int64_t gm = MT - g * kGemmGroupM < kGemmGroupM ? MT - g * kGemmGroupM : kGemmGroupM;
   mt = g * kGemmGroupM + w % gm;
   nt = w / gm;
+}
+
+// ---------------------------------------------------------------------------
+// Addressing of the streaming and row kernels. The kernels compute their
+// accesses with these functions, and tests/test_plan.py sweeps them with the
+// launch shapes the host computes: every access lies inside its tensor and
+// every element is visited once.
+// ---------------------------------------------------------------------------
+
+// Vector index that thread tid handles as its k-th vector of chunk c, for chunks
+// of threads * kv consecutive 16-byte vectors whose k-th vectors lie `threads`
+// apart (one wave's load instruction then covers 1 KiB of consecutive memory).
+// Kernels touch it only when it is < the vector count.
+TS_HOST_DEVICE inline int64_t chunk_vec(int64_t c, int k, int tid, int threads, int kv) {
+  return c * threads * kv + tid + (int64_t)k * threads;
+}
+
+// Chunks of threads * kv vectors that cover nvec vectors.
+TS_HOST_DEVICE inline int64_t chunks_for(int64_t nvec, int threads, int kv) {
+  const int64_t per = (int64_t)threads * kv;
+  return (nvec + per - 1) / per;
+}
+
+// Whether 16-byte vector v of row `row` lies inside a matrix of `rows` rows of
+// nvec vectors (row and v are non-negative by construction); a kernel then
+// accesses row * ld + v * V elements from the matrix's start.
+TS_HOST_DEVICE inline bool row_vec_in(int64_t row, int64_t rows, int64_t v, int64_t nvec) {
+  return row < rows && v < nvec;
+}
+
+// Byte offset of vector v for a buffer resource spanning nvec vectors of
+// vec_bytes each, or kNoAccess past them: an offset no resource of this size
+// covers (bit pattern 0x80000000), so the hardware drops the store or returns
+// zeros. Requires nvec * vec_bytes < 2^31 (the hosts check).
+constexpr int32_t kNoAccess = (int32_t)(-2147483647 - 1);
+TS_HOST_DEVICE inline int32_t vec_boffset(int64_t v, int64_t nvec, int vec_bytes) {
+  return v >= 0 && v < nvec ? (int32_t)(v * vec_bytes) : kNoAccess;
+}
+
+// A RoPE task f of a workgroup: token slot i (0 .. tpb - 1), head hh (Q heads,
+// then K heads) and j, its index within the head (a 16-byte vector pair on the
+// vector path, a rotation pair on the generic path). The divisions are
+// magic-number ones (magic_div), exact whenever f < tpb * tasks_per_token and
+// the host's magic_exact checks hold.
+struct RopeTask {
+  int i, hh, j;
+};
+// Head and index within the head of task r of one token.
+TS_HOST_DEVICE inline RopeTask rope_head_task(int r, int tasks_per_head, uint32_t tph_magic) {
+  RopeTask t;
+  t.i = 0;
+  t.hh = (int)magic_div((uint32_t)r, tph_magic);
+  t.j = r - t.hh * tasks_per_head;
+  return t;
+}
+TS_HOST_DEVICE inline RopeTask rope_task(int f, int tasks_per_token, uint32_t tpt_magic,
+                                         int tasks_per_head, uint32_t tph_magic) {
+  const int i = (int)magic_div((uint32_t)f, tpt_magic);
+  RopeTask t = rope_head_task(f - i * tasks_per_token, tasks_per_head, tph_magic);
+  t.i = i;
+  return t;
+}
+
+// Element offsets within its head of the two vectors (or elements) a RoPE task
+// reads and writes: NeoX pairs (e, e + half), interleaved adjacent pairs in one
+// vector (e2 unused, -1). `width` is the vector width (1 on the generic path).
+struct RopeElems {
+  int e1, e2;
+};
+TS_HOST_DEVICE inline RopeElems rope_elems(int j, int width, int half, bool interleaved) {
+  if (width == 1) return interleaved ? RopeElems{2 * j, 2 * j + 1} : RopeElems{j, j + half};
+  return interleaved ? RopeElems{j * width, -1} : RopeElems{j * width, half + j * width};
 }
 
 }  // namespace ts_plan

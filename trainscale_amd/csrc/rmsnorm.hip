@@ -109,19 +109,23 @@ __global__ __launch_bounds__(TPR > 256 ? TPR : 256) void rms_fwd_reg(
   const int64_t row = (int64_t)blockIdx.x * kRpb + sub;
   const bool valid = row < rows;
 
+  // this thread's vectors of the row (ts_plan::chunk_vec), accessed where
+  // ts_plan::row_vec_in holds
   const T* xr = x + row * ldx;
   u32x4 xv[KV], rv[KR];
 #pragma unroll
   for (int k = 0; k < KV; ++k) {
-    const int v = t + k * TPR;
-    xv[k] = valid && v < nvec ? ld16_stream(xr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+    const int v = (int)ts_plan::chunk_vec(0, k, t, TPR, KV);
+    xv[k] = ts_plan::row_vec_in(row, rows, v, nvec) ? ld16_stream(xr + (int64_t)v * V)
+                                                    : u32x4{0, 0, 0, 0};
   }
   if constexpr (kAdd) {
     const T* rr = add.r + row * add.ldr;
 #pragma unroll
     for (int k = 0; k < KV; ++k) {
-      const int v = t + k * TPR;
-      rv[k] = valid && v < nvec ? ld16_stream(rr + (int64_t)v * V) : u32x4{0, 0, 0, 0};
+      const int v = (int)ts_plan::chunk_vec(0, k, t, TPR, KV);
+      rv[k] = ts_plan::row_vec_in(row, rows, v, nvec) ? ld16_stream(rr + (int64_t)v * V)
+                                                      : u32x4{0, 0, 0, 0};
     }
   } else {
     rv[0] = u32x4{0, 0, 0, 0};

@@ -60,12 +60,6 @@ struct RopeArgs {
   float inv_freq[kMaxHalf];
 };
 
-// n / d as umulhi(n, ceil(2^32 / d)), magic 0 meaning d == 1 (ts_plan::magic_for);
-// exact while n * d < 2^32, which the host checks for every launch.
-__device__ inline uint32_t fast_div(uint32_t n, uint32_t magic) {
-  return magic == 0 ? n : __umulhi(n, magic);
-}
-
 template <typename TabT>
 __device__ inline float tab_load(const void* p, int64_t idx) {
   return Elt<TabT>::load1(static_cast<const TabT*>(p) + idx);
@@ -124,10 +118,13 @@ struct Task {
 template <typename T>
 __device__ inline Task<T> task_at(const RopeArgs& a, int64_t tok0, int f) {
   Task<T> k;
-  k.i = (int)fast_div((uint32_t)f, a.tpt_magic);
-  const int r = f - k.i * a.tasks_per_token;
-  const int hh = (int)fast_div((uint32_t)r, a.tph_magic);
-  k.j = r - hh * a.tasks_per_head;
+  // n / d as umulhi(n, ceil(2^32 / d)) (ts_plan::magic_div), exact while n * d < 2^32,
+  // which the host checks for every launch
+  const ts_plan::RopeTask rt =
+      ts_plan::rope_task(f, a.tasks_per_token, a.tpt_magic, a.tasks_per_head, a.tph_magic);
+  k.i = rt.i;
+  const int hh = rt.hh;
+  k.j = rt.j;
   const int64_t t = tok0 + k.i;
   const int64_t b = t / a.S;
   const int64_t sq = t - b * a.S;
@@ -150,13 +147,9 @@ __device__ inline Task<T> task_at(const RopeArgs& a, int64_t tok0, int f) {
 template <typename T, bool kInterleaved>
 __device__ inline void task_load(const RopeArgs& a, const Task<T>& k, u32x4& v1, u32x4& v2) {
   constexpr int V = Elt<T>::kVec;
-  if constexpr (!kInterleaved) {
-    v1 = ld16_stream(k.src + k.j * V);
-    v2 = ld16_stream(k.src + a.half + k.j * V);
-  } else {
-    v1 = ld16_stream(k.src + k.j * V);
-    v2 = u32x4{0, 0, 0, 0};
-  }
+  const ts_plan::RopeElems e = ts_plan::rope_elems(k.j, V, a.half, kInterleaved);
+  v1 = ld16_stream(k.src + e.e1);
+  v2 = kInterleaved ? u32x4{0, 0, 0, 0} : ld16_stream(k.src + e.e2);
 }
 
 template <typename T, bool kInterleaved>
@@ -165,8 +158,9 @@ __device__ inline void task_rotate_store(const RopeArgs& a, const Task<T>& k, co
   constexpr int V = Elt<T>::kVec;
   const float* crow = cs + k.i * a.half;
   const float* srow = sn + k.i * a.half;
+  const ts_plan::RopeElems el = ts_plan::rope_elems(k.j, V, a.half, kInterleaved);
   if constexpr (!kInterleaved) {
-    const int e1 = k.j * V;
+    const int e1 = el.e1;
     float x1[V], x2[V], o1[V], o2[V];
     Elt<T>::unpack(v1, x1);
     Elt<T>::unpack(v2, x2);
@@ -178,9 +172,9 @@ __device__ inline void task_rotate_store(const RopeArgs& a, const Task<T>& k, co
       o2[p] = x2[p] * c + x1[p] * s;
     }
     st16_stream(k.dst + e1, Elt<T>::pack(o1));
-    st16_stream(k.dst + a.half + e1, Elt<T>::pack(o2));
+    st16_stream(k.dst + el.e2, Elt<T>::pack(o2));
   } else {
-    const int e = k.j * V;
+    const int e = el.e1;
     float x[V], o[V];
     Elt<T>::unpack(v1, x);
 #pragma unroll
@@ -244,9 +238,10 @@ __global__ __launch_bounds__(kMaxThreads) void rope_tok_kernel(const RopeArgs a)
   const int64_t k_in_sh = a.k_in_sh, k_out_sh = a.k_out_sh;
   auto task = [&](int f) {
     Task<T> k;
-    const int hh = (int)fast_div((uint32_t)f, a.tph_magic);
+    const ts_plan::RopeTask rt = ts_plan::rope_head_task(f, a.tasks_per_head, a.tph_magic);
+    const int hh = rt.hh;
     k.i = 0;
-    k.j = f - hh * a.tasks_per_head;
+    k.j = rt.j;
     const bool is_q = hh < a.Hq;  // a select, not a branch (see task_at)
     const T* src_q = qi + hh * q_in_sh;
     T* dst_q = qo + hh * q_out_sh;
@@ -295,8 +290,9 @@ __global__ __launch_bounds__(kMaxThreads) void rope_generic_kernel(const RopeArg
   for (int f = threadIdx.x; f < total; f += blockDim.x) {
     const Task<T> k = task_at<T>(a, tok0, f);
     const int p = k.j;  // pair index
-    const int e1 = kInterleaved ? 2 * p : p;
-    const int e2 = kInterleaved ? 2 * p + 1 : p + a.half;
+    const ts_plan::RopeElems el = ts_plan::rope_elems(p, 1, a.half, kInterleaved);
+    const int e1 = el.e1;
+    const int e2 = el.e2;
     const float x1 = Elt<T>::load1(k.src + e1);
     const float x2 = Elt<T>::load1(k.src + e2);
     const float c = cs[k.i * a.half + p];

@@ -15,6 +15,7 @@
 // within 1 ulp); for g below about -88 the exponential overflows to +inf and
 // sigmoid is 0, for g above about 104 it is exactly 1.
 #include "common.hpp"
+#include "plan.hpp"
 
 namespace {
 
@@ -49,11 +50,14 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_fwd_vec(const T* __restric
                                                               const T* __restrict__ up,
                                                               T* __restrict__ out, int64_t nvec) {
   constexpr int VE = Elt<T>::kVec;
-  const int64_t v0 = (int64_t)blockIdx.x * kSwiThreads * kSwiKv + threadIdx.x;
+  int64_t vk[kSwiKv];  // this thread's vectors (ts_plan::chunk_vec)
+#pragma unroll
+  for (int k = 0; k < kSwiKv; ++k)
+    vk[k] = ts_plan::chunk_vec(blockIdx.x, k, threadIdx.x, kSwiThreads, kSwiKv);
   u32x4 gq[kSwiKv], uq[kSwiKv];
 #pragma unroll
   for (int k = 0; k < kSwiKv; ++k) {
-    const int64_t v = v0 + k * kSwiThreads;
+    const int64_t v = vk[k];
     if (v < nvec) {
       gq[k] = ld16_stream(gate + v * VE);
       uq[k] = ld16_stream(up + v * VE);
@@ -61,7 +65,7 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_fwd_vec(const T* __restric
   }
 #pragma unroll
   for (int k = 0; k < kSwiKv; ++k) {
-    const int64_t v = v0 + k * kSwiThreads;
+    const int64_t v = vk[k];
     if (v < nvec) {
       float g[VE], u[VE];
       Elt<T>::unpack(gq[k], g);
@@ -78,11 +82,14 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_vec(
     const T* __restrict__ dout, const T* __restrict__ gate, const T* __restrict__ up,
     T* __restrict__ dgate, T* __restrict__ dup, int64_t nvec) {
   constexpr int VE = Elt<T>::kVec;
-  const int64_t v0 = (int64_t)blockIdx.x * kSwiThreads * kSwiKv + threadIdx.x;
+  int64_t vk[kSwiKv];  // this thread's vectors (ts_plan::chunk_vec)
+#pragma unroll
+  for (int k = 0; k < kSwiKv; ++k)
+    vk[k] = ts_plan::chunk_vec(blockIdx.x, k, threadIdx.x, kSwiThreads, kSwiKv);
   u32x4 dq[kSwiKv], gq[kSwiKv], uq[kSwiKv];
 #pragma unroll
   for (int k = 0; k < kSwiKv; ++k) {
-    const int64_t v = v0 + k * kSwiThreads;
+    const int64_t v = vk[k];
     if (v < nvec) {
       dq[k] = ld16_stream(dout + v * VE);
       gq[k] = ld16_stream(gate + v * VE);
@@ -91,7 +98,7 @@ __global__ __launch_bounds__(kSwiThreads) void swiglu_bwd_vec(
   }
 #pragma unroll
   for (int k = 0; k < kSwiKv; ++k) {
-    const int64_t v = v0 + k * kSwiThreads;
+    const int64_t v = vk[k];
     if (v < nvec) {
       float d[VE], g[VE], u[VE];
       Elt<T>::unpack(dq[k], d);
@@ -138,7 +145,7 @@ ts_status fwd_typed(const void* gate, const void* up, void* out, int64_t n, hipS
   if (n % VE == 0 && ts_host::aligned16(gate) && ts_host::aligned16(up) &&
       ts_host::aligned16(out)) {
     const int64_t nvec = n / VE;
-    const int64_t blocks = (nvec + kSwiThreads * kSwiKv - 1) / (kSwiThreads * kSwiKv);
+    const int64_t blocks = ts_plan::chunks_for(nvec, kSwiThreads, kSwiKv);
     if (blocks > 0x7fffffff) return ts_host::fail(TS_ERR_SHAPE, "swiglu: tensor too large");
     hipLaunchKernelGGL(swiglu_fwd_vec<T>, dim3((unsigned)blocks), dim3(kSwiThreads), 0, st, g, u,
                        o, nvec);
@@ -163,7 +170,7 @@ ts_status bwd_typed(const void* dout, const void* gate, const void* up, void* dg
   if (n % VE == 0 && ts_host::aligned16(dout) && ts_host::aligned16(gate) &&
       ts_host::aligned16(up) && ts_host::aligned16(dgate) && ts_host::aligned16(dup)) {
     const int64_t nvec = n / VE;
-    const int64_t blocks = (nvec + kSwiThreads * kSwiKv - 1) / (kSwiThreads * kSwiKv);
+    const int64_t blocks = ts_plan::chunks_for(nvec, kSwiThreads, kSwiKv);
     if (blocks > 0x7fffffff) return ts_host::fail(TS_ERR_SHAPE, "swiglu: tensor too large");
     hipLaunchKernelGGL(swiglu_bwd_vec<T>, dim3((unsigned)blocks), dim3(kSwiThreads), 0, st, d, g,
                        u, dg, du, nvec);

@@ -22,6 +22,7 @@
 #include <math.h>
 
 #include "common.hpp"
+#include "plan.hpp"
 
 namespace {
 
@@ -81,10 +82,9 @@ __global__ __launch_bounds__(kBlock) void shard_stats_vec(const T* __restrict__ 
   const Rsrc xi = buf_rsrc(xr, (uint32_t)nvec * 16u);
   u32x4 buf[kKv];
 #pragma unroll
-  for (int k = 0; k < kKv; ++k) {
-    const int v = threadIdx.x + k * kBlock;
-    buf[k] = buf_ld16_stream(xi, v < nvec ? v * 16 : kBufOob);
-  }
+  for (int k = 0; k < kKv; ++k)  // past the row: an offset the resource does not cover
+    buf[k] = buf_ld16_stream(
+        xi, ts_plan::vec_boffset(ts_plan::chunk_vec(0, k, threadIdx.x, kBlock, kKv), nvec, 16));
   const int64_t tl = targets[row] - vocab_start;
   float zt = 0.f;
   if (threadIdx.x == 0 && tl >= 0 && tl < Vp) zt = Elt<T>::load1(xr + tl);
@@ -256,16 +256,19 @@ __global__ __launch_bounds__(kBwdThreads) void shard_bwd_vec(
       shard_bwd_row(targets, lse, grad_output, dloss_scale, smoothing, Vp, vocab_start, row);
   const T* xr = logits + row * ld;
   G* gr = grad + row * ld_grad;
-  const int64_t base = (int64_t)blockIdx.x * kBwdThreads * kBwdKv + threadIdx.x;
+  int64_t vk[kBwdKv];  // this thread's vectors of the row (ts_plan::chunk_vec)
+#pragma unroll
+  for (int k = 0; k < kBwdKv; ++k)
+    vk[k] = ts_plan::chunk_vec(blockIdx.x, k, threadIdx.x, kBwdThreads, kBwdKv);
   u32x4 buf[kBwdKv];
 #pragma unroll
   for (int k = 0; k < kBwdKv; ++k) {
-    const int64_t v = base + (int64_t)k * kBwdThreads;
+    const int64_t v = vk[k];
     buf[k] = v < nvec ? ld16_stream(xr + v * VE) : u32x4{0, 0, 0, 0};
   }
 #pragma unroll
   for (int k = 0; k < kBwdKv; ++k) {
-    const int64_t v = base + (int64_t)k * kBwdThreads;
+    const int64_t v = vk[k];
     if (v < nvec) {
       float z[VE], g[VE];
       Elt<T>::unpack(buf[k], z);
@@ -336,8 +339,7 @@ ts_status bwd_typed(const void* logits, int64_t ld, const int64_t* targets, cons
                    ts_host::aligned16(logits) && ts_host::aligned16(grad) && grad_ok;
   if (vec) {
     const int64_t nvec = Vp / VE;
-    const unsigned gx =
-        (unsigned)((nvec + kBwdThreads * kBwdKv - 1) / (kBwdThreads * kBwdKv));
+    const unsigned gx = (unsigned)ts_plan::chunks_for(nvec, kBwdThreads, kBwdKv);
     for (int64_t r0 = 0; r0 < N; r0 += kMaxGridY) {
       const unsigned gy = (unsigned)(N - r0 < kMaxGridY ? N - r0 : kMaxGridY);
       hipLaunchKernelGGL((shard_bwd_vec<T, G>), dim3(gx, gy), dim3(kBwdThreads), 0, st, lp, ld,
