@@ -31,6 +31,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -60,12 +61,25 @@ def parse():
     return p.parse_args()
 
 
+def kernel_source_hash() -> str:
+    """sha256 (first 16 hex digits) over the library's kernel sources and headers, by
+    name: the key that ties a committed rocprofv3 traffic measurement to the kernels it
+    measured."""
+    h = hashlib.sha256()
+    for f in sorted((ROOT / "trainscale_amd" / "csrc").iterdir()):
+        if f.suffix in (".hip", ".hpp", ".h", ".cpp"):
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def load_traffic():
-    """{kernel: HBM bytes per launch} from the committed rocprofv3 --pmc summary."""
+    """({kernel: HBM bytes per launch}, source hash) from the committed rocprofv3 --pmc
+    summary; the hash is that of the kernel sources it was measured on (None if absent)."""
     f = ROOT / "profiles" / "pmc_traffic.txt"
-    out = {}
+    out, src = {}, None
     if not f.exists():
-        return out
+        return out, src
     for line in f.read_text().splitlines():
         parts = line.split()
         if len(parts) == 3 and parts[0] == "hbm_bytes_per_launch":
@@ -73,7 +87,20 @@ def load_traffic():
                 out[parts[1]] = int(parts[2])
             except ValueError:
                 pass
-    return out
+        elif len(parts) == 2 and parts[0] == "kernel_source_sha256":
+            src = parts[1]
+    return out, src
+
+
+def traffic_for(kernel: str):
+    """(HBM bytes per launch of `kernel`, where the figure comes from): the committed
+    measurement when it was taken on the kernel sources in this tree, else (None, why)."""
+    measured, measured_src = load_traffic()
+    now = kernel_source_hash()
+    if measured_src != now:
+        return None, (f"none: profiles/pmc_traffic.txt was measured on kernel sources "
+                      f"{measured_src}, these are {now}")
+    return measured.get(kernel), f"profiles/pmc_traffic.txt (kernel sources {now})"
 
 
 def cpu_threads() -> int:
@@ -729,7 +756,7 @@ def main():
                          "ms_after_512MB_flush": round(per_op_flushed[name], 4)}
     kernels["ce_fwd_bwd"]["bytes_touched"] = W.ce_bytes_fused(N, S0["n_valid"], V)
     dom = max(order, key=lambda n: kernels[n]["ms"])
-    traffic = load_traffic().get(kernel_names[dom])
+    traffic, traffic_source = traffic_for(kernel_names[dom])
     roofline = {
         "kernel": kernel_names[dom],
         "op": dom,
@@ -740,6 +767,7 @@ def main():
         "frac": kernels[dom]["frac"],
         "traffic": traffic,
         "algorithmic_bytes": op_bytes[dom],
+        "traffic_source": traffic_source,
     }
     op_sum = sum(per_op.values())
     op_sum_flushed = sum(per_op_flushed.values())

@@ -25,6 +25,9 @@ indices. A small C++ driver compiled with g++ sweeps many shapes and checks:
   maps to one (token slot, head, index) in range, each once, and its elements
   (rope_elems) lie inside the head, for the vector and generic paths and both
   layouts;
+* one-wave-per-row kernels (wave_row over wave_row_blocks) own every row once,
+  a label's logit is read only at a column inside its row (label_col), and a
+  vocabulary split into shards gives each label to exactly one shard (shard_col);
 * RoPE workgroups are whole waves within 256..1024 threads and their cos/sin
   staging fits the LDS bound;
 * umulhi(n, ceil(2^32/d)) == n / d wherever magic_exact(n_max, d) admits it,
@@ -50,6 +53,7 @@ DRIVER = r"""
 #include <cstdlib>
 #include <initializer_list>
 #include <vector>
+#include <algorithm>
 #include "plan.hpp"
 using namespace ts_plan;
 
@@ -238,9 +242,14 @@ int main() {
         const long long full = nvec / ((long long)threads * kv);
         for (long long c = 0; c < full; ++c)
           for (int k = 0; k < kv; ++k)
-            for (int t = 0; t < threads; ++t) seen2[chunk_vec(c, k, t, threads, kv)]++;
+            for (int t = 0; t < threads; ++t) {
+              const long long v = chunk_vec(c, k, t, threads, kv);
+              CHECK(v >= 0 && v < nvec, "whole chunk reaches vector %lld of %lld", v, nvec);
+              if (v >= 0 && v < nvec) seen2[v]++;
+            }
         for (int t = 0; t < threads; ++t)
-          for (long long v = chunk_vec(full, 0, t, threads, kv); v < nvec; v += threads) seen2[v]++;
+          for (long long v = chunk_vec(full, 0, t, threads, kv); v < nvec; v += threads)
+            if (v >= 0) seen2[v]++;
         for (long long v = 0; v < nvec; ++v) CHECK(seen2[v] == 1, "row loop visits %lld %d times", v, seen2[v]);
         // buffer offsets of register rows (ce_fused_vec, shard stats): inside a
         // resource of nvec vectors, or an offset no such resource covers
@@ -308,6 +317,53 @@ int main() {
               CHECK(u.hh == t.hh && u.j == t.j, "token-kernel task split");
             }
           }
+        }
+      }
+    }
+  }
+  // One-wave-per-row kernels (flce_rows, flce_rows_t, flce_shard_rows): the grid
+  // wave_row_blocks gives assigns each row to one wave, and the waves past the
+  // last row are exactly those the kernel's row check sends home
+  for (int waves : {1, 4, 16}) {
+    for (long long rows : {1ll, 3ll, 4ll, 5ll, 2047ll, 2048ll, 8193ll}) {
+      std::vector<int> seen(rows, 0);
+      const long long blocks = wave_row_blocks(rows, waves);
+      CHECK(blocks * waves >= rows && (blocks - 1) * waves < rows, "wave_row_blocks");
+      for (long long b = 0; b < blocks; ++b)
+        for (int w = 0; w < waves; ++w) {
+          const long long r = wave_row(b, w, waves);
+          if (r < rows) seen[r]++;
+        }
+      for (long long r = 0; r < rows; ++r) CHECK(seen[r] == 1, "row %lld owned %d times", r, seen[r]);
+    }
+  }
+  // Label columns: a logit is read only at a column inside the row, and a
+  // vocabulary split into shards gives every label in [0, V) to exactly one shard
+  {
+    const long long big = 0x7fffffffffffffffll;
+    for (long long V : {1ll, 7ll, 50257ll, 128256ll}) {
+      for (long long ign : {-100ll, 0ll, 5ll}) {
+        for (long long lab : {-big - 1, -101ll, -100ll, -1ll, 0ll, 1ll, 5ll, 6ll, V - 1, V, V + 1, big}) {
+          const long long c = label_col(lab, V, ign);
+          if (lab == ign) CHECK(c == kLabelIgnored, "ignored label");
+          else if (lab >= 0 && lab < V) CHECK(c == lab, "label column");
+          else CHECK(c == kLabelOutside, "label outside");
+        }
+      }
+      for (int P : {1, 2, 3, 8}) {
+        const long long Vp = (V + P - 1) / P;
+        for (long long lab : {-big - 1, -1ll, 0ll, 1ll, Vp - 1, Vp, V / 2, V - 1, V, big}) {
+          int owners = 0;
+          for (int p = 0; p < P; ++p) {
+            const long long start = p * Vp, width = std::min(Vp, V - start);
+            if (width <= 0) continue;
+            const long long c = shard_col(lab, start, width);
+            if (c != kLabelOutside) {
+              owners++;
+              CHECK(c >= 0 && c < width && start + c == lab, "shard column %lld of %lld", c, width);
+            }
+          }
+          CHECK(owners == (lab >= 0 && lab < V ? 1 : 0), "label %lld held by %d shards", lab, owners);
         }
       }
     }

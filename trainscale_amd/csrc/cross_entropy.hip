@@ -157,10 +157,11 @@ __global__ __launch_bounds__(kThreads) void ce_fwd_vec(const T* __restrict__ log
   if (threadIdx.x == 0) {
     const float l = m + logf(s);
     float out;
-    if (label < 0 || label >= V) {
+    const int64_t col = ts_plan::label_col(label, V, ignore_index);  // not ignored here
+    if (col < 0) {
       out = __builtin_nanf("");
     } else {
-      const float zt = xform<kXform>(Elt<T>::load1(xr + label), xf);
+      const float zt = xform<kXform>(Elt<T>::load1(xr + col), xf);
       out = l - zt;
       if constexpr (kSmooth) out = (1.f - smoothing) * out + smoothing * (l - sz / (float)V);
     }
@@ -200,10 +201,11 @@ __global__ __launch_bounds__(kThreads) void ce_fwd_generic(
   if (threadIdx.x == 0) {
     const float l = m + logf(s);
     float out;
-    if (label < 0 || label >= V) {
+    const int64_t col = ts_plan::label_col(label, V, ignore_index);  // not ignored here
+    if (col < 0) {
       out = __builtin_nanf("");
     } else {
-      const float zt = xform<kXform>(Elt<T>::load1(xr + label), xf);
+      const float zt = xform<kXform>(Elt<T>::load1(xr + col), xf);
       out = l - zt;
       if constexpr (kSmooth) out = (1.f - smoothing) * out + smoothing * (l - sz / (float)V);
     }
@@ -495,10 +497,11 @@ __global__ __launch_bounds__(kFusedThreads) void ce_fused_vec(
   for (int k = 0; k < kFusedKv; ++k) asm volatile("" : "+v"(buf[k]));
   if (threadIdx.x == 0) {
     float out;
-    if (label < 0 || label >= V) {
+    const int64_t col = ts_plan::label_col(label, V, ignore_index);  // not ignored here
+    if (col < 0) {
       out = __builtin_nanf("");
     } else {
-      const float zt = xform<kXform>(Elt<T>::load1(xr + label), xf);
+      const float zt = xform<kXform>(Elt<T>::load1(xr + col), xf);
       out = l - zt;
       if constexpr (kSmooth) out = (1.f - smoothing) * out + smoothing * (l - sz / (float)V);
     }

@@ -412,17 +412,20 @@ __global__ __launch_bounds__(256) void flce_count(const int64_t* __restrict__ la
   if (threadIdx.x == 0) *n_valid = (int)c;
 }
 
+// Row waves per workgroup of the one-wave-per-row kernels.
+constexpr int kRowWaves = 4;
+
 // Per row of a chunk (one wave per row): lse from the row's slice statistics
 // (contiguous [nparts] float2), loss = lse - z[label] with z[label] read from
 // the chunk's bf16 logits. Fixed combination order: lane-strided partial
 // (max, sum) pairs, then a DPP/lane-read fold.
-__global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stats, int64_t nparts,
+__global__ __launch_bounds__(64 * kRowWaves) void flce_rows(const float2* __restrict__ stats, int64_t nparts,
                                                  const __bf16* __restrict__ logits, int64_t ldl,
                                                  const int64_t* __restrict__ labels, int64_t M,
                                                  int64_t V, int64_t ignore_index,
                                                  float* __restrict__ lse_out,
                                                  float* __restrict__ loss_rows) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = ts_plan::wave_row(blockIdx.x, threadIdx.x >> 6, kRowWaves);
   const int lane = threadIdx.x & 63;
   if (r >= M) return;  // wave-uniform
   const float2* sr = stats + r * nparts;
@@ -437,11 +440,11 @@ __global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stat
   s = wave_sum(s);
   if (lane != 0) return;
   const float l = m + logf(s);
-  const int64_t lab = labels[r];
+  const int64_t col = ts_plan::label_col(labels[r], V, ignore_index);
   float out;
-  if (lab == ignore_index) out = 0.f;
-  else if (lab < 0 || lab >= V) out = __builtin_nanf("");
-  else out = l - Elt<__bf16>::load1(logits + r * ldl + lab);
+  if (col == ts_plan::kLabelIgnored) out = 0.f;
+  else if (col == ts_plan::kLabelOutside) out = __builtin_nanf("");
+  else out = l - Elt<__bf16>::load1(logits + r * ldl + col);
   lse_out[r] = l;
   loss_rows[r] = out;
 }
@@ -450,13 +453,13 @@ __global__ __launch_bounds__(256) void flce_rows(const float2* __restrict__ stat
 // statistics of the transformed logits t, and loss = lse - t[label] with
 // t[label] from zlab, written by the statistics epilogue (0 on ignore_index
 // rows, NaN for other labels outside [0, V)).
-__global__ __launch_bounds__(256) void flce_rows_t(const float2* __restrict__ stats,
+__global__ __launch_bounds__(64 * kRowWaves) void flce_rows_t(const float2* __restrict__ stats,
                                                    int64_t nparts, const float* __restrict__ zlab,
                                                    const int64_t* __restrict__ labels, int64_t M,
                                                    int64_t V, int64_t ignore_index,
                                                    float* __restrict__ lse_out,
                                                    float* __restrict__ loss_rows) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = ts_plan::wave_row(blockIdx.x, threadIdx.x >> 6, kRowWaves);
   const int lane = threadIdx.x & 63;
   if (r >= M) return;  // wave-uniform
   const float2* sr = stats + r * nparts;
@@ -471,10 +474,10 @@ __global__ __launch_bounds__(256) void flce_rows_t(const float2* __restrict__ st
   s = wave_sum(s);
   if (lane != 0) return;
   const float l = m + logf(s);
-  const int64_t lab = labels[r];
+  const int64_t col = ts_plan::label_col(labels[r], V, ignore_index);
   float out;
-  if (lab == ignore_index) out = 0.f;
-  else if (lab < 0 || lab >= V) out = __builtin_nanf("");
+  if (col == ts_plan::kLabelIgnored) out = 0.f;
+  else if (col == ts_plan::kLabelOutside) out = __builtin_nanf("");
   else out = l - zlab[r];
   lse_out[r] = l;
   loss_rows[r] = out;
@@ -504,7 +507,7 @@ struct ShardStats {
 // Per row of the shard's logits (one wave per row): the shard lse from the
 // GEMM's slice statistics and the label's logit when vocab_start <= label <
 // vocab_start + Vp, read from the bf16 logits.
-__global__ __launch_bounds__(256) void flce_shard_rows(const float2* __restrict__ stats,
+__global__ __launch_bounds__(64 * kRowWaves) void flce_shard_rows(const float2* __restrict__ stats,
                                                        int64_t nparts,
                                                        const __bf16* __restrict__ logits,
                                                        int64_t ldl,
@@ -512,7 +515,7 @@ __global__ __launch_bounds__(256) void flce_shard_rows(const float2* __restrict_
                                                        int64_t M, int64_t Vp,
                                                        int64_t vocab_start,
                                                        ShardStats* __restrict__ out) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = ts_plan::wave_row(blockIdx.x, threadIdx.x >> 6, kRowWaves);
   const int lane = threadIdx.x & 63;
   if (r >= M) return;  // wave-uniform
   const float2* sr = stats + r * nparts;
@@ -526,8 +529,8 @@ __global__ __launch_bounds__(256) void flce_shard_rows(const float2* __restrict_
   }
   s = wave_sum(s);
   if (lane != 0) return;
-  const int64_t tl = labels[r] - vocab_start;
-  const float zt = tl >= 0 && tl < Vp ? Elt<__bf16>::load1(logits + r * ldl + tl) : 0.f;
+  const int64_t tl = ts_plan::shard_col(labels[r], vocab_start, Vp);
+  const float zt = tl >= 0 ? Elt<__bf16>::load1(logits + r * ldl + tl) : 0.f;
   out[r] = ShardStats{m + logf(s), zt, 0.f, 0.f};
 }
 
@@ -693,10 +696,13 @@ __global__ __launch_bounds__(256) void fill_zero_u32(uint32_t* __restrict__ p, i
 
 // x[i] *= *scale unless *scale == 1, over n elements of type T: nvec 16-byte
 // vectors from x (x 16-byte aligned when nvec > 0), then the n - nvec * VE
-// elements after them one at a time. The grid is capped (kScaleGrid
-// workgroups, each thread four vectors per sweep) so that the common no-op
-// case, an upstream gradient of exactly 1, costs little more than a launch.
-constexpr int kScaleGrid = 2048;
+// elements after them one at a time. The grid is capped at kScaleGrid
+// workgroups (one per CU), each thread four vectors per sweep. Measured on
+// MI355X over a [16384, 128256] bf16 gradient: factor 2 at 5.6 TB/s with 256 or
+// 512 workgroups against 5.0 TB/s with 2048; the no-op (factor exactly 1) costs
+// the same 5.9-6.0 us between HIP events for any grid from 64 to 2048
+// workgroups, what an empty kernel costs there.
+constexpr int kScaleGrid = 256;
 constexpr int kScaleUnroll = 4;
 // The factor is *num, or *num / *den when den is given. With hint_out, the
 // first thread also stores *num there when it is finite and non-zero (else
@@ -910,7 +916,7 @@ extern "C" ts_status ts_flce_fwd_bwd(const void* hidden, int64_t ldh, const void
     g.ldc = ldl;
     g.stats = stats;
     TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_gemm_logits"));
-    hipLaunchKernelGGL(flce_rows, dim3((unsigned)((Mc + 3) / 4)), dim3(256), 0, st, stats,
+    hipLaunchKernelGGL(flce_rows, dim3((unsigned)ts_plan::wave_row_blocks(Mc, kRowWaves)), dim3(64 * kRowWaves), 0, st, stats,
                        lay.nparts, Lc, ldl, labels + r0, Mc, V, ignore_index, lse_ws + r0,
                        rows_ws + r0);
     TS_TRY(ts_host::check_launch("flce_rows"));
@@ -1133,7 +1139,7 @@ ts_status flce_forward_impl(const char* who, const void* hidden, int64_t ldh, co
   g.C = static_cast<__bf16*>(logits);  // NULL: the statistics only
   g.ldc = logits_ld(V);
   TS_TRY(launch_gemm<kEpiStats>(g, st, "flce_gemm_stats"));
-  hipLaunchKernelGGL(flce_rows_t, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, stats,
+  hipLaunchKernelGGL(flce_rows_t, dim3((unsigned)ts_plan::wave_row_blocks(N, kRowWaves)), dim3(64 * kRowWaves), 0, st, stats,
                      lay.nparts, zlab, labels, N, V, ignore_index, lse_ws, rows_ws);
   TS_TRY(ts_host::check_launch("flce_rows_t"));
   if (loss == nullptr) return TS_OK;
@@ -1496,7 +1502,7 @@ extern "C" ts_status ts_flce_vocab_fwd(const void* hidden, int64_t ldh, const vo
   g.ldc = Vp;
   g.stats = part;
   TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_vocab_gemm_logits"));
-  hipLaunchKernelGGL(flce_shard_rows, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, part,
+  hipLaunchKernelGGL(flce_shard_rows, dim3((unsigned)ts_plan::wave_row_blocks(N, kRowWaves)), dim3(64 * kRowWaves), 0, st, part,
                      lay.nparts, L, Vp, labels, N, Vp, vocab_start,
                      reinterpret_cast<ShardStats*>(stats));
   return ts_host::check_launch("flce_shard_rows");

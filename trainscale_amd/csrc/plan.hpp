@@ -311,6 +311,32 @@ TS_HOST_DEVICE inline int32_t vec_boffset(int64_t v, int64_t nvec, int vec_bytes
   return v >= 0 && v < nvec ? (int32_t)(v * vec_bytes) : kNoAccess;
 }
 
+// Row owned by wave `wave` of workgroup `block` in a one-wave-per-row kernel
+// with `waves` row waves per workgroup (flce_rows); such a kernel returns,
+// wave-uniformly, for rows at or past its row count.
+TS_HOST_DEVICE inline int64_t wave_row(int64_t block, int wave, int waves) {
+  return block * waves + wave;
+}
+// Workgroups of `waves` row waves that cover `rows` rows.
+TS_HOST_DEVICE inline int64_t wave_row_blocks(int64_t rows, int waves) {
+  return (rows + waves - 1) / waves;
+}
+
+// A row's label as a column of its logits: the label itself when 0 <= label < V;
+// kLabelIgnored for ignore_index (the row reads nothing and its loss is 0);
+// kLabelOutside for any other label (nothing is read; the row's loss is NaN).
+constexpr int64_t kLabelIgnored = -1;
+constexpr int64_t kLabelOutside = -2;
+TS_HOST_DEVICE inline int64_t label_col(int64_t label, int64_t V, int64_t ignore_index) {
+  if (label == ignore_index) return kLabelIgnored;
+  return label >= 0 && label < V ? label : kLabelOutside;
+}
+// The label's column in the vocabulary shard [vocab_start, vocab_start + Vp)
+// (vocab_start >= 0), or kLabelOutside when the shard does not hold it.
+TS_HOST_DEVICE inline int64_t shard_col(int64_t label, int64_t vocab_start, int64_t Vp) {
+  return label >= vocab_start && label - vocab_start < Vp ? label - vocab_start : kLabelOutside;
+}
+
 // A RoPE task f of a workgroup: token slot i (0 .. tpb - 1), head hh (Q heads,
 // then K heads) and j, its index within the head (a 16-byte vector pair on the
 // vector path, a rotation pair on the generic path). The divisions are

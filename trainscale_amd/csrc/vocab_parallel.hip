@@ -85,9 +85,9 @@ __global__ __launch_bounds__(kBlock) void shard_stats_vec(const T* __restrict__ 
   for (int k = 0; k < kKv; ++k)  // past the row: an offset the resource does not cover
     buf[k] = buf_ld16_stream(
         xi, ts_plan::vec_boffset(ts_plan::chunk_vec(0, k, threadIdx.x, kBlock, kKv), nvec, 16));
-  const int64_t tl = targets[row] - vocab_start;
+  const int64_t tl = ts_plan::shard_col(targets[row], vocab_start, Vp);
   float zt = 0.f;
-  if (threadIdx.x == 0 && tl >= 0 && tl < Vp) zt = Elt<T>::load1(xr + tl);
+  if (threadIdx.x == 0 && tl >= 0) zt = Elt<T>::load1(xr + tl);
 
   float m = -INFINITY, mb = 0.f, s = 0.f, sz = 0.f;
   auto sum_exp = [&](const float (&z)[VE], float bias) {
@@ -163,8 +163,8 @@ __global__ __launch_bounds__(kGenThreads) void shard_stats_generic(
   float lse, gz;
   block_lse<kGenThreads / kWave>(m, s, sz, lds, lse, gz);
   if (threadIdx.x == 0) {
-    const int64_t tl = targets[row] - vocab_start;
-    const float zt = tl >= 0 && tl < Vp ? Elt<T>::load1(xr + tl) : 0.f;
+    const int64_t tl = ts_plan::shard_col(targets[row], vocab_start, Vp);
+    const float zt = tl >= 0 ? Elt<T>::load1(xr + tl) : 0.f;
     stats[row] = Stats{lse, zt, gz, 0.f};
   }
 }
@@ -229,7 +229,7 @@ __device__ inline ShardBwd shard_bwd_row(const int64_t* targets, const float* ls
   r.a1 = dl * (1.f - smoothing);
   r.c = smoothing == 0.f ? 0.f : dl * smoothing / (float)Vp;
   r.lse2 = lse[row] * kLog2e;
-  r.tl = targets[row] - vocab_start;
+  r.tl = ts_plan::shard_col(targets[row], vocab_start, Vp);  // no column matches kLabelOutside
   return r;
 }
 
