@@ -165,6 +165,38 @@ def test_strided_input(gpu):
     check_against_oracle(x, w, dy, 1e-6)
 
 
+def test_gemma_norm_routing_as_the_reference(gpu):
+    """registry/__init__.py:1058-1077 patches GemmaRMSNorm with the plain RMSNorm kernel:
+    the patched module computes x * rstd * w (w = 0 at initialisation gives zeros) where
+    its own forward computes x * rstd * (1 + w). KernelPatcher does the same by default;
+    skip_inexact_norms keeps the module's own forward."""
+    import torch.nn as nn
+    from trainscale_amd import registry
+
+    class GemmaRMSNorm(nn.Module):
+        def __init__(self, n):
+            super().__init__()
+            self.weight = nn.Parameter(torch.zeros(n))
+            self.eps = 1e-6
+
+        def forward(self, h):
+            var = h.float().pow(2).mean(-1, keepdim=True)
+            return (h.float() * torch.rsqrt(var + self.eps) * (1.0 + self.weight.float())).to(h.dtype)
+
+    torch.manual_seed(15)
+    x = torch.randn(16, 512, device=gpu).to(BF)
+    own = GemmaRMSNorm(512).to(gpu)
+    y_own = own(x)
+    patched = GemmaRMSNorm(512).to(gpu)
+    registry.KernelPatcher().patch(patched)
+    y_ref, _ = oracle.rms_norm_fwd(x, patched.weight.detach(), 1e-6)
+    assert_ulp(patched(x), y_ref, 1)
+    assert torch.count_nonzero(patched(x)) == 0 and torch.count_nonzero(y_own) > 0
+    kept = GemmaRMSNorm(512).to(gpu)
+    registry.KernelPatcher(skip_inexact_norms=True).patch(kept)
+    assert torch.equal(kept(x), y_own)
+
+
 def test_dw_deterministic(gpu):
     wl = workloads.rmsnorm_workload(gpu, scale=0.25)
     x, w, dy = wl.tensors["x"], wl.tensors["w"], wl.tensors["dy"]

@@ -97,6 +97,35 @@ def test_patch_boundary_keeps_cpu_modules_on_their_own_forward():
     assert "LlamaRMSNorm" in registry.LAYER_PATCHES
 
 
+class GemmaRMSNorm(nn.Module):
+    """HF Gemma's norm: x * rstd * (1 + w), w initialised to zeros."""
+
+    def __init__(self, n, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.zeros(n))
+        self.eps = eps
+
+    def forward(self, h):
+        var = h.float().pow(2).mean(-1, keepdim=True)
+        return (h.float() * torch.rsqrt(var + self.eps) * (1.0 + self.weight.float())).to(h.dtype)
+
+
+def test_norms_with_other_math_are_patched_as_the_reference_does_unless_skipped():
+    # registry/__init__.py:1058-1077 routes GemmaRMSNorm to the plain RMSNorm kernel;
+    # KernelPatcher does too by default, and leaves it alone with skip_inexact_norms
+    assert registry.LAYER_PATCHES["GemmaRMSNorm"] is registry.auto_patch_layernorm
+    assert set(registry.NORMS_WITH_OTHER_MATH) <= set(registry.LAYER_PATCHES)
+    m1 = nn.Sequential(GemmaRMSNorm(8), LlamaRMSNorm(8))
+    p1 = registry.KernelPatcher()
+    p1.patch(m1)
+    assert p1.patched_layers == [("0", "GemmaRMSNorm"), ("1", "LlamaRMSNorm")]
+    m2 = nn.Sequential(GemmaRMSNorm(8), LlamaRMSNorm(8))
+    p2 = registry.KernelPatcher(skip_inexact_norms=True)
+    p2.patch(m2)
+    assert p2.patched_layers == [("1", "LlamaRMSNorm")]
+    assert not getattr(m2[0], "_trainscale_amd_patched", False)
+
+
 class LlamaMLP(nn.Module):
     def __init__(self, h, i):
         super().__init__()

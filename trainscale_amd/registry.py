@@ -29,7 +29,7 @@ import sys
 from .kernels.fused_kernels import fast_rms_layernorm, swiglu_forward
 from .kernels.rope_kernels import RoPEConfig, RoPEScalingType, hf_apply_rotary_pos_emb
 
-__all__ = ["LAYER_PATCHES", "register_layer_patch", "auto_patch_layernorm", "auto_patch_mlp",
+__all__ = ["LAYER_PATCHES", "NORMS_WITH_OTHER_MATH", "register_layer_patch", "auto_patch_layernorm", "auto_patch_mlp",
            "auto_patch_rope", "KernelPatcher", "patch_model"]
 
 LAYER_PATCHES: Dict[str, Callable[[nn.Module], None]] = {}
@@ -63,6 +63,21 @@ for _name in ("LlamaRMSNorm", "Qwen2RMSNorm", "Qwen3RMSNorm", "GemmaRMSNorm", "G
               "DeepseekRMSNorm", "DeepseekV2RMSNorm", "MixtralRMSNorm", "DbrxLayerNorm",
               "GrokRMSNorm", "InternVLRMSNorm"):
     register_layer_patch(_name, auto_patch_layernorm)
+
+# Registered norm classes whose own forward is not x * rstd * w. The reference's
+# table (registry/__init__.py:1058-1077) routes them to the plain RMSNorm kernel all
+# the same, and so does KernelPatcher by default, to stay a drop-in: Gemma's norms
+# compute x * rstd * (1 + w) with w initialised to zeros (a patched Gemma model
+# normalises with weight 0 where its own forward uses 1); Cohere's, StarCoder's and
+# DBRX's LayerNorms subtract the row mean (and may add a bias).
+# KernelPatcher(skip_inexact_norms=True) leaves these modules on their own forward.
+NORMS_WITH_OTHER_MATH: Dict[str, str] = {
+    "GemmaRMSNorm": "x * rstd * (1 + w)",
+    "Gemma2RMSNorm": "x * rstd * (1 + w)",
+    "CohereLayerNorm": "LayerNorm: subtracts the mean",
+    "StarcoderLayerNorm": "LayerNorm: subtracts the mean, adds a bias",
+    "DbrxLayerNorm": "LayerNorm: subtracts the mean",
+}
 
 
 def auto_patch_mlp(module: nn.Module) -> None:
@@ -153,12 +168,15 @@ class KernelPatcher:
 
     ``patch_attention`` and ``patch_fp8`` are accepted for signature
     compatibility; this layer registers no attention or FP8 patches, so they
-    select nothing.
+    select nothing. ``skip_inexact_norms`` (not in the reference) leaves the
+    classes of NORMS_WITH_OTHER_MATH unpatched; by default they are patched, as
+    the reference patches them.
     """
 
     def __init__(self, patch_layernorm: bool = True, patch_mlp: bool = True,
                  patch_attention: bool = True, patch_rope: bool = True, patch_fp8: bool = False,
-                 verbose: bool = False):
+                 verbose: bool = False, skip_inexact_norms: bool = False):
+        self.skip_inexact_norms = skip_inexact_norms
         self.patch_layernorm = patch_layernorm
         self.patch_mlp = patch_mlp
         self.patch_attention = patch_attention
@@ -175,6 +193,8 @@ class KernelPatcher:
                 continue
             if cls.endswith(("RMSNorm", "LayerNorm")):
                 if not self.patch_layernorm:
+                    continue
+                if self.skip_inexact_norms and cls in NORMS_WITH_OTHER_MATH:
                     continue
             elif cls.endswith("MLP"):
                 if not self.patch_mlp:
