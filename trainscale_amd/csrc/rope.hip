@@ -152,6 +152,20 @@ __device__ inline void task_load(const RopeArgs& a, const Task<T>& k, u32x4& v1,
   v2 = kInterleaved ? u32x4{0, 0, 0, 0} : ld16_stream(k.src + e.e2);
 }
 
+// The rotation's two outputs, x1 c - x2 s and x2 c + x1 s, with each product
+// rounded to fp32 before the sum (no fused multiply-add): the roundings of the
+// reference's eager rotation (triton_kernels.py:908-925) and of the CPU
+// restatement, so that from the same cos/sin values the outputs are bit-identical
+// to theirs. The backward passes -s.
+__device__ inline float rot_lo(float x1, float x2, float c, float s) {
+#pragma clang fp contract(off)
+  return x1 * c - x2 * s;
+}
+__device__ inline float rot_hi(float x1, float x2, float c, float s) {
+#pragma clang fp contract(off)
+  return x2 * c + x1 * s;
+}
+
 template <typename T, bool kInterleaved>
 __device__ inline void task_rotate_store(const RopeArgs& a, const Task<T>& k, const u32x4& v1,
                                          const u32x4& v2, const float* cs, const float* sn) {
@@ -168,8 +182,8 @@ __device__ inline void task_rotate_store(const RopeArgs& a, const Task<T>& k, co
     for (int p = 0; p < V; ++p) {
       const float c = crow[e1 + p];
       const float s = srow[e1 + p];
-      o1[p] = x1[p] * c - x2[p] * s;
-      o2[p] = x2[p] * c + x1[p] * s;
+      o1[p] = rot_lo(x1[p], x2[p], c, s);
+      o2[p] = rot_hi(x1[p], x2[p], c, s);
     }
     st16_stream(k.dst + e1, Elt<T>::pack(o1));
     st16_stream(k.dst + el.e2, Elt<T>::pack(o2));
@@ -181,8 +195,8 @@ __device__ inline void task_rotate_store(const RopeArgs& a, const Task<T>& k, co
     for (int p = 0; p < V / 2; ++p) {
       const float c = crow[e / 2 + p];
       const float s = srow[e / 2 + p];
-      o[2 * p] = x[2 * p] * c - x[2 * p + 1] * s;
-      o[2 * p + 1] = x[2 * p + 1] * c + x[2 * p] * s;
+      o[2 * p] = rot_lo(x[2 * p], x[2 * p + 1], c, s);
+      o[2 * p + 1] = rot_hi(x[2 * p], x[2 * p + 1], c, s);
     }
     st16_stream(k.dst + e, Elt<T>::pack(o));
   }
@@ -297,8 +311,8 @@ __global__ __launch_bounds__(kMaxThreads) void rope_generic_kernel(const RopeArg
     const float x2 = Elt<T>::load1(k.src + e2);
     const float c = cs[k.i * a.half + p];
     const float s = sn[k.i * a.half + p];
-    Elt<T>::store1(k.dst + e1, x1 * c - x2 * s);
-    Elt<T>::store1(k.dst + e2, x2 * c + x1 * s);
+    Elt<T>::store1(k.dst + e1, rot_lo(x1, x2, c, s));
+    Elt<T>::store1(k.dst + e2, rot_hi(x1, x2, c, s));
   }
 }
 
