@@ -337,9 +337,11 @@ ts_status ts_ce_vocab_shard_bwd(const void* logits, int64_t ld, ts_dtype dtype,
  * an LM head split by rows over the tensor-parallel ranks, the layout of
  * VocabParallelEmbedding / ColumnParallelLinear, distributed/tensor_parallel.py).
  * weight: this rank's [Vp, H] rows, vocabulary columns vocab_start ..
- * vocab_start + Vp - 1. N, H and Vp are multiples of 8. Both phases take the
+ * vocab_start + Vp - 1, any Vp. N and H are multiples of 8 (the Python
+ * wrapper pads other shapes: ignored rows, zero columns). Both phases take the
  * same workspace of ts_flce_vocab_workspace_size(N, Vp) bytes, which carries
- * the shard's logits from phase 1 to phase 2 and must not change in between.
+ * the shard's logits (rows of round_up(Vp, 8) columns) from phase 1 to phase 2
+ * and must not change in between.
  *
  * Phase 1: logits = hidden @ weight^T (bf16, into the workspace) and the
  * per-row partials stats[4r .. 4r + 3] = {lse over the shard, the logit of

@@ -165,7 +165,11 @@ def test_flce_vocab_validation(lib):
         k.get("N", 64), k.get("H", 128), k.get("Vp", 256), k.get("v0", 0), k.get("stats", FAKE),
         k.get("ws", FAKE), k.get("wsb", ws_need), st)
     assert fwd(N=60) == SHAPE       # not a multiple of 8
+    assert fwd(H=100) == SHAPE
     assert fwd(Vp=0) == SHAPE
+    # any shard width: the shard's logits rows are padded to whole 16-byte vectors
+    assert lib.ts_flce_vocab_workspace_size(64, 1001) >= 64 * 1008 * 2
+    assert fwd(Vp=1001, wsb=0) == WORKSPACE  # past the shape checks, stopped before a launch
     assert fwd(ldh=64) == SHAPE
     assert fwd(Vp=1 << 23) == SHAPE
     assert fwd(v0=-8) == INVALID

@@ -1432,7 +1432,7 @@ VocabLayout vocab_layout(int64_t N, int64_t Vp) {
     off += (bytes + 255) / 256 * 256;
     return o;
   };
-  l.off_logits = take((size_t)N * Vp * 2);
+  l.off_logits = take((size_t)N * logits_ld(Vp) * 2);  // rows of whole 16-byte vectors
   l.off_stats = take((size_t)l.nparts * N * sizeof(float2));
   l.off_lse = take((size_t)N * 4);
   l.off_rows = take((size_t)N * 4);
@@ -1449,11 +1449,12 @@ ts_status check_vocab(const void* hidden, int64_t ldh, const void* weight, int64
   if (N <= 0 || H <= 0 || Vp <= 0)
     return fail(TS_ERR_SHAPE, "%s: bad shape N=%lld H=%lld Vp=%lld", who, (long long)N,
                 (long long)H, (long long)Vp);
-  if (N % 8 != 0 || H % 8 != 0 || Vp % 8 != 0)
-    return fail(TS_ERR_SHAPE, "%s: N, H and Vp must be multiples of 8", who);
+  if (N % 8 != 0 || H % 8 != 0)
+    return fail(TS_ERR_SHAPE, "%s: N and H must be multiples of 8", who);
   if (ldh < H || ldw < H || ldh % 8 != 0 || ldw % 8 != 0)
     return fail(TS_ERR_SHAPE, "%s: row strides must be >= H and multiples of 8", who);
-  // 32-bit buffer offsets, as for ts_flce_fwd_bwd (here the logits' row stride is Vp)
+  // 32-bit buffer offsets, as for ts_flce_fwd_bwd (the logits' row stride is
+  // round_up(Vp, 8))
   if (Vp > ((int64_t)1 << 22) || H > ((int64_t)1 << 20) || N > ((int64_t)1 << 22) ||
       ldh > ((int64_t)1 << 22) || ldw > ((int64_t)1 << 22))
     return fail(TS_ERR_SHAPE, "%s: shape beyond the kernel's index range", who);
@@ -1499,11 +1500,12 @@ extern "C" ts_status ts_flce_vocab_fwd(const void* hidden, int64_t ldh, const vo
   g.N = Vp;
   g.K = H;
   g.C = L;
-  g.ldc = Vp;
+  g.ldc = logits_ld(Vp);
   g.stats = part;
   TS_TRY(launch_gemm<kEpiLogits>(g, st, "flce_vocab_gemm_logits"));
-  hipLaunchKernelGGL(flce_shard_rows, dim3((unsigned)ts_plan::wave_row_blocks(N, kRowWaves)), dim3(64 * kRowWaves), 0, st, part,
-                     lay.nparts, L, Vp, labels, N, Vp, vocab_start,
+  hipLaunchKernelGGL(flce_shard_rows, dim3((unsigned)ts_plan::wave_row_blocks(N, kRowWaves)),
+                     dim3(64 * kRowWaves), 0, st, part, lay.nparts, L, logits_ld(Vp), labels, N,
+                     Vp, vocab_start,
                      reinterpret_cast<ShardStats*>(stats));
   return ts_host::check_launch("flce_shard_rows");
 }
@@ -1548,8 +1550,9 @@ extern "C" ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const vo
                      reduction == 0 ? 1 : 0, loss, scale);
   TS_TRY(ts_host::check_launch("flce_loss"));
   if (grad_hidden_partial == nullptr && grad_weight_shard == nullptr) return TS_OK;
-  const int64_t dchunks = ts_plan::chunks_for(Vp / 8, 256, kDlKv);
-  hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(N * dchunks)), dim3(256), 0, st, L, Vp,
+  const int64_t ldl = logits_ld(Vp);
+  const int64_t dchunks = ts_plan::chunks_for((Vp + 7) / 8, 256, kDlKv);
+  hipLaunchKernelGGL(flce_dlogits, dim3((unsigned)(N * dchunks)), dim3(256), 0, st, L, ldl,
                      lse_ws, labels, Vp, dchunks, ignore_index, scale, vocab_start);
   TS_TRY(ts_host::check_launch("flce_dlogits"));
   const __bf16* Hd = static_cast<const __bf16*>(hidden);
@@ -1557,8 +1560,8 @@ extern "C" ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const vo
   using ts_gemm::kKMajor;
   using ts_gemm::kMNMajor;
   GemmArgs dh{};
-  dh.A = L;  // dlogits [N, Vp], K-major
-  dh.lda = Vp;
+  dh.A = L;  // dlogits [N, Vp], K-major (zero from Vp to the end of the row's last vector)
+  dh.lda = ldl;
   dh.B = Wd;  // weight shard [Vp, H] as the [H, Vp] operand: MN-major
   dh.ldb = ldw;
   dh.M = N;
@@ -1568,7 +1571,7 @@ extern "C" ts_status ts_flce_vocab_bwd(const void* hidden, int64_t ldh, const vo
   dh.ldc = H;
   GemmArgs dw{};
   dw.A = L;  // dlogits [N, Vp] as the [Vp, N] operand: MN-major
-  dw.lda = Vp;
+  dw.lda = ldl;
   dw.B = Hd;  // hidden [N, H] as the [H, N] operand: MN-major
   dw.ldb = ldh;
   dw.M = Vp;

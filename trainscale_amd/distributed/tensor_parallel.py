@@ -141,7 +141,7 @@ class VocabParallelLinearCrossEntropyFunction(torch.autograd.Function):
         shape = hidden.shape
         ex = _exchange
         stats, state = linear_ce_vocab_phase1(hidden.reshape(-1, shape[-1]), weight_shard,
-                                              labels, vocab_start)
+                                              labels, vocab_start, ignore_index)
         stats_all = ex.gather(stats) if ex.world_size > 1 else stats.unsqueeze(0)
         loss, _, _, gh, gw = linear_ce_vocab_phase2(
             state, stats_all, ignore_index, reduction,

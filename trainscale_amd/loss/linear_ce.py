@@ -285,12 +285,14 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
 
 class VocabShardState:
     """What phase 2 of the vocabulary-parallel linear CE needs from phase 1: the
-    rank's operands and the workspace that holds its shard's logits."""
+    rank's operands (padded to whole groups of 8 rows and 8 columns: the kernels'
+    shape), the caller's N and H, and the workspace that holds its shard's logits."""
 
-    def __init__(self, hidden, weight, labels, vocab_start, ws, ws_bytes, dev):
+    def __init__(self, hidden, weight, labels, vocab_start, ws, ws_bytes, dev, n0, h0):
         self.hidden, self.weight, self.labels = hidden, weight, labels
         self.vocab_start, self.ws, self.ws_bytes, self.dev = vocab_start, ws, ws_bytes, dev
         self.N, self.H = hidden.shape
+        self.N0, self.H0 = n0, h0
         self.Vp = weight.shape[0]
         self.ldh = hidden.stride(0) if self.N > 1 else self.H
         self.ldw = weight.stride(0) if self.Vp > 1 else self.H
@@ -303,34 +305,43 @@ def _rows_operand(t: Tensor) -> Tensor:
 
 
 def linear_ce_vocab_phase1(hidden: Tensor, weight_shard: Tensor, labels: Tensor,
-                           vocab_start: int):
+                           vocab_start: int, ignore_index: int = -100):
     """ts_flce_vocab_fwd: this rank's logits over its shard of the LM head (kept in the
     workspace) and its per-row partials [N, 4] fp32, the tensor the ranks exchange.
-    Returns (partials, state)."""
+    Returns (partials, state). Any N, H and shard width Vp: the kernels take N and H in
+    groups of 8, so other shapes run on copies padded with rows labelled ignore_index
+    (which phase 2 must then be given) and zero columns."""
     dev = _lib.require_gpu("vocab_parallel_linear_cross_entropy", hidden, weight_shard, labels)
     if hidden.dtype != torch.bfloat16 or weight_shard.dtype != torch.bfloat16:
         raise TypeError("vocab_parallel_linear_cross_entropy: hidden and weight must be bfloat16")
     if hidden.dim() != 2 or weight_shard.dim() != 2 or hidden.shape[1] != weight_shard.shape[1]:
         raise ValueError(f"vocab_parallel_linear_cross_entropy: hidden {tuple(hidden.shape)} and "
                          f"weight {tuple(weight_shard.shape)} must be [N, H] and [Vp, H]")
+    n0, h0 = hidden.shape
+    labels = labels.reshape(-1)
+    if labels.shape[0] != n0:
+        raise ValueError(f"vocab_parallel_linear_cross_entropy: {labels.shape[0]} labels for "
+                         f"{n0} rows")
+    labels = labels.to(torch.int64).contiguous()
+    hidden, weight_shard, _ = _pad_h(hidden, weight_shard)
+    if n0 % 8 != 0:
+        pad = 8 - n0 % 8
+        hidden = torch.cat([hidden, hidden.new_zeros((pad, hidden.shape[1]))])
+        labels = torch.cat([labels, labels.new_full((pad,), int(ignore_index))])
     hidden, weight_shard = _rows_operand(hidden), _rows_operand(weight_shard)
     N = hidden.shape[0]
-    labels = labels.reshape(-1)
-    if labels.shape[0] != N:
-        raise ValueError(f"vocab_parallel_linear_cross_entropy: {labels.shape[0]} labels for "
-                         f"{N} rows")
-    labels = labels.to(torch.int64).contiguous()
     lib = _lib.load()
     ws_bytes = int(lib.ts_flce_vocab_workspace_size(N, weight_shard.shape[0]))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    state = VocabShardState(hidden, weight_shard, labels, int(vocab_start), ws, ws_bytes, dev)
+    state = VocabShardState(hidden, weight_shard, labels, int(vocab_start), ws, ws_bytes, dev,
+                            n0, h0)
     stats = torch.empty((N, 4), dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
         check(lib.ts_flce_vocab_fwd(ptr(hidden), state.ldh, ptr(weight_shard), state.ldw,
                                     ptr(labels), N, state.H, state.Vp, state.vocab_start,
                                     ptr(stats), ptr(ws), ws_bytes, _lib.stream_handle(dev)),
               "ts_flce_vocab_fwd")
-    return stats, state
+    return stats[:n0], state
 
 
 def linear_ce_vocab_phase2(state: VocabShardState, stats_all: Tensor, ignore_index: int = -100,
@@ -338,14 +349,18 @@ def linear_ce_vocab_phase2(state: VocabShardState, stats_all: Tensor, ignore_ind
                            need_grad_weight: bool = True):
     """ts_flce_vocab_bwd from every rank's partials [P, N, 4]: returns (loss, loss_rows,
     lse, grad_hidden_partial [N, H] or None, grad_weight_shard [Vp, H] or None) for an
-    upstream gradient of 1; grad_hidden_partial is this rank's term of the sum over ranks."""
+    upstream gradient of 1; grad_hidden_partial is this rank's term of the sum over ranks.
+    ignore_index must be the one phase 1 was given."""
     if reduction not in _REDUCTIONS:
         raise ValueError(f"vocab_parallel_linear_cross_entropy: reduction must be 'mean' or "
                          f"'sum', got {reduction!r}")
-    if (stats_all.dim() != 3 or stats_all.shape[1] != state.N or stats_all.shape[2] != 4 or
+    if (stats_all.dim() != 3 or stats_all.shape[1] != state.N0 or stats_all.shape[2] != 4 or
             stats_all.dtype != torch.float32):
         raise ValueError(f"vocab_parallel_linear_cross_entropy: partials must be fp32 "
-                         f"[P, {state.N}, 4], got {stats_all.dtype} {tuple(stats_all.shape)}")
+                         f"[P, {state.N0}, 4], got {stats_all.dtype} {tuple(stats_all.shape)}")
+    if state.N != state.N0:  # the padded rows are ignored: their partials take no part
+        stats_all = torch.cat([stats_all, stats_all.new_zeros(
+            (stats_all.shape[0], state.N - state.N0, 4))], dim=1)
     stats_all = stats_all.contiguous()
     dev = state.dev
     loss = torch.empty((), dtype=torch.float32, device=dev)
@@ -364,7 +379,9 @@ def linear_ce_vocab_phase2(state: VocabShardState, stats_all: Tensor, ignore_ind
                                     ptr(loss_rows), ptr(lse), ptr(gh), ptr(gw), ptr(state.ws),
                                     state.ws_bytes, _lib.stream_handle(dev)),
               "ts_flce_vocab_bwd")
-    return loss, loss_rows, lse, gh, gw
+    n0 = state.N0
+    gh = _unpad(gh[:n0], state.H0) if gh is not None else None
+    return loss, loss_rows[:n0], lse[:n0], gh, _unpad(gw, state.H0)
 
 
 def _scale_(t: Optional[Tensor], scale: Tensor) -> None:
