@@ -17,7 +17,8 @@ from trainscale_amd.distributed import vocab_parallel_cross_entropy
 from trainscale_amd.kernels import (Fast_CrossEntropyLoss, Fast_RoPE, Fast_SwiGLU,
                                     apply_rope, apply_rope_theta, fast_cross_entropy_loss)
 from trainscale_amd.kernels.layernorm_kernels import fused_add_rms_layernorm
-from trainscale_amd.loss import ChunkedCrossEntropyLoss, fused_linear_cross_entropy
+from trainscale_amd.loss import (ChunkedCrossEntropyLoss, fused_linear_cross_entropy,
+                                 selective_log_softmax)
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
@@ -96,3 +97,24 @@ def test_vocab_parallel_empty(gpu):
     assert math.isnan(loss.item())  # loss.mean() over no rows, as the reference
     loss.backward()
     assert x.grad.shape == x.shape
+
+
+def test_vocab_parallel_linear_ce_empty(gpu):
+    from trainscale_amd.distributed import vocab_parallel_linear_cross_entropy
+    hidden = torch.randn(0, 100, device=gpu).to(BF).requires_grad_()
+    weight = torch.ones(777, 100, device=gpu).to(BF).requires_grad_()
+    labels = torch.zeros(0, dtype=torch.int64, device=gpu)
+    loss = vocab_parallel_linear_cross_entropy(hidden, weight, labels)
+    assert loss.item() == 0.0  # as fused_linear_cross_entropy over no rows
+    loss.backward()
+    assert hidden.grad.shape == (0, 100)
+    assert weight.grad.shape == weight.shape and torch.count_nonzero(weight.grad) == 0
+
+
+def test_selective_log_softmax_empty(gpu):
+    logits = torch.randn(2, 0, 1000, device=gpu).to(BF).requires_grad_()
+    ids = torch.zeros(2, 0, dtype=torch.int64, device=gpu)
+    out = selective_log_softmax(logits, ids, temperature=0.7)
+    assert out.shape == (2, 0) and out.dtype == BF
+    out.float().sum().backward()
+    assert logits.grad.shape == logits.shape

@@ -330,6 +330,10 @@ def linear_ce_vocab_phase1(hidden: Tensor, weight_shard: Tensor, labels: Tensor,
         labels = torch.cat([labels, labels.new_full((pad,), int(ignore_index))])
     hidden, weight_shard = _rows_operand(hidden), _rows_operand(weight_shard)
     N = hidden.shape[0]
+    if N == 0:  # no rows: nothing to launch; phase 2 returns the empty results
+        state = VocabShardState(hidden, weight_shard, labels, int(vocab_start), None, 0, dev,
+                                n0, h0)
+        return torch.empty((0, 4), dtype=torch.float32, device=dev), state
     lib = _lib.load()
     ws_bytes = int(lib.ts_flce_vocab_workspace_size(N, weight_shard.shape[0]))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
@@ -358,6 +362,14 @@ def linear_ce_vocab_phase2(state: VocabShardState, stats_all: Tensor, ignore_ind
             stats_all.dtype != torch.float32):
         raise ValueError(f"vocab_parallel_linear_cross_entropy: partials must be fp32 "
                          f"[P, {state.N0}, 4], got {stats_all.dtype} {tuple(stats_all.shape)}")
+    if state.N == 0:  # no rows: loss 0 (the mean over no valid rows, as the one-GPU kernel)
+        dev = state.dev
+        gh = (torch.empty((0, state.H0), dtype=torch.bfloat16, device=dev)
+              if need_grad_hidden else None)
+        gw = (torch.zeros((state.Vp, state.H0), dtype=torch.bfloat16, device=dev)
+              if need_grad_weight else None)
+        empty = torch.empty((0,), dtype=torch.float32, device=dev)
+        return torch.zeros((), dtype=torch.float32, device=dev), empty, empty.clone(), gh, gw
     if state.N != state.N0:  # the padded rows are ignored: their partials take no part
         stats_all = torch.cat([stats_all, stats_all.new_zeros(
             (stats_all.shape[0], state.N - state.N0, 4))], dim=1)
