@@ -190,3 +190,24 @@ def test_rope_patch_routes_hf_apply_and_keeps_cpu_path():
         assert torch.equal(before, after)
     finally:
         ml.apply_rotary_pos_emb = original
+
+
+def test_guard_bands_see_every_stray_write():
+    """The guard-band check of tests/test_gpu_guard.py, on the CPU: a write one element
+    before the tensor, one past it, or into the padding between its rows is seen, and
+    so is a changed NaN payload; writes inside the tensor are not."""
+    from helpers import Guarded, same
+    for dtype in (torch.bfloat16, torch.float16, torch.float32, torch.uint8):
+        vals = torch.arange(12).reshape(3, 4).to(dtype)
+        g = Guarded(3, 4, 6, dtype, torch.device("cpu"), vals)
+        assert g.intact() and torch.equal(g.t, vals)
+        g.t.zero_()
+        assert g.intact()  # inside the tensor
+        base = g.t.storage_offset()
+        for off in (-1, 4, 6 * 2 + 4, 6 * 3):  # before, row padding (two rows), past the end
+            h = Guarded(3, 4, 6, dtype, torch.device("cpu"), vals)
+            h.buf[base + off] = 1
+            assert not h.intact(), (dtype, off)
+    a = torch.tensor([float("nan")], dtype=torch.bfloat16)
+    b = a.view(torch.int16).clone().add_(1).view(torch.bfloat16)  # another NaN payload
+    assert same(a, a) and not same(a, b)
