@@ -78,3 +78,62 @@ def test_step_in_graph_matches_eager(gpu):
                  "grad"]
         for name, a, b in zip(names, got, ref):
             assert torch.equal(a, b), (rep, name)
+
+
+def _capture(gpu, step):
+    """Warm up on a side stream, then capture step() into a graph; returns (graph, outs)."""
+    side = torch.cuda.Stream(gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step()
+    return graph, outs
+
+
+@pytest.mark.parametrize("schedule", ["one_call", "two_pass", "stored_logits"])
+def test_linear_ce_in_graph_matches_eager(gpu, schedule):
+    """The fused linear CE captured and replayed: the one-call schedule in two token
+    chunks with grad_weight summed in its bf16 output (the running sum starts from the
+    first chunk's GEMM, not from memory that must be cleared), the two-pass schedule
+    with the RL transforms and per-row upstream gradients, and the stored-logits one.
+    N, H and V are off the 16-byte vector (the wrapper pads); four replays with new
+    inputs in between, each equal to eager calls bit for bit."""
+    from trainscale_amd.loss.linear_ce import (linear_ce_backward, linear_ce_forward,
+                                               linear_ce_forward_backward)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    N, H, V = 517, 100, 4099
+    h = torch.randn(N, H, device=gpu, generator=g).to(BF)
+    w = (0.1 * torch.randn(V, H, device=gpu, generator=g)).to(BF)
+    labels = torch.randint(0, V, (N,), device=gpu, generator=g)
+    labels[::9] = -100
+    dloss = torch.rand(N, device=gpu, generator=g) - 0.3
+    xf = dict(logit_softcapping=30.0, logit_scaling=0.9, temperature=0.8)
+
+    def step():
+        if schedule == "one_call":
+            loss, rows, lse, gh, gw = linear_ce_forward_backward(h, w, labels,
+                                                                 grad_weight_accum="bf16")
+            return [loss, rows, lse, gh, gw]
+        keep = schedule == "stored_logits"
+        out = linear_ce_forward(h, w, labels, reduction="none", keep_logits=keep, **xf)
+        gh, gw = linear_ce_backward(h, w, labels, out[2], dloss, reduction="none",
+                                    logits=out[3] if keep else None, **xf)
+        return [out[1], out[2], gh, gw]
+
+    graph, outs = _capture(gpu, step)
+    for rep in range(4):
+        h.copy_(torch.randn(N, H, device=gpu, generator=g).to(BF))
+        w.copy_((0.1 * torch.randn(V, H, device=gpu, generator=g)).to(BF))
+        dloss.copy_(torch.rand(N, device=gpu, generator=g) - 0.3)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [o.clone() for o in outs]
+        ref = step()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(got, ref)):
+            assert torch.equal(a, b), (schedule, rep, i)
