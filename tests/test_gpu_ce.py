@@ -477,7 +477,6 @@ def test_c3_full_schedule_b_equals_schedule_a_on_every_row(gpu):
     reference's two-pass contract (ce_fwd_vec then ce_bwd_vec, schedule A) on all
     16384 rows of C3: losses within 1e-6, gradients within 1 bf16 ulp; and every valid
     row of the one-pass gradient sums to zero within its elements' rounding."""
-    from helpers import ulp_diff
     wl = workloads.ce_workload(gpu)
     logits, labels = wl.tensors["logits"], wl.tensors["labels"]
     N, V = logits.shape

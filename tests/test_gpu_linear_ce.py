@@ -15,7 +15,6 @@ Bars:
   star's 2e-2 absolute holds as well (one bf16 ulp where |g| >= 4 makes that larger).
 With logits exact in bf16, the loss pins the logits GEMM's tiling and index math.
 """
-import math
 from types import SimpleNamespace
 
 import numpy as np

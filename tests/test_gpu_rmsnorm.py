@@ -12,7 +12,7 @@ import oracle
 from helpers import assert_ulp, golden, max_ulp, round_to
 from trainscale_amd import ops, workloads
 from trainscale_amd.kernels import (Fast_RMS_LayerNorm, RMSLayerNormFunction, RMSNorm,
-                                    fast_rms_layernorm, rms_layernorm)
+                                    rms_layernorm)
 
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16

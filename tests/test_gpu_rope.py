@@ -14,12 +14,11 @@ Bars:
   the products nearly cancel, that is many ulps of the small result.
 * The golden vectors (float64 rotations) within 1 ulp in both modes.
 """
-import numpy as np
 import pytest
 import torch
 
 import oracle
-from helpers import assert_ulp, golden, max_ulp, round_to
+from helpers import assert_ulp, golden, round_to
 from trainscale_amd import workloads
 from trainscale_amd.kernels import (Fast_RoPE, RotaryEmbedding, apply_rope, apply_rope_qk,
                                     apply_rope_theta, fast_rope_embedding,

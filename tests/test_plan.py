@@ -37,7 +37,6 @@ indices. A small C++ driver compiled with g++ sweeps many shapes and checks:
 It also checks the exported size query of the built library against the
 driver's figure for the same shapes.
 """
-import ctypes
 import shutil
 import subprocess
 from pathlib import Path

@@ -14,7 +14,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from ._lib import I32, I64, F32, SZ, check, ptr
+from ._lib import check, ptr
 
 # round modes of ts_rmsnorm_fwd
 ROUND_ONCE = 0

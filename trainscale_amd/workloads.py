@@ -7,7 +7,6 @@ traffic of one forward+backward pass that roofline fractions are computed from.
 """
 from __future__ import annotations
 
-import math
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
