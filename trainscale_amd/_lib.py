@@ -6,6 +6,7 @@ raises. Build the library with ``python -m trainscale_amd.build``.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import re
 import threading
@@ -147,9 +148,24 @@ def check(status: int, what: str) -> None:
         raise KernelError(what, status, last_error())
 
 
+# torch's current-stream query without building a Stream object (the form torch's
+# own kernel launchers use); the public API where a build lacks it
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> ctypes.c_void_p:
     """The HIP stream torch is currently using on `device`."""
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(device.index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def on_device(device: torch.device):
+    """A context under which `device` is the current device, for a launch on its stream
+    (a no-op context when it already is, the common case)."""
+    if device.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)
 
 
 def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:

@@ -145,12 +145,12 @@ def linear_ce_forward(hidden: Tensor, weight: Tensor, labels: Tensor, ignore_ind
             int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
             float(logit_scaling), float(temperature), ptr(loss), ptr(rows), ptr(lse))
     if not keep_logits:
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             check(lib.ts_flce_forward(*args, ptr(ws), ws_bytes, _lib.stream_handle(dev)),
                   "ts_flce_forward")
         return loss, rows, lse
     logits = torch.empty((N, _logits_ld(V)), dtype=torch.bfloat16, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_flce_forward_keep(*args, ptr(logits), ptr(ws), ws_bytes,
                                        _lib.stream_handle(dev)), "ts_flce_forward_keep")
     return loss, rows, lse, logits[:, :V]
@@ -191,7 +191,7 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
                              f"returns them)")
         ws_bytes = int(lib.ts_flce_backward_kept_workspace_size(N))
         ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             check(lib.ts_flce_backward_kept(
                 ptr(hidden), _ld(hidden), ptr(weight), _ld(weight), ptr(labels), N, H, V,
                 int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
@@ -202,7 +202,7 @@ def linear_ce_backward(hidden: Tensor, weight: Tensor, labels: Tensor, lse: Tens
     chunk = int(vocab_chunk) if vocab_chunk else 0
     ws_bytes = int(lib.ts_flce_backward_workspace_size(N, H, V, chunk))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_flce_backward(
             ptr(hidden), _ld(hidden), ptr(weight), _ld(weight), ptr(labels), N, H, V,
             int(ignore_index), _REDUCTIONS_2P[reduction], float(logit_softcapping),
@@ -275,7 +275,7 @@ def linear_ce_forward_backward(hidden: Tensor, weight: Tensor, labels: Tensor,
     ws_bytes = int(lib.ts_flce_workspace_size(N, H, V, chunk,
                                               (TS_FLCE_GRADS if grads else 0) | flags))
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_flce_fwd_bwd(
             ptr(hidden), ldh, ptr(weight), ldw, ptr(labels), N, H, V, int(ignore_index),
             _REDUCTIONS[reduction], ptr(loss), ptr(loss_rows), ptr(lse), ptr(gh), ptr(gw),
@@ -340,7 +340,7 @@ def linear_ce_vocab_phase1(hidden: Tensor, weight_shard: Tensor, labels: Tensor,
     state = VocabShardState(hidden, weight_shard, labels, int(vocab_start), ws, ws_bytes, dev,
                             n0, h0)
     stats = torch.empty((N, 4), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_flce_vocab_fwd(ptr(hidden), state.ldh, ptr(weight_shard), state.ldw,
                                     ptr(labels), N, state.H, state.Vp, state.vocab_start,
                                     ptr(stats), ptr(ws), ws_bytes, _lib.stream_handle(dev)),
@@ -383,7 +383,7 @@ def linear_ce_vocab_phase2(state: VocabShardState, stats_all: Tensor, ignore_ind
     gw = (torch.empty((state.Vp, state.H), dtype=torch.bfloat16, device=dev)
           if need_grad_weight else None)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_flce_vocab_bwd(ptr(state.hidden), state.ldh, ptr(state.weight), state.ldw,
                                     ptr(state.labels), state.N, state.H, state.Vp,
                                     state.vocab_start, ptr(stats_all), stats_all.shape[0],

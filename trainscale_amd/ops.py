@@ -57,7 +57,7 @@ def rmsnorm_forward(x2d: Tensor, ldx: int, weight: Optional[Tensor], eps: float,
             raise ValueError(f"rmsnorm: weight shape {tuple(weight.shape)} != ({cols},)")
         weight = weight.contiguous()
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_rmsnorm_fwd(
             ptr(x2d), ldx, _lib.dtype_code(x2d, "rmsnorm"),
             ptr(weight), _lib.dtype_code(weight, "rmsnorm weight") if weight is not None else 0,
@@ -87,7 +87,7 @@ def add_rmsnorm_forward(x2d: Tensor, ldx: int, r2d: Tensor, ldr: int, weight: Op
             raise ValueError(f"add_rmsnorm: weight shape {tuple(weight.shape)} != ({cols},)")
         weight = weight.contiguous()
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_add_rmsnorm_fwd(
             ptr(x2d), ldx, ptr(r2d), ldr, _lib.dtype_code(x2d, "add_rmsnorm"),
             ptr(weight), _lib.dtype_code(weight, "add_rmsnorm weight") if weight is not None else 0,
@@ -116,7 +116,7 @@ def rmsnorm_backward(dy2d: Tensor, lddy: int, x2d: Tensor, ldx: int, weight: Opt
         ws_bytes = int(lib.ts_rmsnorm_bwd_workspace_size(rows, cols))
         ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     w_code = _lib.dtype_code(weight, "rmsnorm weight") if weight is not None else 0
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_rmsnorm_bwd(
             ptr(dy2d), lddy, ptr(x2d), ldx, _lib.dtype_code(x2d, "rmsnorm"),
             ptr(weight), w_code, ptr(rstd.contiguous()), ptr(dx), cols, ptr(dw),
@@ -220,7 +220,7 @@ def rope_apply(q_in: Optional[Tensor], q_out: Optional[Tensor],
         return (_norm_stride(t, 0), _norm_stride(t, 1), _norm_stride(t, 2))
 
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_rope_apply(
             ptr(q_in), ptr(q_out), *strides(q_in), *strides(q_out), Hq,
             ptr(k_in), ptr(k_out), *strides(k_in), *strides(k_out), Hk,
@@ -259,7 +259,7 @@ def ce_forward(logits2d: Tensor, ld: int, labels: Tensor, ignore_index: int = -1
     if n == 0:
         return loss, lse
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_ce_fwd(ptr(logits2d), ld, _lib.dtype_code(logits2d, "cross_entropy"),
                             ptr(labels), n, v, int(ignore_index), float(logit_scale),
                             float(softcap), float(label_smoothing), ptr(loss), ptr(lse),
@@ -292,7 +292,7 @@ def ce_backward(logits2d: Tensor, ld: int, labels: Tensor, lse: Tensor, dloss: T
     if n == 0:
         return grad
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_ce_bwd(ptr(logits2d), ld, _lib.dtype_code(logits2d, "cross_entropy"),
                             ptr(labels), ptr(lse.contiguous()), ptr(dloss), dstride,
                             float(dloss_scale), ptr(grad), ld_grad,
@@ -334,7 +334,7 @@ def ce_forward_backward(logits2d: Tensor, ld: int, labels: Tensor, dloss: Tensor
     if n == 0:
         return loss, lse, grad
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_ce_fwd_bwd(ptr(logits2d), ld, _lib.dtype_code(logits2d, "cross_entropy"),
                                 ptr(labels), n, v, int(ignore_index), float(logit_scale),
                                 float(softcap), float(label_smoothing), ptr(dloss), dstride,
@@ -359,7 +359,7 @@ def ce_vocab_shard_stats(logits2d: Tensor, ld: int, targets: Tensor, vocab_start
     if n == 0:
         return stats
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_ce_vocab_shard_stats(ptr(logits2d), ld,
                                           _lib.dtype_code(logits2d, "vocab_parallel_cross_entropy"),
                                           ptr(targets), n, vp, int(vocab_start), ptr(stats),
@@ -381,7 +381,7 @@ def ce_vocab_merge(stats_all: Tensor, self_index: int, vp: int,
     if n == 0:
         return lse, loss
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_ce_vocab_merge(ptr(stats_all), p, int(self_index), n, int(vp),
                                     float(label_smoothing), ptr(lse), ptr(loss),
                                     _lib.stream_handle(dev)), "ts_ce_vocab_merge")
@@ -402,7 +402,7 @@ def ce_vocab_shard_backward(logits2d: Tensor, ld: int, targets: Tensor, lse: Ten
         return grad
     go = grad_output.detach().reshape(-1)[:1].float().contiguous()
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_ce_vocab_shard_bwd(ptr(logits2d), ld,
                                         _lib.dtype_code(logits2d, "vocab_parallel_cross_entropy"),
                                         ptr(targets), ptr(lse.contiguous()), ptr(go),
@@ -423,7 +423,7 @@ def scale_(t: Tensor, scale: Tensor) -> Tensor:
         raise ValueError("scale_: tensor must be contiguous")
     scale = scale.detach().to(torch.float32).reshape(1).contiguous()
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_scale_inplace(ptr(t), t.numel(), _lib.dtype_code(t, "scale_"), ptr(scale),
                                    _lib.stream_handle(dev)), "ts_scale_inplace")
     return t
@@ -442,7 +442,7 @@ def rescale_(t: Tensor, now: Tensor, used: Tensor, hint_out: Optional[Tensor] = 
                                  or hint_out.device != t.device):
         raise ValueError("rescale_: hint_out must be a one-element fp32 tensor on the device")
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_rescale_inplace(ptr(t), t.numel(), _lib.dtype_code(t, "rescale_"),
                                      ptr(now), ptr(used), ptr(hint_out),
                                      _lib.stream_handle(dev)), "ts_rescale_inplace")
@@ -464,7 +464,7 @@ def swiglu_forward(gate: Tensor, up: Tensor) -> Tensor:
     gate, up = gate.contiguous(), up.contiguous()
     out = torch.empty_like(gate)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_swiglu_fwd(ptr(gate), ptr(up), ptr(out), gate.numel(),
                                 _lib.dtype_code(gate, "swiglu"), _lib.stream_handle(dev)),
               "ts_swiglu_fwd")
@@ -480,7 +480,7 @@ def swiglu_backward(dout: Tensor, gate: Tensor, up: Tensor) -> Tuple[Tensor, Ten
         raise ValueError(f"swiglu: dout {tuple(dout.shape)} != gate {tuple(gate.shape)}")
     dgate, dup = torch.empty_like(gate), torch.empty_like(up)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         check(lib.ts_swiglu_bwd(ptr(dout), ptr(gate), ptr(up), ptr(dgate), ptr(dup),
                                 gate.numel(), _lib.dtype_code(gate, "swiglu"),
                                 _lib.stream_handle(dev)), "ts_swiglu_bwd")
