@@ -193,3 +193,64 @@ def test_linear_ce_rl_sweep(gpu, N, H, V, cap, scale, temp, chunk):
     dloss = (torch.rand(N, generator=g) - 0.3).to(gpu)
     check_two_pass(h, w, labels, reduction="none", dloss=dloss, chunk=chunk,
                    logit_softcapping=cap, logit_scaling=scale, temperature=temp)
+
+
+# ---------------------------------------------------------------------------
+# The smallest shapes each op takes
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N", [1, 5])
+def test_ce_one_class(gpu, N):
+    """V = 1: lse is the logit itself, every loss 0 and every gradient 0 (both schedules)."""
+    logits = torch.randn(N, 1, device=gpu).to(BF)
+    labels = torch.zeros(N, dtype=torch.int64, device=gpu)
+    ref, ref_lse = oracle.ce_fwd(logits.cpu(), labels.cpu())
+    dl = torch.ones(1, device=gpu)
+    loss, lse, grad = ops.ce_forward_backward(logits, 1, labels, dl)
+    l2, lse2 = ops.ce_forward(logits, 1, labels)
+    g2 = torch.empty_like(logits)
+    ops.ce_backward(logits, 1, labels, lse2, dl, g2, 1)
+    for lo, ls, g in ((loss, lse, grad), (l2, lse2, g2)):
+        assert torch.equal(lo.cpu(), ref) and torch.count_nonzero(lo) == 0
+        assert torch.equal(ls.cpu(), ref_lse)
+        assert torch.count_nonzero(g) == 0
+
+
+def test_linear_ce_one_class_and_one_row(gpu):
+    """V = 1 (every loss exactly 0; the gradients 0 up to the rounding of exp(z - lse), which
+    the element-wise bounds hold) and N = 1, H = 1, through the one-call and two-pass
+    schedules."""
+    from trainscale_amd.loss.linear_ce import linear_ce_forward, linear_ce_forward_backward
+    g = torch.Generator().manual_seed(9)
+    h = torch.randn(7, 16, generator=g).to(BF).to(gpu)
+    w = torch.randn(1, 16, generator=g).to(BF).to(gpu)
+    labels = torch.zeros(7, dtype=torch.int64, device=gpu)
+    loss, rows, _, gh, gw = linear_ce_forward_backward(h, w, labels)
+    assert loss.item() == 0.0 and torch.count_nonzero(rows) == 0
+    assert float(gh.float().abs().max()) < 1e-4 and float(gw.float().abs().max()) < 1e-4
+    lce_check(h, w, labels)
+    loss2, _, _ = linear_ce_forward(h, w, labels)
+    assert loss2.item() == 0.0
+    check_two_pass(h, w, labels)
+    # one token, a one-element hidden state
+    h1 = torch.randn(1, 1, generator=g).to(BF).to(gpu)
+    w1 = torch.randn(300, 1, generator=g).to(BF).to(gpu)
+    lab1 = torch.tensor([17], device=gpu)
+    lce_check(h1, w1, lab1)
+    check_two_pass(h1, w1, lab1)
+
+
+def test_rmsnorm_one_column_and_rope_one_pair(gpu):
+    """RMSNorm over rows of one element (y = x / |x| * w up to eps) and RoPE with a
+    head of one pair (D = 2), table and in-register."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(37, 1, generator=g).to(BF).to(gpu)
+    w = (1 + 0.05 * torch.randn(1, generator=g)).to(BF).to(gpu)
+    dy = torch.randn(37, 1, generator=g).to(BF).to(gpu)
+    rms_check(x, w, dy, 1e-6)
+    q = torch.randn(2, 5, 3, 2, generator=g).to(BF).to(gpu)
+    cos, sin = oracle.rope_tables(2, 5, 10000.0)
+    pos = oracle.rope_positions(2, 5)
+    assert_rope(apply_rope(q, cos.to(gpu), sin.to(gpu), inplace=False), q, cos, sin, pos,
+                exact=True)
+    assert_rope(apply_rope_theta(q, 10000.0, inplace=False), q, cos, sin, pos)
