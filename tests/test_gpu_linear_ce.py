@@ -15,6 +15,7 @@ Bars:
   star's 2e-2 absolute holds as well (one bf16 ulp where |g| >= 4 makes that larger).
 With logits exact in bf16, the loss pins the logits GEMM's tiling and index math.
 """
+import math
 from types import SimpleNamespace
 
 import numpy as np
@@ -761,3 +762,30 @@ def test_two_pass_strided_rows(gpu):
     _, rows_c, lse_c, gh_c, gw_c = check_two_pass(h.contiguous(), w.contiguous(), labels, "sum",
                                                   chunk=256)
     assert torch.equal(rows, rows_c) and torch.equal(gh, gh_c) and torch.equal(gw, gw_c)
+
+
+@pytest.mark.parametrize("schedule", ["one_call", "two_pass", "stored_logits"])
+def test_out_of_range_labels_give_nan_rows(gpu, schedule):
+    """A label outside [0, V) that is not ignore_index (the reference's F.cross_entropy
+    rejects it) gives that row a NaN loss, as the CE kernels do, and leaves the other
+    rows' losses as they are; the reduced loss is then NaN."""
+    g = torch.Generator().manual_seed(12)
+    N, H, V = 64, 32, 1000
+    h = torch.randn(N, H, generator=g).to(BF).to(gpu)
+    w = (0.1 * torch.randn(V, H, generator=g)).to(BF).to(gpu)
+    labels = torch.randint(0, V, (N,), generator=g).to(gpu)
+    labels[3] = -100
+    bad = labels.clone()
+    bad[5], bad[9] = V, -7
+    if schedule == "one_call":
+        run = lambda lab: linear_ce_forward_backward(h, w, lab)[:2]
+    else:
+        run = lambda lab: linear_ce_forward(h, w, lab, reduction="mean",
+                                            keep_logits=schedule == "stored_logits")[:2]
+    loss_ok, rows_ok = run(labels)
+    loss_bad, rows_bad = run(bad)
+    assert math.isfinite(loss_ok.item()) and math.isnan(loss_bad.item())
+    assert torch.isnan(rows_bad[5]) and torch.isnan(rows_bad[9])
+    keep = torch.ones(N, dtype=torch.bool, device=gpu)
+    keep[5] = keep[9] = False
+    assert torch.equal(rows_bad[keep], rows_ok[keep])
